@@ -1,0 +1,175 @@
+"""ctypes binding of libpa_fp8.so (the C ABI declared in include/pa_fp8.h).
+
+The library is required: importing this module when it has not been built
+raises, and there is no CPU or PyTorch fallback for any kernel.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("PA_FP8_LIB", str(_HERE / "libpa_fp8.so")))
+
+PA_FP8_ABI_VERSION = 1
+PA_FP8_BF16, PA_FP8_F16, PA_FP8_F32 = 0, 1, 2
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+
+
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("exp_sums", _vp),
+        ("max_logits", _vp),
+        ("tmp_out", _vp),
+        ("query", _vp),
+        ("key_cache", _vp),
+        ("value_cache", _vp),
+        ("block_tables", _vp),
+        ("context_lengths", _vp),
+        ("key_scale", _vp),
+        ("value_scale", _vp),
+        ("stride_q_seq", _i64),
+        ("stride_q_head", _i64),
+        ("stride_k_block", _i64),
+        ("stride_k_head", _i64),
+        ("stride_v_block", _i64),
+        ("stride_v_head", _i64),
+        ("stride_es_seq", _i64),
+        ("stride_es_head", _i64),
+        ("stride_es_part", _i64),
+        ("stride_to_seq", _i64),
+        ("stride_to_head", _i64),
+        ("stride_to_part", _i64),
+        ("stride_to_group", _i64),
+        ("stride_bt_seq", _i64),
+        ("stride_ks_block", _i64),
+        ("stride_ks_head", _i64),
+        ("batch_size", _i32),
+        ("num_kv_heads", _i32),
+        ("query_group_size", _i32),
+        ("query_length", _i32),
+        ("head_dim", _i32),
+        ("block_size", _i32),
+        ("num_blocks", _i32),
+        ("max_blocks_per_seq", _i32),
+        ("max_context_partition_num", _i32),
+        ("sliding_window", _i32),
+        ("per_token_kv", _i32),
+        ("query_dtype", _i32),
+        ("softmax_scale", _f32),
+        ("reserved", _i32),
+    ]
+
+
+class ReduceArgs(ctypes.Structure):
+    _fields_ = [
+        ("output", _vp),
+        ("exp_sums", _vp),
+        ("max_logits", _vp),
+        ("tmp_out", _vp),
+        ("stride_o_seq", _i64),
+        ("stride_o_len", _i64),
+        ("stride_o_head", _i64),
+        ("stride_o_group", _i64),
+        ("stride_es_seq", _i64),
+        ("stride_es_head", _i64),
+        ("stride_es_part", _i64),
+        ("stride_to_seq", _i64),
+        ("stride_to_head", _i64),
+        ("stride_to_part", _i64),
+        ("stride_to_group", _i64),
+        ("batch_size", _i32),
+        ("num_kv_heads", _i32),
+        ("query_group_size", _i32),
+        ("query_length", _i32),
+        ("head_dim", _i32),
+        ("max_context_partition_num", _i32),
+        ("out_dtype", _i32),
+        ("reserved", _i32),
+    ]
+
+
+class MetadataArgs(ctypes.Structure):
+    _fields_ = [
+        ("seqlens_qo_indptr", _vp),
+        ("context_lens", _vp),
+        ("work_indptr", _vp),
+        ("work_info", _vp),
+        ("reduce_indptr", _vp),
+        ("reduce_final_map", _vp),
+        ("reduce_partial_map", _vp),
+        ("num_batches", _i32),
+        ("gqa", _i32),
+        ("num_heads_k", _i32),
+        ("num_cu", _i32),
+        ("kv_granularity", _i32),
+        ("query_length", _i32),
+        ("max_work", _i32),
+        ("max_split_tiles", _i32),
+    ]
+
+
+EXPORTED_SYMBOLS = (
+    "pa_fp8_decode_partitions",
+    "pa_fp8_lse_reduce",
+    "pa_fp8_metadata_v1",
+    "pa_fp8_status_string",
+    "pa_fp8_abi_version",
+)
+
+
+class PaFp8Error(RuntimeError):
+    """A libpa_fp8 entry point returned a non-zero status."""
+
+    def __init__(self, func: str, status: int, text: str):
+        super().__init__(f"{func} failed with status {status}: {text}")
+        self.status = status
+
+
+def _load() -> ctypes.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"libpa_fp8.so not found at {LIB_PATH}; build it with `python -m flydsl_amd.build` "
+            "(there is no fallback implementation)"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    lib.pa_fp8_decode_partitions.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
+    lib.pa_fp8_decode_partitions.restype = ctypes.c_int
+    lib.pa_fp8_lse_reduce.argtypes = [ctypes.POINTER(ReduceArgs), _vp]
+    lib.pa_fp8_lse_reduce.restype = ctypes.c_int
+    lib.pa_fp8_metadata_v1.argtypes = [ctypes.POINTER(MetadataArgs), _vp]
+    lib.pa_fp8_metadata_v1.restype = ctypes.c_int
+    lib.pa_fp8_status_string.argtypes = [ctypes.c_int]
+    lib.pa_fp8_status_string.restype = ctypes.c_char_p
+    lib.pa_fp8_abi_version.argtypes = []
+    lib.pa_fp8_abi_version.restype = ctypes.c_int
+    ver = lib.pa_fp8_abi_version()
+    if ver != PA_FP8_ABI_VERSION:
+        raise ImportError(f"libpa_fp8.so ABI version {ver} != expected {PA_FP8_ABI_VERSION}; rebuild the library")
+    return lib
+
+
+LIB = _load()
+
+
+def check(func: str, status: int) -> None:
+    if status != 0:
+        raise PaFp8Error(func, status, LIB.pa_fp8_status_string(status).decode())
+
+
+def decode_partitions(args: DecodeArgs, stream: int) -> None:
+    check("pa_fp8_decode_partitions", LIB.pa_fp8_decode_partitions(ctypes.byref(args), _vp(stream)))
+
+
+def lse_reduce(args: ReduceArgs, stream: int) -> None:
+    check("pa_fp8_lse_reduce", LIB.pa_fp8_lse_reduce(ctypes.byref(args), _vp(stream)))
+
+
+def metadata_v1(args: MetadataArgs, stream: int) -> None:
+    check("pa_fp8_metadata_v1", LIB.pa_fp8_metadata_v1(ctypes.byref(args), _vp(stream)))

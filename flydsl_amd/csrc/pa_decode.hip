@@ -1,0 +1,602 @@
+// gfx950 split-context FP8-KV paged-attention decode and its log-sum-exp reduce.
+//
+// Work decomposition (grid = (batch, kv_heads, partition slots), one workgroup per
+// slot, NW waves per workgroup):
+//   * slot z of sequence b covers the 256-token partitions [z*pps, min((z+1)*pps, T))
+//     with T = ceil(ctx/256), pps = ceil(T/P) (kernels/pa_decode_fp8.py:2311-2320);
+//     with a sliding window the partitions start at tile max(ctx-ql-sw,0)/256
+//     (kernels/pa_decode_swa.py:1359-1368) and the first window tile is trimmed
+//     to the 16-token group holding the window start.
+//   * the slot's tokens are cut into 64-token steps (4 groups of 16 tokens); wave w
+//     takes steps w, w+NW, ... and runs its own online softmax; the waves merge
+//     through LDS at the end and write one partial (exp_sum, max_logit, bf16 out).
+//
+// Per step a lane issues eight 16-byte K loads and eight 16-byte V loads (the
+// 16 KiB a wave consumes per step); the next step is prefetched while the current
+// one is computed.  fp8 e4m3fn is converted exactly to bf16 in registers
+// (v_cvt_scalef32_pk_bf16_fp8) and both products run on v_mfma_f32_16x16x32_bf16:
+//   QK : C[token][qrow] = sum_d K[token][d] Q[qrow][d]   (4 tiles x 4 k-steps)
+//   PV : C[dim][qrow]   = sum_t V[t][dim] P[qrow][t]     (8 dim tiles x 2 k-steps)
+// QK tile jt, row 4*kg+i holds token 16*kg + 4*jt + i of the step, so the QK
+// output lane (qrow, kg) owns exactly the 16 tokens of group kg -- the tokens its
+// PV operand needs (one 16-byte trans_v row of group kg) -- and P goes from the QK
+// accumulators to the PV MFMA without any cross-lane movement.
+#include "pa_common.h"
+#include "pa_fp8.h"
+
+using namespace pa;
+
+namespace {
+
+struct DecodeParams {
+    float *exp_sums;
+    float *max_logits;
+    uint16_t *tmp_out;
+    const uint16_t *query;
+    const uint8_t *kc;
+    const uint8_t *vc;
+    const int32_t *bt;
+    const int32_t *ctx;
+    const float *ks;
+    const float *vs;
+    int64_t s_q_seq, s_q_head;
+    int64_t s_k_block, s_k_head;
+    int64_t s_v_block, s_v_head;
+    int64_t s_es_seq, s_es_head, s_es_part;
+    int64_t s_to_seq, s_to_head, s_to_part, s_to_group;
+    int64_t s_bt_seq;
+    int64_t s_ks_block, s_ks_head;
+    int32_t g, ql, eqgs, bs_log2;
+    int32_t num_blocks, max_blocks, max_parts, sw;
+    int32_t q_f16;
+    float qk_scale;  // softmax_scale * log2(e)
+};
+
+struct ReduceParams {
+    void *out;
+    const float *es;
+    const float *ml;
+    const uint16_t *to;
+    int64_t s_o_seq, s_o_len, s_o_head, s_o_group;
+    int64_t s_es_seq, s_es_head, s_es_part;
+    int64_t s_to_seq, s_to_head, s_to_part, s_to_group;
+    int32_t g, max_parts;
+};
+
+__device__ __forceinline__ bf16x8 load_q8(const uint16_t *p, bool f16) {
+    uint4 raw = *reinterpret_cast<const uint4 *>(p);
+    if (!f16) return __builtin_bit_cast(bf16x8, raw);
+    f16x8 hv = __builtin_bit_cast(f16x8, raw);
+    bf16x8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (__bf16)(float)hv[i];
+    return r;
+}
+
+__device__ __forceinline__ bf16x8 pack_bf16x8(f32x4 a, f32x4 b) {
+    bf16x4 x = __builtin_convertvector(a, bf16x4);
+    bf16x4 y = __builtin_convertvector(b, bf16x4);
+    return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+template <bool PER_TOKEN>
+struct StepData {
+    uint4 k[4][2];  // [tile][chunk] 16 fp8 each
+    uint4 v[8];     // [dim tile]    16 fp8 each (16 tokens of one head dim)
+    f32x4 ks[4];    // per-token K scales of the lane's 16 tokens
+    f32x4 vs[4];
+};
+
+template <int MTP, bool PER_TOKEN, int NW>
+__global__ __launch_bounds__(NW * 64) void pa_decode_partition_kernel(const DecodeParams p) {
+    constexpr int D = kHeadDim;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15;
+    const int kg = lane >> 4;
+    const int b = blockIdx.x;
+    const int h = blockIdx.y;
+    const int z = blockIdx.z;
+    const int bs = 1 << p.bs_log2;
+
+    // ---- slot -> token range (integer planner, bit-exact with the oracle)
+    int64_t ctx64 = p.ctx[b];
+    const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
+    ctx64 = ctx64 < 0 ? 0 : (ctx64 > cap ? cap : ctx64);
+    const int ctx = (int)ctx64;
+    const int T = (ctx + kPartition - 1) / kPartition;
+    int seq_start = 0;
+    if (p.sw > 0) seq_start = max(ctx - p.ql - p.sw, 0);
+    const int first_tile = seq_start / kPartition;
+    const int vis = T - first_tile;
+    const int pps = vis > 0 ? (vis + p.max_parts - 1) / p.max_parts : 0;
+    const int plo = first_tile + z * pps;
+    const int phi = min(plo + pps, T);
+    int tok_lo = plo * kPartition;
+    const int tok_hi = min(phi * kPartition, ctx);
+    if (tok_lo < seq_start) tok_lo = seq_start & ~(kGroup - 1);
+
+    float *es = p.exp_sums + b * p.s_es_seq + h * p.s_es_head + z * p.s_es_part;
+    float *ml = p.max_logits + b * p.s_es_seq + h * p.s_es_head + z * p.s_es_part;
+    uint16_t *to = p.tmp_out + b * p.s_to_seq + h * p.s_to_head + z * p.s_to_part;
+
+    if (tok_lo >= tok_hi) {  // empty slot (kernels/pa_decode_fp8.py:2591-2598)
+        for (int r = tid; r < p.eqgs; r += NW * 64) {
+            es[r] = 0.0f;
+            ml[r] = -INFINITY;
+        }
+        for (int i = tid; i < p.eqgs * (D / 8); i += NW * 64) {
+            const int r = i / (D / 8), c = i % (D / 8);
+            *reinterpret_cast<uint4 *>(to + r * p.s_to_group + c * 8) = make_uint4(0, 0, 0, 0);
+        }
+        return;
+    }
+
+    // ---- query operands (B of the QK MFMA): lane (qrow l16, kg) holds dims 32kg..32kg+31
+    bf16x8 qop[MTP][4];
+    int lo_n[MTP], hi_n[MTP];
+#pragma unroll
+    for (int mg = 0; mg < MTP; ++mg) {
+        const int n = mg * 16 + l16;
+        if (n < p.eqgs) {
+            const int qi = n / p.g;
+            const int gi = n - qi * p.g;
+            const uint16_t *qrow =
+                p.query + (int64_t)(b * p.ql + qi) * p.s_q_seq + (int64_t)(h * p.g + gi) * p.s_q_head + 32 * kg;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) qop[mg][s] = load_q8(qrow + 8 * s, p.q_f16 != 0);
+            hi_n[mg] = min(tok_hi, ctx + 1 - p.ql + qi);
+            lo_n[mg] = p.sw > 0 ? max(tok_lo, ctx - p.ql - p.sw + qi) : tok_lo;
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) qop[mg][s] = bf16x8{};
+            hi_n[mg] = 0;
+            lo_n[mg] = 0;
+        }
+    }
+    const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
+    const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
+
+    // ---- per-lane running state
+    float m_run[MTP], l_run[MTP];
+    f32x4 o[MTP][8];
+#pragma unroll
+    for (int mg = 0; mg < MTP; ++mg) {
+        m_run[mg] = -INFINITY;
+        l_run[mg] = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) o[mg][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const int ngroups = (tok_hi - tok_lo + kGroup - 1) / kGroup;
+    const int nsteps = (ngroups + 3) / 4;
+    const int last_group = tok_lo + (ngroups - 1) * kGroup;
+    const int32_t *bt_row = p.bt + (int64_t)b * p.s_bt_seq;
+    const uint8_t *kc_h = p.kc + (int64_t)h * p.s_k_head;
+    const uint8_t *vc_h = p.vc + (int64_t)h * p.s_v_head;
+    const int kchunk = bs * 16;  // bytes between 16-dim chunks of one (block, head)
+    const int k_lane_off = (l16 & 3) * 16 + (2 * kg) * kchunk;
+    const int v_lane_off = l16 * 16;
+
+    auto group_loc = [&](int gstart, int &phys, int &sub) {
+        const int gs = min(gstart, last_group);
+        const int e = bt_row[gs >> p.bs_log2];
+        phys = min(max(e, 0), p.num_blocks - 1);
+        sub = (gs & (bs - 1)) >> 4;
+    };
+
+    auto load_step = [&](int step, StepData<PER_TOKEN> &sd) {
+        const int t0 = tok_lo + step * kStep;
+        int pk, sk;
+        group_loc(t0 + 16 * (l16 >> 2), pk, sk);
+        const uint8_t *kb = kc_h + (int64_t)pk * p.s_k_block + sk * 256 + k_lane_off;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            sd.k[jt][0] = ld16(kb + jt * 64);
+            sd.k[jt][1] = ld16(kb + kchunk + jt * 64);
+        }
+        int pv, sv;
+        group_loc(t0 + 16 * kg, pv, sv);
+        const uint8_t *vb = vc_h + (int64_t)pv * p.s_v_block + sv * (D * 16) + v_lane_off;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) sd.v[m] = ld16(vb + m * 256);
+        if constexpr (PER_TOKEN) {
+            const int64_t so = (int64_t)pv * p.s_ks_block + (int64_t)h * p.s_ks_head + sv * 16;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                sd.ks[q4] = *reinterpret_cast<const f32x4 *>(p.ks + so + 4 * q4);
+                sd.vs[q4] = *reinterpret_cast<const f32x4 *>(p.vs + so + 4 * q4);
+            }
+        }
+    };
+
+    auto compute_step = [&](int step, const StepData<PER_TOKEN> &sd) {
+        const int trow = tok_lo + step * kStep + 16 * kg;  // token of (tile jt, i) = trow + 4jt + i
+        f32x4 sc[MTP][4];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            const bf16x8 a0 = fp8x8_to_bf16x8(sd.k[jt][0].x, sd.k[jt][0].y);
+            const bf16x8 a1 = fp8x8_to_bf16x8(sd.k[jt][0].z, sd.k[jt][0].w);
+            const bf16x8 a2 = fp8x8_to_bf16x8(sd.k[jt][1].x, sd.k[jt][1].y);
+            const bf16x8 a3 = fp8x8_to_bf16x8(sd.k[jt][1].z, sd.k[jt][1].w);
+#pragma unroll
+            for (int mg = 0; mg < MTP; ++mg) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                acc = mfma_bf16(a0, qop[mg][0], acc);
+                acc = mfma_bf16(a1, qop[mg][1], acc);
+                acc = mfma_bf16(a2, qop[mg][2], acc);
+                acc = mfma_bf16(a3, qop[mg][3], acc);
+                sc[mg][jt] = acc;
+            }
+        }
+        bf16x8 pop[MTP][2];
+#pragma unroll
+        for (int mg = 0; mg < MTP; ++mg) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = trow + 4 * jt + i;
+                    float s = sc[mg][jt][i] * (PER_TOKEN ? k_fac * sd.ks[jt][i] : k_fac);
+                    s = (t >= lo_n[mg] && t < hi_n[mg]) ? s : -INFINITY;
+                    sc[mg][jt][i] = s;
+                    mx = fmaxf(mx, s);
+                }
+            }
+            mx = fmaxf(mx, shfl_xor_f(mx, 16));
+            mx = fmaxf(mx, shfl_xor_f(mx, 32));
+            const float m_new = fmaxf(m_run[mg], mx);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float alpha = fast_exp2(m_run[mg] - m_use);
+            m_run[mg] = m_new;
+            float psum = 0.0f;
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float pv = fast_exp2(sc[mg][jt][i] - m_use);
+                    psum += pv;
+                    if constexpr (PER_TOKEN) pv *= sd.vs[jt][i];
+                    sc[mg][jt][i] = pv;
+                }
+            }
+            l_run[mg] = l_run[mg] * alpha + psum;
+#pragma unroll
+            for (int m = 0; m < 8; ++m) o[mg][m] *= alpha;
+            pop[mg][0] = pack_bf16x8(sc[mg][0], sc[mg][1]);
+            pop[mg][1] = pack_bf16x8(sc[mg][2], sc[mg][3]);
+        }
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const bf16x8 v0 = fp8x8_to_bf16x8(sd.v[m].x, sd.v[m].y);
+            const bf16x8 v1 = fp8x8_to_bf16x8(sd.v[m].z, sd.v[m].w);
+#pragma unroll
+            for (int mg = 0; mg < MTP; ++mg) {
+                o[mg][m] = mfma_bf16(v0, pop[mg][0], o[mg][m]);
+                o[mg][m] = mfma_bf16(v1, pop[mg][1], o[mg][m]);
+            }
+        }
+    };
+
+    // ---- main loop: prefetch step s+NW while computing step s
+    int step = wave;
+    StepData<PER_TOKEN> cur;
+    if (step < nsteps) load_step(step, cur);
+    while (step < nsteps) {
+        const int nxt_step = step + NW;
+        StepData<PER_TOKEN> nxt;
+        if (nxt_step < nsteps) load_step(nxt_step, nxt);
+        compute_step(step, cur);
+        cur = nxt;
+        step = nxt_step;
+    }
+
+    // ---- finish: sum the four kg-lane partial exp sums of each query row
+#pragma unroll
+    for (int mg = 0; mg < MTP; ++mg) {
+        float lt = l_run[mg];
+        lt += shfl_xor_f(lt, 16);
+        lt += shfl_xor_f(lt, 32);
+        l_run[mg] = lt;
+    }
+
+    if constexpr (NW == 1) {
+#pragma unroll
+        for (int mg = 0; mg < MTP; ++mg) {
+            const int r = mg * 16 + l16;
+            if (r < p.eqgs) {
+                const float L = l_run[mg];
+                const float inv = L > 0.f ? v_fac / L : 0.f;
+#pragma unroll
+                for (int m = 0; m < 8; ++m) {
+                    const f32x4 v = o[mg][m] * inv;
+                    uint2 pk;
+                    pk.x = uint32_t(f32_to_bf16_bits(v[0])) | (uint32_t(f32_to_bf16_bits(v[1])) << 16);
+                    pk.y = uint32_t(f32_to_bf16_bits(v[2])) | (uint32_t(f32_to_bf16_bits(v[3])) << 16);
+                    *reinterpret_cast<uint2 *>(to + r * p.s_to_group + 16 * m + 4 * kg) = pk;
+                }
+                if (kg == 0) {
+                    es[r] = L;
+                    ml[r] = L > 0.f ? m_run[mg] * kLn2 : -INFINITY;
+                }
+            }
+        }
+    } else {
+        constexpr int DP = D + 4;
+        __shared__ float s_o[NW][16][DP];
+        __shared__ float s_m[NW][16];
+        __shared__ float s_l[NW][16];
+        constexpr int E = 16 * D / (NW * 64);  // outputs per thread in the merge
+        const int flat = tid * E;
+        const int n = flat / D;
+        const int d0 = flat % D;
+#pragma unroll
+        for (int mg = 0; mg < MTP; ++mg) {
+#pragma unroll
+            for (int m = 0; m < 8; ++m) *reinterpret_cast<f32x4 *>(&s_o[wave][l16][16 * m + 4 * kg]) = o[mg][m];
+            if (kg == 0) {
+                s_m[wave][l16] = m_run[mg];
+                s_l[wave][l16] = l_run[mg];
+            }
+            __syncthreads();
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][n]);
+            const float Ms = M == -INFINITY ? 0.0f : M;
+            float f[NW];
+            float L = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                f[w] = fast_exp2(s_m[w][n] - Ms);
+                L += s_l[w][n] * f[w];
+            }
+            const float inv = L > 0.f ? v_fac / L : 0.f;
+            const int r = mg * 16 + n;
+            if (r < p.eqgs) {
+#pragma unroll
+                for (int e0 = 0; e0 < E; e0 += 8) {
+                    uint32_t pk[4];
+#pragma unroll
+                    for (int j = 0; j < 8; j += 2) {
+                        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+                        for (int w = 0; w < NW; ++w) {
+                            a0 += s_o[w][n][d0 + e0 + j] * f[w];
+                            a1 += s_o[w][n][d0 + e0 + j + 1] * f[w];
+                        }
+                        pk[j / 2] = uint32_t(f32_to_bf16_bits(a0 * inv)) | (uint32_t(f32_to_bf16_bits(a1 * inv)) << 16);
+                    }
+                    *reinterpret_cast<uint4 *>(to + r * p.s_to_group + d0 + e0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+                }
+                if (d0 == 0) {
+                    es[r] = L;
+                    ml[r] = L > 0.f ? M * kLn2 : -INFINITY;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Log-sum-exp merge of the P partials of one (sequence, kv head, query row):
+// one wave, lane owns head dims 2*lane and 2*lane+1 (kernels/pa_decode_swa.py:954-1130).
+template <int OUT>
+__global__ __launch_bounds__(64) void pa_lse_reduce_kernel(const ReduceParams p) {
+    const int lane = threadIdx.x;
+    const int b = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
+    const float *es = p.es + b * p.s_es_seq + h * p.s_es_head + r;
+    const float *ml = p.ml + b * p.s_es_seq + h * p.s_es_head + r;
+    const uint16_t *to = p.to + b * p.s_to_seq + h * p.s_to_head + r * p.s_to_group + 2 * lane;
+    const int P = p.max_parts;
+
+    float mloc = -INFINITY;
+    for (int z = lane; z < P; z += 64) mloc = fmaxf(mloc, ml[z * p.s_es_part]);
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) mloc = fmaxf(mloc, shfl_xor_f(mloc, sh));
+    const float Ms = mloc == -INFINITY ? 0.0f : mloc;
+    float wl = 0.f;
+    for (int z = lane; z < P; z += 64) {
+        const float mz = ml[z * p.s_es_part];
+        wl += es[z * p.s_es_part] * fast_exp2((mz - Ms) * kLog2e);
+    }
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) wl += shfl_xor_f(wl, sh);
+    const float inv = wl > 0.f ? 1.0f / wl : 0.0f;
+
+    float a0 = 0.f, a1 = 0.f;
+    for (int z = 0; z < P; ++z) {
+        const float w = es[z * p.s_es_part] * fast_exp2((ml[z * p.s_es_part] - Ms) * kLog2e) * inv;
+        if (w != 0.f) {
+            const uint32_t two = *reinterpret_cast<const uint32_t *>(to + z * p.s_to_part);
+            a0 += w * bf16_bits_to_f32(uint16_t(two & 0xffffu));
+            a1 += w * bf16_bits_to_f32(uint16_t(two >> 16));
+        }
+    }
+    const int qi = r / p.g, gi = r - (r / p.g) * p.g;
+    const int64_t off = b * p.s_o_seq + qi * p.s_o_len + h * p.s_o_head + gi * p.s_o_group + 2 * lane;
+    if constexpr (OUT == PA_FP8_F32) {
+        float *o = reinterpret_cast<float *>(p.out) + off;
+        *reinterpret_cast<float2 *>(o) = make_float2(a0, a1);
+    } else if constexpr (OUT == PA_FP8_F16) {
+        uint16_t *o = reinterpret_cast<uint16_t *>(p.out) + off;
+        *reinterpret_cast<uint32_t *>(o) = uint32_t(f32_to_f16_bits(a0)) | (uint32_t(f32_to_f16_bits(a1)) << 16);
+    } else {
+        uint16_t *o = reinterpret_cast<uint16_t *>(p.out) + off;
+        *reinterpret_cast<uint32_t *>(o) = uint32_t(f32_to_bf16_bits(a0)) | (uint32_t(f32_to_bf16_bits(a1)) << 16);
+    }
+}
+
+constexpr int kWaves = 4;
+
+template <int MTP, bool PT>
+hipError_t launch_decode(const DecodeParams &p, dim3 grid, hipStream_t s) {
+    hipLaunchKernelGGL((pa_decode_partition_kernel<MTP, PT, kWaves>), grid, dim3(kWaves * 64), 0, s, p);
+    return hipGetLastError();
+}
+
+bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+int log2_pow2(int v) {
+    if (v <= 0 || (v & (v - 1)) != 0) return -1;
+    int l = 0;
+    while ((1 << l) < v) ++l;
+    return l;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pa_fp8_abi_version(void) { return PA_FP8_ABI_VERSION; }
+
+const char *pa_fp8_status_string(int status) {
+    switch (status) {
+    case PA_FP8_OK: return "ok";
+    case PA_FP8_ERR_NULL_POINTER: return "a required pointer is NULL";
+    case PA_FP8_ERR_HEAD_DIM: return "unsupported head_dim (only 128 is built)";
+    case PA_FP8_ERR_BLOCK_SIZE: return "block_size must be a power of two >= 16";
+    case PA_FP8_ERR_GROUP: return "query_length * query_group_size must be in 1..64";
+    case PA_FP8_ERR_SHAPE: return "a size, stride or alignment is out of range";
+    case PA_FP8_ERR_DTYPE: return "unsupported dtype";
+    case PA_FP8_ERR_PARTITIONS: return "max_context_partition_num must be in 1..65535";
+    case PA_FP8_ERR_WORKLIST: return "worklist buffers too small for the schedule";
+    default: break;
+    }
+    if (status >= PA_FP8_ERR_HIP) return hipGetErrorString((hipError_t)(status - PA_FP8_ERR_HIP));
+    return "unknown status";
+}
+
+int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
+    if (!a) return PA_FP8_ERR_NULL_POINTER;
+    if (a->batch_size < 0 || a->num_kv_heads <= 0 || a->query_group_size <= 0 || a->query_length <= 0)
+        return PA_FP8_ERR_SHAPE;
+    if (a->head_dim != kHeadDim) return PA_FP8_ERR_HEAD_DIM;
+    const int bs_log2 = log2_pow2(a->block_size);
+    if (bs_log2 < 4) return PA_FP8_ERR_BLOCK_SIZE;
+    const int eqgs = a->query_length * a->query_group_size;
+    if (eqgs < 1 || eqgs > 64) return PA_FP8_ERR_GROUP;
+    if (a->max_context_partition_num < 1 || a->max_context_partition_num > 65535) return PA_FP8_ERR_PARTITIONS;
+    if (a->query_dtype != PA_FP8_BF16 && a->query_dtype != PA_FP8_F16) return PA_FP8_ERR_DTYPE;
+    if (a->num_kv_heads > 65535 || a->sliding_window < 0) return PA_FP8_ERR_SHAPE;
+    if (a->batch_size == 0) return PA_FP8_OK;
+    if (!a->exp_sums || !a->max_logits || !a->tmp_out || !a->query || !a->key_cache || !a->value_cache ||
+        !a->block_tables || !a->context_lengths || !a->key_scale || !a->value_scale)
+        return PA_FP8_ERR_NULL_POINTER;
+    if (a->num_blocks <= 0 || a->max_blocks_per_seq <= 0) return PA_FP8_ERR_SHAPE;
+    // 16-byte vector accesses: caches, query rows and partial rows must be 16-byte aligned
+    if (!aligned16(a->key_cache) || !aligned16(a->value_cache) || !aligned16(a->query) || !aligned16(a->tmp_out))
+        return PA_FP8_ERR_SHAPE;
+    if ((a->stride_k_block | a->stride_k_head | a->stride_v_block | a->stride_v_head) & 15) return PA_FP8_ERR_SHAPE;
+    if ((a->stride_q_seq | a->stride_q_head) & 7) return PA_FP8_ERR_SHAPE;
+    if ((a->stride_to_seq | a->stride_to_head | a->stride_to_part | a->stride_to_group) & 7) return PA_FP8_ERR_SHAPE;
+    if (a->per_token_kv) {
+        if (!aligned16(a->key_scale) || !aligned16(a->value_scale)) return PA_FP8_ERR_SHAPE;
+        if ((a->stride_ks_block | a->stride_ks_head) & 3) return PA_FP8_ERR_SHAPE;
+    }
+
+    DecodeParams p;
+    p.exp_sums = a->exp_sums;
+    p.max_logits = a->max_logits;
+    p.tmp_out = reinterpret_cast<uint16_t *>(a->tmp_out);
+    p.query = reinterpret_cast<const uint16_t *>(a->query);
+    p.kc = a->key_cache;
+    p.vc = a->value_cache;
+    p.bt = a->block_tables;
+    p.ctx = a->context_lengths;
+    p.ks = a->key_scale;
+    p.vs = a->value_scale;
+    p.s_q_seq = a->stride_q_seq;
+    p.s_q_head = a->stride_q_head;
+    p.s_k_block = a->stride_k_block;
+    p.s_k_head = a->stride_k_head;
+    p.s_v_block = a->stride_v_block;
+    p.s_v_head = a->stride_v_head;
+    p.s_es_seq = a->stride_es_seq;
+    p.s_es_head = a->stride_es_head;
+    p.s_es_part = a->stride_es_part;
+    p.s_to_seq = a->stride_to_seq;
+    p.s_to_head = a->stride_to_head;
+    p.s_to_part = a->stride_to_part;
+    p.s_to_group = a->stride_to_group;
+    p.s_bt_seq = a->stride_bt_seq;
+    p.s_ks_block = a->per_token_kv ? a->stride_ks_block : 0;
+    p.s_ks_head = a->per_token_kv ? a->stride_ks_head : 0;
+    p.g = a->query_group_size;
+    p.ql = a->query_length;
+    p.eqgs = eqgs;
+    p.bs_log2 = bs_log2;
+    p.num_blocks = a->num_blocks;
+    p.max_blocks = a->max_blocks_per_seq;
+    p.max_parts = a->max_context_partition_num;
+    p.sw = a->sliding_window;
+    p.q_f16 = a->query_dtype == PA_FP8_F16;
+    p.qk_scale = a->softmax_scale * kLog2e;
+
+    const dim3 grid(a->batch_size, a->num_kv_heads, a->max_context_partition_num);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int mtp = (eqgs + 15) / 16;
+    hipError_t err;
+    const bool pt = a->per_token_kv != 0;
+    switch (mtp * 2 + (pt ? 1 : 0)) {
+    case 2: err = launch_decode<1, false>(p, grid, s); break;
+    case 3: err = launch_decode<1, true>(p, grid, s); break;
+    case 4: err = launch_decode<2, false>(p, grid, s); break;
+    case 5: err = launch_decode<2, true>(p, grid, s); break;
+    case 6: err = launch_decode<3, false>(p, grid, s); break;
+    case 7: err = launch_decode<3, true>(p, grid, s); break;
+    case 8: err = launch_decode<4, false>(p, grid, s); break;
+    default: err = launch_decode<4, true>(p, grid, s); break;
+    }
+    return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
+}
+
+int pa_fp8_lse_reduce(const pa_fp8_reduce_args *a, void *stream) {
+    if (!a) return PA_FP8_ERR_NULL_POINTER;
+    if (a->batch_size < 0 || a->num_kv_heads <= 0 || a->query_group_size <= 0 || a->query_length <= 0)
+        return PA_FP8_ERR_SHAPE;
+    if (a->head_dim != kHeadDim) return PA_FP8_ERR_HEAD_DIM;
+    if (a->max_context_partition_num < 1) return PA_FP8_ERR_PARTITIONS;
+    const int eqgs = a->query_length * a->query_group_size;
+    if (eqgs > 65535 || a->num_kv_heads > 65535) return PA_FP8_ERR_SHAPE;
+    if (a->out_dtype != PA_FP8_BF16 && a->out_dtype != PA_FP8_F16 && a->out_dtype != PA_FP8_F32)
+        return PA_FP8_ERR_DTYPE;
+    if (a->batch_size == 0) return PA_FP8_OK;
+    if (!a->output || !a->exp_sums || !a->max_logits || !a->tmp_out) return PA_FP8_ERR_NULL_POINTER;
+    const int esz = a->out_dtype == PA_FP8_F32 ? 4 : 2;
+    if ((reinterpret_cast<uintptr_t>(a->output) & (2 * esz - 1)) || (reinterpret_cast<uintptr_t>(a->tmp_out) & 3))
+        return PA_FP8_ERR_SHAPE;
+    if ((a->stride_o_seq | a->stride_o_len | a->stride_o_head | a->stride_o_group) & 1) return PA_FP8_ERR_SHAPE;
+    if ((a->stride_to_seq | a->stride_to_head | a->stride_to_part | a->stride_to_group) & 1) return PA_FP8_ERR_SHAPE;
+
+    ReduceParams p;
+    p.out = a->output;
+    p.es = a->exp_sums;
+    p.ml = a->max_logits;
+    p.to = reinterpret_cast<const uint16_t *>(a->tmp_out);
+    p.s_o_seq = a->stride_o_seq;
+    p.s_o_len = a->stride_o_len;
+    p.s_o_head = a->stride_o_head;
+    p.s_o_group = a->stride_o_group;
+    p.s_es_seq = a->stride_es_seq;
+    p.s_es_head = a->stride_es_head;
+    p.s_es_part = a->stride_es_part;
+    p.s_to_seq = a->stride_to_seq;
+    p.s_to_head = a->stride_to_head;
+    p.s_to_part = a->stride_to_part;
+    p.s_to_group = a->stride_to_group;
+    p.g = a->query_group_size;
+    p.max_parts = a->max_context_partition_num;
+    const dim3 grid(a->batch_size, a->num_kv_heads, eqgs);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    switch (a->out_dtype) {
+    case PA_FP8_F32: hipLaunchKernelGGL(pa_lse_reduce_kernel<PA_FP8_F32>, grid, dim3(64), 0, s, p); break;
+    case PA_FP8_F16: hipLaunchKernelGGL(pa_lse_reduce_kernel<PA_FP8_F16>, grid, dim3(64), 0, s, p); break;
+    default: hipLaunchKernelGGL(pa_lse_reduce_kernel<PA_FP8_BF16>, grid, dim3(64), 0, s, p); break;
+    }
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
+}
+
+}  // extern "C"

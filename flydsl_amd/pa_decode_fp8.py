@@ -1,0 +1,487 @@
+"""Drop-in host API of the FP8 paged-attention decode path (gfx950 / MI355X).
+
+Same names, arguments, return tags and error behaviour as the reference
+launcher module kernels/pa_decode_fp8.py:
+
+* ``pa_decode_ps_launch``     -- kernels/pa_decode_fp8.py:2812-3202
+* ``get_pa_metadata``         -- kernels/pa_decode_fp8.py:1729-1859
+* ``get_recommended_splits``  -- kernels/pa_decode_fp8.py:1922-1949
+
+Every kernel is a hand-written HIP kernel in libpa_fp8.so reached through the
+C ABI of include/pa_fp8.h; tensors are plain torch device tensors.
+"""
+
+from __future__ import annotations
+
+import functools
+import math
+
+import torch
+
+from . import _lib
+from .pa_decode_swa import _reduce_args, get_sw_max_context_partition_num  # noqa: F401
+from .pa_metadata import get_pa_metadata_info_v1, get_pa_metadata_v1
+
+KV_COMPUTE_BLOCK = 256  # tokens per context partition (kernels/pa_decode_fp8.py:36)
+_PA_METADATA_GRID_OVERSUB = 3  # kernels/pa_decode_fp8.py:37-40
+_PA_DECODE_PS_SMALL_BLOCK_SIZES = (16, 64)  # kernels/pa_decode_fp8.py:1955
+HEAD_DIM = 128
+
+_PACKED_FP8_QUERY_DTYPES = tuple(
+    dt
+    for dt in (torch.uint8, getattr(torch, "float8_e4m3fnuz", None), getattr(torch, "float8_e4m3fn", None))
+    if dt is not None
+)
+_FP8_CACHE_DTYPES = tuple(
+    dt for dt in (torch.uint8, torch.int8, getattr(torch, "float8_e4m3fn", None)) if dt is not None
+)
+
+
+def _cdiv(a: int, b: int) -> int:
+    return (a + b - 1) // b
+
+
+@functools.lru_cache(maxsize=16)
+def _cu_count(device_index: int) -> int:
+    return torch.cuda.get_device_properties(device_index).multi_processor_count
+
+
+def _device_cu_count(dev: torch.device) -> int:
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    return _cu_count(idx)
+
+
+def get_recommended_splits(
+    num_sequences: int,
+    num_kv_heads: int,
+    split_kv_blocks: int = 1,
+    *,
+    sliding_window: int = 0,
+    context_partition_size: int = KV_COMPUTE_BLOCK,
+    query_length: int = 1,
+) -> int:
+    """Recommended ``max_context_partition_num`` (kernels/pa_decode_fp8.py:1922-1949).
+
+    Sliding window: ``cdiv(sliding_window + query_length - 1, partition) + 1``.
+    Otherwise ``clamp(cdiv(2*CUs, max(1, seqs*kv_heads*split)) * split, 4, 8)``.
+    """
+    if sliding_window > 0:
+        return _cdiv(sliding_window + query_length - 1, context_partition_size) + 1
+    num_sm = _cu_count(torch.cuda.current_device()) * 2
+    denom = max(1, num_sequences * num_kv_heads * split_kv_blocks)
+    n = _cdiv(num_sm, denom) * split_kv_blocks
+    return max(4, min(n, 8))
+
+
+def _is_current_stream_capturing() -> bool:
+    if not torch.cuda.is_available():
+        return False
+    try:
+        return torch.cuda.is_current_stream_capturing()
+    except RuntimeError:
+        return False
+
+
+def _prepare_scale_tensor(name: str, scale, *, device: torch.device, is_graph_capturing: bool) -> torch.Tensor:
+    """float / tensor -> f32 device tensor (kernels/pa_decode_fp8.py:1871-1895)."""
+    if isinstance(scale, torch.Tensor):
+        if is_graph_capturing:
+            if scale.device != device:
+                raise ValueError(f"CUDA graph capture requires `{name}` to already be on {device}, got {scale.device}.")
+            if scale.dtype != torch.float32:
+                raise ValueError(f"CUDA graph capture requires `{name}` to already be float32, got {scale.dtype}.")
+            return scale
+        return scale.to(device=device, dtype=torch.float32)
+    if is_graph_capturing:
+        raise ValueError(
+            f"CUDA graph capture requires `{name}` to be passed as a pre-created float32 tensor on the target device."
+        )
+    return torch.tensor([float(scale or 1.0)], device=device, dtype=torch.float32)
+
+
+def _get_query_input_dtype(query: torch.Tensor) -> str:
+    if query.dtype in _PACKED_FP8_QUERY_DTYPES:
+        return "packed_fp8"
+    if query.dtype == torch.bfloat16:
+        return "bf16"
+    if query.dtype == torch.float16:
+        return "f16"
+    raise ValueError(
+        f"Unsupported query dtype for pa_decode_ps_launch: {query.dtype}. Expected packed FP8/uint8, bf16, or f16."
+    )
+
+
+def _get_output_dtype_str(output: torch.Tensor) -> str:
+    if output.dtype == torch.bfloat16:
+        return "bf16"
+    if output.dtype == torch.float16:
+        return "f16"
+    if output.dtype == torch.float32:
+        return "f32"
+    raise ValueError(
+        f"Unsupported output dtype for pa_decode_ps_launch reduce: {output.dtype}. Expected bf16, f16, or f32."
+    )
+
+
+def _check_int32(name: str, t: torch.Tensor, ndim: int) -> None:
+    if t.dtype != torch.int32 or t.dim() != ndim:
+        raise ValueError(f"`{name}` must be a {ndim}-D int32 tensor, got {tuple(t.shape)} {t.dtype}")
+
+
+def _check_cache_layouts(key_cache: torch.Tensor, value_cache: torch.Tensor, head_size: int) -> int:
+    if key_cache.dim() != 5:
+        raise ValueError(f"key_cache must be [num_blocks, kv_heads, head_dim/16, block_size, 16], got {tuple(key_cache.shape)}")
+    if key_cache.element_size() != 1 or value_cache.element_size() != 1:
+        raise ValueError("key_cache / value_cache must hold one-byte fp8 e4m3fn values (uint8 / float8_e4m3fn view)")
+    nb, hkv, dc, bs, x = key_cache.shape
+    if x != 16 or dc * 16 != head_size:
+        raise ValueError(f"key_cache inner dims {tuple(key_cache.shape[2:])} do not match head_dim {head_size}")
+    if value_cache.dim() != 5:
+        raise NotImplementedError("pa_decode_ps_launch: trans_v=False (4-D value_cache) not yet supported.")
+    if tuple(value_cache.shape) != (nb, hkv, bs // 16, head_size, 16):
+        raise ValueError(f"value_cache {tuple(value_cache.shape)} is not the trans_v layout of key_cache")
+    if key_cache.stride()[2:] != (bs * 16, 16, 1):
+        raise ValueError("key_cache must be contiguous within each (block, kv head) tile")
+    if value_cache.stride()[2:] != (head_size * 16, 16, 1):
+        raise ValueError("value_cache must be contiguous within each (block, kv head) tile")
+    return bs
+
+
+def _u8(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.uint8 else t.view(torch.uint8)
+
+
+def _decode_args(
+    *,
+    query,
+    key_cache,
+    value_cache,
+    block_tables,
+    context_lengths,
+    key_scale,
+    value_scale,
+    per_token_kv,
+    exp_sums,
+    max_logits,
+    temporary_output,
+    query_length,
+    query_group_size,
+    max_parts,
+    sliding_window,
+    softmax_scale,
+) -> _lib.DecodeArgs:
+    a = _lib.DecodeArgs()
+    a.exp_sums = exp_sums.data_ptr()
+    a.max_logits = max_logits.data_ptr()
+    a.tmp_out = temporary_output.data_ptr()
+    a.query = query.data_ptr()
+    a.key_cache = key_cache.data_ptr()
+    a.value_cache = value_cache.data_ptr()
+    a.block_tables = block_tables.data_ptr()
+    a.context_lengths = context_lengths.data_ptr()
+    a.key_scale = key_scale.data_ptr()
+    a.value_scale = value_scale.data_ptr()
+    a.stride_q_seq, a.stride_q_head = query.stride(0), query.stride(1)
+    a.stride_k_block, a.stride_k_head = key_cache.stride(0), key_cache.stride(1)
+    a.stride_v_block, a.stride_v_head = value_cache.stride(0), value_cache.stride(1)
+    a.stride_es_seq, a.stride_es_head, a.stride_es_part = exp_sums.stride(0), exp_sums.stride(1), exp_sums.stride(2)
+    a.stride_to_seq, a.stride_to_head = temporary_output.stride(0), temporary_output.stride(1)
+    a.stride_to_part, a.stride_to_group = temporary_output.stride(2), temporary_output.stride(3)
+    a.stride_bt_seq = block_tables.stride(0)
+    if per_token_kv:
+        a.stride_ks_block, a.stride_ks_head = key_scale.stride(0), key_scale.stride(1)
+    a.batch_size = context_lengths.shape[0]
+    a.num_kv_heads = key_cache.shape[1]
+    a.query_group_size = query_group_size
+    a.query_length = query_length
+    a.head_dim = query.shape[-1]
+    a.block_size = key_cache.shape[-2]
+    a.num_blocks = key_cache.shape[0]
+    a.max_blocks_per_seq = block_tables.shape[1]
+    a.max_context_partition_num = max_parts
+    a.sliding_window = sliding_window
+    a.per_token_kv = 1 if per_token_kv else 0
+    a.query_dtype = _lib.PA_FP8_F16 if query.dtype == torch.float16 else _lib.PA_FP8_BF16
+    a.softmax_scale = float(softmax_scale)
+    return a
+
+
+def _check_intermediates(exp_sums, max_logits, temporary_output, shape, head_size):
+    if tuple(exp_sums.shape) != shape or exp_sums.dtype != torch.float32 or exp_sums.stride(3) != 1:
+        raise ValueError(f"exp_sums must be float32 {shape} with a unit last stride")
+    if tuple(max_logits.shape) != shape or max_logits.dtype != torch.float32 or max_logits.stride(3) != 1:
+        raise ValueError(f"max_logits must be float32 {shape} with a unit last stride")
+    if exp_sums.stride() != max_logits.stride():
+        raise ValueError("exp_sums and max_logits must share strides")
+    if (
+        tuple(temporary_output.shape) != shape + (head_size,)
+        or temporary_output.dtype != torch.bfloat16
+        or temporary_output.stride(4) != 1
+    ):
+        raise ValueError(f"temporary_output must be bfloat16 {shape + (head_size,)} with a unit last stride")
+
+
+def _validate_scale(name: str, scale: torch.Tensor, per_token: bool, key_cache: torch.Tensor) -> None:
+    nb, hkv, _, bs, _ = key_cache.shape
+    if per_token:
+        if scale.dim() != 4 or tuple(scale.shape) != (nb, hkv, bs, 1) or scale.stride(2) != 1:
+            raise ValueError(f"per-token `{name}` must be float32 [num_blocks, kv_heads, block_size, 1], got {tuple(scale.shape)}")
+    elif scale.numel() != 1:
+        raise ValueError(f"per-tensor `{name}` must hold one value, got {tuple(scale.shape)}")
+
+
+def _run_partitioned(
+    output,
+    query,
+    key_cache,
+    value_cache,
+    context_lengths,
+    block_tables,
+    softmax_scale,
+    key_scale,
+    value_scale,
+    per_token_kv,
+    sliding_window,
+    max_parts,
+    exp_sums,
+    max_logits,
+    temporary_output,
+    stream,
+    is_graph_capturing,
+    path_name,
+):
+    dev = query.device
+    batch_size = context_lengths.shape[0]
+    num_query_heads = query.shape[1]
+    num_kv_heads = key_cache.shape[1]
+    head_size = query.shape[-1]
+    query_group_size = num_query_heads // num_kv_heads
+    query_length = query.shape[0] // batch_size if batch_size else 1
+    eqgs = query_length * query_group_size
+    shape = (batch_size, num_kv_heads, max_parts, eqgs)
+    if is_graph_capturing and (exp_sums is None or max_logits is None or temporary_output is None):
+        raise ValueError(
+            "CUDA graph capture requires preallocated `exp_sums`, `max_logits`, "
+            f"and `temporary_output` for the {path_name} path."
+        )
+    # every slot (including empty ones) is written by the kernel, so no fill is needed
+    if exp_sums is None:
+        exp_sums = torch.empty(shape, device=dev, dtype=torch.float32)
+    if max_logits is None:
+        max_logits = torch.empty(shape, device=dev, dtype=torch.float32)
+    if temporary_output is None:
+        temporary_output = torch.empty(shape + (head_size,), device=dev, dtype=torch.bfloat16)
+    _check_intermediates(exp_sums, max_logits, temporary_output, shape, head_size)
+    output_5d = output.view(batch_size, query_length, num_kv_heads, query_group_size, head_size)
+    args = _decode_args(
+        query=query,
+        key_cache=_u8(key_cache),
+        value_cache=_u8(value_cache),
+        block_tables=block_tables,
+        context_lengths=context_lengths,
+        key_scale=key_scale,
+        value_scale=value_scale,
+        per_token_kv=per_token_kv,
+        exp_sums=exp_sums,
+        max_logits=max_logits,
+        temporary_output=temporary_output,
+        query_length=query_length,
+        query_group_size=query_group_size,
+        max_parts=max_parts,
+        sliding_window=sliding_window,
+        softmax_scale=softmax_scale,
+    )
+    _lib.decode_partitions(args, stream)
+    rargs = _reduce_args(output_5d, exp_sums, max_logits, temporary_output, max_parts, _get_output_dtype_str(output))
+    _lib.lse_reduce(rargs, stream)
+
+
+def pa_decode_ps_launch(
+    output: torch.Tensor,
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    context_lengths: torch.Tensor,
+    kv_page_indices: torch.Tensor,
+    kv_indptr: torch.Tensor,
+    softmax_scale: float,
+    key_scale: torch.Tensor = None,
+    value_scale: torch.Tensor = None,
+    *,
+    sliding_window: int = 0,
+    metadata: dict = None,
+    block_tables: torch.Tensor = None,
+    max_context_partition_num: int = 0,
+    exp_sums: torch.Tensor = None,
+    max_logits: torch.Tensor = None,
+    temporary_output: torch.Tensor = None,
+    stream=None,
+) -> str:
+    """Paged-attention decode over an fp8 e4m3fn KV cache (kernels/pa_decode_fp8.py:2812-3202).
+
+    Routing follows the reference: ``sliding_window > 0`` -> sliding-window
+    split-context path; block sizes 16 / 64 -> small-block split-context path;
+    other block sizes -> partitioned path over the same kernels (the reference
+    routes them to its persistent worklist kernel).  Every path is one
+    partition kernel plus the log-sum-exp reduce and writes ``output`` in place.
+
+    Returns the path tag: "ps_sw_partitioned" / "ps_sw_fused_partitioned",
+    "ps_small_block" or "ps_partitioned".
+    """
+    if query.dim() != 3:
+        raise ValueError(f"query must be [num_seqs*query_length, num_heads, head_dim], got {tuple(query.shape)}")
+    num_query_heads = query.shape[1]
+    num_kv_heads = key_cache.shape[1]
+    query_input_dtype = _get_query_input_dtype(query)
+    dev = query.device
+    is_graph_capturing = _is_current_stream_capturing()
+    key_scale = _prepare_scale_tensor("key_scale", key_scale, device=dev, is_graph_capturing=is_graph_capturing)
+    value_scale = _prepare_scale_tensor("value_scale", value_scale, device=dev, is_graph_capturing=is_graph_capturing)
+    if query_input_dtype == "packed_fp8":
+        raise ValueError(
+            "`pa_decode_ps_launch` no longer accepts host query_scale and only supports "
+            "bf16/f16 query inputs with kernel-internal query scale computation."
+        )
+    head_size = query.shape[-1]
+    if head_size != HEAD_DIM:
+        raise ValueError(f"Unsupported head_dim={head_size}; this build supports {HEAD_DIM}.")
+    if num_query_heads % num_kv_heads != 0:
+        raise ValueError("Query heads must be divisible by KV heads")
+    _check_int32("context_lengths", context_lengths, 1)
+    batch_size = context_lengths.shape[0]
+    if batch_size == 0 or query.shape[0] % batch_size != 0:
+        raise ValueError(f"query rows {query.shape[0]} are not a multiple of batch size {batch_size}")
+    if tuple(output.shape) != tuple(query.shape):
+        raise ValueError(f"output shape {tuple(output.shape)} must equal query shape {tuple(query.shape)}")
+    _get_output_dtype_str(output)
+    if query.stride(2) != 1 or not output.is_contiguous():
+        raise ValueError("query needs a unit last stride and output must be contiguous")
+    block_size = _check_cache_layouts(key_cache, value_cache, head_size)
+    if block_size < 16 or block_size & (block_size - 1):
+        raise ValueError(f"pa_decode_ps_launch: unsupported block_size={block_size}; expected a power of two >= 16.")
+    per_token_kv = key_scale.ndim > 1
+    _validate_scale("key_scale", key_scale, per_token_kv, key_cache)
+    _validate_scale("value_scale", value_scale, value_scale.ndim > 1, key_cache)
+    if (value_scale.ndim > 1) != per_token_kv:
+        raise ValueError("key_scale and value_scale must both be per-tensor or both per-token")
+    query_length = query.shape[0] // batch_size
+    query_group_size = num_query_heads // num_kv_heads
+    if query_length * query_group_size > 64:
+        raise ValueError("query_length * (num_query_heads // num_kv_heads) must be <= 64")
+    for name, t in (("query", query), ("key_cache", key_cache), ("value_cache", value_cache), ("output", output),
+                    ("context_lengths", context_lengths), ("key_scale", key_scale), ("value_scale", value_scale)):
+        if t.device != dev:
+            raise ValueError(f"`{name}` is on {t.device}, expected {dev}")
+    if block_tables is None:
+        raise ValueError(
+            f"pa_decode_ps_launch: block_size={block_size} requires `block_tables` "
+            "(per-sequence physical block index table)."
+        )
+    _check_int32("block_tables", block_tables, 2)
+    if block_tables.shape[0] != batch_size or block_tables.stride(1) != 1 or block_tables.device != dev:
+        raise ValueError("block_tables must be [num_seqs, max_blocks] on the query device with a unit last stride")
+    s = stream if stream is not None else torch.cuda.current_stream(dev)
+    stream_handle = s.cuda_stream if hasattr(s, "cuda_stream") else int(s)
+
+    if sliding_window > 0:
+        if max_context_partition_num == 0:
+            max_context_partition_num = get_recommended_splits(
+                batch_size,
+                num_kv_heads,
+                sliding_window=sliding_window,
+                context_partition_size=KV_COMPUTE_BLOCK,
+                query_length=query_length,
+            )
+        _run_partitioned(output, query, key_cache, value_cache, context_lengths, block_tables, softmax_scale,
+                         key_scale, value_scale, per_token_kv, sliding_window, max_context_partition_num,
+                         exp_sums, max_logits, temporary_output, stream_handle, is_graph_capturing, "sliding-window")
+        return "ps_sw_fused_partitioned" if max_context_partition_num <= 1 else "ps_sw_partitioned"
+
+    if max_context_partition_num == 0:
+        max_context_partition_num = get_recommended_splits(
+            batch_size, num_kv_heads, split_kv_blocks=max(1, KV_COMPUTE_BLOCK // block_size)
+        )
+    path = "small-block PS" if block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES else "partitioned"
+    _run_partitioned(output, query, key_cache, value_cache, context_lengths, block_tables, softmax_scale,
+                     key_scale, value_scale, per_token_kv, 0, max_context_partition_num,
+                     exp_sums, max_logits, temporary_output, stream_handle, is_graph_capturing, path)
+    return "ps_small_block" if block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES else "ps_partitioned"
+
+
+def get_pa_metadata(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    context_lengths: torch.Tensor,
+    kv_indptr: torch.Tensor,
+    num_query_heads: int,
+    num_kv_heads: int,
+    partition_size: int = KV_COMPUTE_BLOCK,
+):
+    """Worklist metadata for the persistent decode (kernels/pa_decode_fp8.py:1729-1859).
+
+    Runs the device scheduler ``get_pa_metadata_v1`` over
+    ``num_sm = (CUs * 3 // kv_heads) * kv_heads`` bins; work_info kv ranges are
+    cumulative ``partition_size``-token partition indices.  Synchronises once on
+    ``reduce_indptr[-1]`` to size the partial buffers, as the reference does.
+    """
+    dev = query.device
+    batch_size = context_lengths.shape[0]
+    query_length = query.shape[0] // batch_size
+    head_size = query.shape[-1]
+    num_sm = _device_cu_count(dev) * _PA_METADATA_GRID_OVERSUB
+    num_sm = (num_sm // num_kv_heads) * num_kv_heads
+    seqlens_qo_indptr = torch.arange(batch_size + 1, dtype=torch.int32, device=dev) * query_length
+    parts = (context_lengths.to(torch.int32) + (partition_size - 1)) // partition_size
+    partition_indptr = torch.zeros(batch_size + 1, dtype=torch.int32, device=dev)
+    partition_indptr[1:] = torch.cumsum(parts, dim=0).to(torch.int32)
+    block_size = key_cache.shape[-2]
+    infos = get_pa_metadata_info_v1(batch_size, num_kv_heads, num_cu=num_sm)
+    bufs = [torch.empty(shape, dtype=dtype, device=dev) for shape, dtype in infos]
+    work_metadata_ptrs, work_indptr, work_info, reduce_indptr, reduce_final_map, reduce_partial_map = bufs
+    get_pa_metadata_v1(
+        seqlens_qo_indptr,
+        kv_indptr,
+        context_lengths,
+        num_query_heads // num_kv_heads,
+        num_kv_heads,
+        True,
+        work_metadata_ptrs,
+        work_indptr,
+        work_info,
+        reduce_indptr,
+        reduce_final_map,
+        reduce_partial_map,
+        kv_granularity=partition_size,
+        block_size=block_size,
+        max_seqlen_qo=query_length,
+        uni_seqlen_qo=query_length,
+        fast_mode=True,
+        max_split_per_batch=-1,
+        num_cu=num_sm,
+    )
+    work_info_flat = work_info.reshape(-1).contiguous()
+    num_partials = int(reduce_indptr[-1].item())
+    partial_output = torch.empty(
+        ((num_partials + 1) * query_length, 1, num_query_heads, head_size), dtype=torch.float32, device=dev
+    )
+    partial_lse = torch.empty(((num_partials + 1) * query_length, 1, num_query_heads, 1), dtype=torch.float32, device=dev)
+    return {
+        "work_indptr": work_indptr,
+        "work_info_flat": work_info_flat,
+        "partition_indptr": partition_indptr,
+        "reduce_indptr": reduce_indptr,
+        "reduce_final_map": reduce_final_map,
+        "reduce_partial_map": reduce_partial_map,
+        "num_sm": num_sm,
+        "partial_output": partial_output,
+        "partial_lse": partial_lse,
+        "stride_po_partial": query_length * num_query_heads * head_size,
+        "stride_pl_partial": query_length * num_query_heads,
+        "stride_po_ql": num_query_heads * head_size,
+        "stride_pl_ql": num_query_heads,
+        "query_length": query_length,
+    }
+
+
+def softmax_scale_for(head_dim: int = HEAD_DIM) -> float:
+    return 1.0 / math.sqrt(head_dim)

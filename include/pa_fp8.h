@@ -1,0 +1,172 @@
+/*
+ * pa_fp8.h -- C ABI of libpa_fp8.so, the gfx950 (MI355X) FP8-KV paged-attention
+ * decode library.
+ *
+ * Every entry point takes plain pointers and sizes, launches on the caller's
+ * HIP stream, never allocates, never synchronises and returns a status code
+ * (PA_FP8_OK == 0).  Device pointers are HIP device addresses; strides are in
+ * ELEMENTS of the tensor they describe.
+ *
+ * The reference reaches its kernels through MLIR-generated host stubs,
+ * `_mlir_ciface_<launcher>(void **packed_args)`, that end in
+ * `mgpuLaunchKernel` -> `hipModuleLaunchKernel`
+ * (lib/Runtime/ROCm/FlyRocmRuntimeWrappers.cpp:58-62).  Each entry point below
+ * replaces one such launcher; the citation on each names it.
+ */
+#ifndef PA_FP8_H
+#define PA_FP8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PA_FP8_ABI_VERSION 1
+
+enum pa_fp8_status {
+    PA_FP8_OK = 0,
+    PA_FP8_ERR_NULL_POINTER = 1,     /* a required pointer is NULL            */
+    PA_FP8_ERR_HEAD_DIM = 2,         /* head_dim other than 128               */
+    PA_FP8_ERR_BLOCK_SIZE = 3,       /* block_size not a power of two >= 16   */
+    PA_FP8_ERR_GROUP = 4,            /* query_length * group_size not in 1..64 */
+    PA_FP8_ERR_SHAPE = 5,            /* a size or stride out of range         */
+    PA_FP8_ERR_DTYPE = 6,            /* unsupported query / output dtype      */
+    PA_FP8_ERR_PARTITIONS = 7,       /* max_context_partition_num out of range */
+    PA_FP8_ERR_WORKLIST = 8,         /* metadata buffer too small             */
+    PA_FP8_ERR_HIP = 1000            /* 1000 + hipError_t of a failed launch  */
+};
+
+/* element types of query / output tensors */
+enum pa_fp8_dtype { PA_FP8_BF16 = 0, PA_FP8_F16 = 1, PA_FP8_F32 = 2 };
+
+/*
+ * Split-context decode: one workgroup per (sequence, kv head, partition slot).
+ * Writes the per-slot partials the LSE reduce consumes:
+ *   exp_sums / max_logits  f32  [B, Hkv, P, ql*g]   (sum of exp(logit - max), natural-log max)
+ *   tmp_out                bf16 [B, Hkv, P, ql*g, D] (output normalised by its own exp sum)
+ * Empty slots write (0, -inf, 0).
+ * Slot z covers 256-token partitions [z*pps, min((z+1)*pps, T)), T = ceil(ctx/256),
+ * pps = ceil(T/P) (kernels/pa_decode_fp8.py:2311-2320).  With sliding_window > 0
+ * the partitions start at tile max(ctx-ql-sw, 0)/256 (kernels/pa_decode_swa.py:1359-1368).
+ *
+ * Inputs:
+ *   query          [B*ql, Hq, D] bf16 or f16 (query_dtype)
+ *   key_cache      [nb, Hkv, D/16, bs, 16] fp8 e4m3fn
+ *   value_cache    [nb, Hkv, bs/16, D, 16] fp8 e4m3fn (trans_v layout)
+ *   block_tables   [B, max_blocks] int32; context_lengths [B] int32
+ *   key_scale / value_scale: per-tensor [1] f32, or per-token [nb, Hkv, bs, 1] f32
+ *   (per_token_kv = 1, element = blk*stride_ks_block + h*stride_ks_head + slot)
+ *
+ * Replaces the launcher of `compile_pa_decode_ps` (kernels/pa_decode_fp8.py:2739-2803,
+ * called at :3061-3093) and of `compile_pa_decode_sw` (kernels/pa_decode_swa.py:1195-1724,
+ * called at kernels/pa_decode_fp8.py:2937-2974).
+ */
+typedef struct pa_fp8_decode_args {
+    float *exp_sums;
+    float *max_logits;
+    void *tmp_out;
+    const void *query;
+    const uint8_t *key_cache;
+    const uint8_t *value_cache;
+    const int32_t *block_tables;
+    const int32_t *context_lengths;
+    const float *key_scale;
+    const float *value_scale;
+    int64_t stride_q_seq, stride_q_head;
+    int64_t stride_k_block, stride_k_head;
+    int64_t stride_v_block, stride_v_head;
+    int64_t stride_es_seq, stride_es_head, stride_es_part;
+    int64_t stride_to_seq, stride_to_head, stride_to_part, stride_to_group;
+    int64_t stride_bt_seq;
+    int64_t stride_ks_block, stride_ks_head;
+    int32_t batch_size;
+    int32_t num_kv_heads;
+    int32_t query_group_size;
+    int32_t query_length;
+    int32_t head_dim;
+    int32_t block_size;
+    int32_t num_blocks;          /* physical blocks in the caches (entries are clamped into range) */
+    int32_t max_blocks_per_seq;  /* block_tables.shape[1] */
+    int32_t max_context_partition_num;
+    int32_t sliding_window;      /* 0 = off */
+    int32_t per_token_kv;        /* 0 = per-tensor scales, 1 = per-token */
+    int32_t query_dtype;         /* PA_FP8_BF16 or PA_FP8_F16 */
+    float softmax_scale;
+    int32_t reserved;
+} pa_fp8_decode_args;
+
+int pa_fp8_decode_partitions(const pa_fp8_decode_args *args, void *hip_stream);
+
+/*
+ * Log-sum-exp reduce of the partials into the final output
+ *   out[b, qi, h, gi, d] = sum_z w_z * tmp_out[b, h, z, qi*g+gi, d],
+ *   w_z = s_z e^(m_z - M) / sum_z s_z e^(m_z - M),  M = max_z m_z
+ * Output dtype bf16 / f16 / f32 (out_dtype); strides describe the 5-D view
+ * [B, ql, Hkv, g, D] of the [B*ql, Hq, D] output.
+ *
+ * Replaces the launcher of `compile_pa_decode_sw_reduce`
+ * (kernels/pa_decode_swa.py:1132-1183, called at kernels/pa_decode_fp8.py:3094-3120).
+ */
+typedef struct pa_fp8_reduce_args {
+    void *output;
+    const float *exp_sums;
+    const float *max_logits;
+    const void *tmp_out;
+    int64_t stride_o_seq, stride_o_len, stride_o_head, stride_o_group;
+    int64_t stride_es_seq, stride_es_head, stride_es_part;
+    int64_t stride_to_seq, stride_to_head, stride_to_part, stride_to_group;
+    int32_t batch_size;
+    int32_t num_kv_heads;
+    int32_t query_group_size;
+    int32_t query_length;
+    int32_t head_dim;
+    int32_t max_context_partition_num;
+    int32_t out_dtype;           /* PA_FP8_BF16, PA_FP8_F16 or PA_FP8_F32 */
+    int32_t reserved;
+} pa_fp8_reduce_args;
+
+int pa_fp8_lse_reduce(const pa_fp8_reduce_args *args, void *hip_stream);
+
+/*
+ * get_pa_metadata_v1 worklist scheduler, run on the device by one thread
+ * (the reference also runs it serially on one wave).  Writes work_indptr
+ * [num_cu+1], work_info [max_work, 8], reduce_indptr [B+1],
+ * reduce_final_map [B, 2], reduce_partial_map [max_split_tiles]; only the
+ * valid prefixes are defined.  kv_granularity must be a power of two and
+ * num_cu a multiple of num_heads_k.
+ *
+ * Replaces the launcher of `compile_pa_metadata_v1` (kernels/pa_metadata.py:422-447,
+ * called from get_pa_metadata_v1 at :515-524).
+ */
+typedef struct pa_fp8_metadata_args {
+    const int32_t *seqlens_qo_indptr;
+    const int32_t *context_lens;
+    int32_t *work_indptr;
+    int32_t *work_info;
+    int32_t *reduce_indptr;
+    int32_t *reduce_final_map;
+    int32_t *reduce_partial_map;
+    int32_t num_batches;
+    int32_t gqa;
+    int32_t num_heads_k;
+    int32_t num_cu;
+    int32_t kv_granularity;
+    int32_t query_length;
+    int32_t max_work;
+    int32_t max_split_tiles;
+} pa_fp8_metadata_args;
+
+int pa_fp8_metadata_v1(const pa_fp8_metadata_args *args, void *hip_stream);
+
+/* Human-readable text of a status code (static storage). */
+const char *pa_fp8_status_string(int status);
+
+/* PA_FP8_ABI_VERSION of the built library. */
+int pa_fp8_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PA_FP8_H */

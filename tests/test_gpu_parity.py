@@ -1,0 +1,76 @@
+"""GPU parity: the HIP decode path vs the CPU oracle on identical seeded inputs.
+
+Tolerance is the north-star contract: bf16 outputs within atol 2e-2 / rtol 2e-2
+of the oracle (restatement of the reference's torch path), partition indexing
+exact (see pa_testlib.check_partials).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from flydsl_amd.workloads import CONFIGS, build_workload, scaled
+from tests.pa_testlib import check_partials, compare_outputs, launch
+
+pytestmark = pytest.mark.gpu
+
+
+def _spread(n: int, k: int):
+    if n <= k:
+        return list(range(n))
+    return sorted({round(i * (n - 1) / (k - 1)) for i in range(k)})
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
+def test_baseline_config_outputs(name):
+    """Every benchmark configuration at full size; oracle on a spread of sequences."""
+    cfg = CONFIGS[name]
+    print(f"[parity] {name}: {cfg.description}", flush=True)
+    w = build_workload(cfg, "cuda")
+    out, tag, _ = launch(w)
+    assert tag == ("ps_sw_partitioned" if cfg.sliding_window else "ps_small_block")
+    worst = compare_outputs(w, out, _spread(cfg.batch, 6))
+    print(f"[parity] {name}: max |diff| {worst:.3e}", flush=True)
+
+
+SMALL_CASES = {
+    "bs16_pt_g4": dict(base="c2", batch=5, ctx_kind="uniform", ctx_a=1, ctx_b=3000),
+    "bs16_tok_g4": dict(base="c3", batch=6, ctx_kind="uniform", ctx_a=1, ctx_b=3000),
+    "bs64_tok_mtp4_g16": dict(base="c5", batch=3, ctx_kind="uniform", ctx_a=4, ctx_b=1500),
+    "sw_small": dict(base="c4", batch=4, sliding_window=300, ctx_kind="uniform", ctx_a=1, ctx_b=2000),
+    "sw_mtp": dict(base="c4", batch=4, sliding_window=100, query_length=3, ctx_kind="uniform", ctx_a=3, ctx_b=900),
+    "ql2_g8_bs32": dict(base="c2", batch=3, num_q_heads=16, num_kv_heads=2, block_size=32, query_length=2,
+                        ctx_kind="uniform", ctx_a=2, ctx_b=1200),
+    "g1_bs128": dict(base="c2", batch=3, num_q_heads=4, num_kv_heads=4, block_size=128, ctx_kind="uniform",
+                     ctx_a=1, ctx_b=900),
+    "bs1024_tok": dict(base="c3", batch=3, block_size=1024, ctx_kind="uniform", ctx_a=1, ctx_b=2100),
+}
+
+
+@pytest.mark.parametrize("case", sorted(SMALL_CASES))
+@pytest.mark.parametrize("max_parts", [1, 3, 8])
+def test_small_cases_with_partials(case, max_parts):
+    """Ragged small shapes, every sequence and every partition slot checked."""
+    kw = dict(SMALL_CASES[case])
+    cfg = scaled(CONFIGS[kw.pop("base")], name=case, **kw)
+    print(f"[parity] {case} P={max_parts}", flush=True)
+    w = build_workload(cfg, "cuda", seed=7)
+    out, _, partials = launch(w, max_parts=max_parts, with_partials=True)
+    compare_outputs(w, out, range(cfg.batch))
+    check_partials(w, partials, max_parts, range(cfg.batch))
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+def test_output_dtypes(out_dtype):
+    cfg = scaled(CONFIGS["c2"], name="odt", batch=3, ctx_kind="uniform", ctx_a=5, ctx_b=700)
+    w = build_workload(cfg, "cuda", seed=3)
+    out, _, _ = launch(w, out_dtype=out_dtype)
+    compare_outputs(w, out, range(cfg.batch))
+
+
+def test_f16_query():
+    cfg = scaled(CONFIGS["c3"], name="f16q", batch=3, ctx_kind="uniform", ctx_a=5, ctx_b=700)
+    w = build_workload(cfg, "cuda", seed=5)
+    out, _, _ = launch(w, query=w["query"].to(torch.float16))
+    compare_outputs(w, out, range(cfg.batch))
