@@ -79,20 +79,19 @@ __device__ __forceinline__ bf16x8 pack_bf16x8(f32x4 a, f32x4 b) {
     return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-template <bool PER_TOKEN>
-struct StepData {
-    uint4 k[4][2];  // [tile][chunk] 16 fp8 each
-    uint4 v[8];     // [dim tile]    16 fp8 each (16 tokens of one head dim)
-    f32x4 ks[4];    // per-token K scales of the lane's 16 tokens
-    f32x4 vs[4];
-};
-
-template <int MTP, bool PER_TOKEN, int NW>
-__global__ __launch_bounds__(NW * 64) void pa_decode_partition_kernel(const DecodeParams p) {
+// Rows: a workgroup has NW = RS * NS waves.  Wave w owns query-row groups
+// [rs*MTPW, (rs+1)*MTPW) (rs = w % RS, 16 rows per group) and the steps
+// ns, ns+NS, ... of the slot (ns = w / RS).  Waves of the same rs merge their
+// online-softmax states through LDS at the end.
+template <int MTPW, int RS, int NS, bool PER_TOKEN>
+__global__ __launch_bounds__(RS * NS * 64) void pa_decode_partition_kernel(const DecodeParams p) {
     constexpr int D = kHeadDim;
+    constexpr int NW = RS * NS;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rs = wave % RS;
+    const int ns = wave / RS;
     const int l16 = lane & 15;
     const int kg = lane >> 4;
     const int b = blockIdx.x;
@@ -133,12 +132,14 @@ __global__ __launch_bounds__(NW * 64) void pa_decode_partition_kernel(const Deco
         return;
     }
 
-    // ---- query operands (B of the QK MFMA): lane (qrow l16, kg) holds dims 32kg..32kg+31
-    bf16x8 qop[MTP][4];
-    int lo_n[MTP], hi_n[MTP];
+    // ---- query operands (B of the QK MFMA): lane (qrow l16, kg) holds dims 32kg..32kg+31.
+    // Keys visible to a row: [lo_n, hi_n) (causal bound ctx+1-ql+qi, window start ctx-ql-sw+qi).
+    bf16x8 qop[MTPW][4];
+    int lo_n[MTPW], hi_n[MTPW];
+    int lo_max = tok_lo, hi_min = tok_hi;  // wave-uniform bounds over the wave's live rows
 #pragma unroll
-    for (int mg = 0; mg < MTP; ++mg) {
-        const int n = mg * 16 + l16;
+    for (int mg = 0; mg < MTPW; ++mg) {
+        const int n = (rs * MTPW + mg) * 16 + l16;
         if (n < p.eqgs) {
             const int qi = n / p.g;
             const int gi = n - qi * p.g;
@@ -151,18 +152,28 @@ __global__ __launch_bounds__(NW * 64) void pa_decode_partition_kernel(const Deco
         } else {
 #pragma unroll
             for (int s = 0; s < 4; ++s) qop[mg][s] = bf16x8{};
-            hi_n[mg] = 0;
-            lo_n[mg] = 0;
+            hi_n[mg] = tok_hi;  // padded rows: any finite value, never stored
+            lo_n[mg] = tok_lo;
         }
+        lo_max = max(lo_max, lo_n[mg]);
+        hi_min = min(hi_min, hi_n[mg]);
     }
+    // the min / max over the 16 rows of a group: rows differ only through qi
+    for (int sh = 1; sh < 16; sh <<= 1) {
+        lo_max = max(lo_max, __shfl_xor(lo_max, sh, 64));
+        hi_min = min(hi_min, __shfl_xor(hi_min, sh, 64));
+    }
+    lo_max = __builtin_amdgcn_readfirstlane(lo_max);
+    hi_min = __builtin_amdgcn_readfirstlane(hi_min);
+
     const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
     const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
 
     // ---- per-lane running state
-    float m_run[MTP], l_run[MTP];
-    f32x4 o[MTP][8];
+    float m_run[MTPW], l_run[MTPW];
+    f32x4 o[MTPW][8];
 #pragma unroll
-    for (int mg = 0; mg < MTP; ++mg) {
+    for (int mg = 0; mg < MTPW; ++mg) {
         m_run[mg] = -INFINITY;
         l_run[mg] = 0.0f;
 #pragma unroll
@@ -179,49 +190,75 @@ __global__ __launch_bounds__(NW * 64) void pa_decode_partition_kernel(const Deco
     const int k_lane_off = (l16 & 3) * 16 + (2 * kg) * kchunk;
     const int v_lane_off = l16 * 16;
 
-    auto group_loc = [&](int gstart, int &phys, int &sub) {
-        const int gs = min(gstart, last_group);
+    // lane's K group (QK row owner) is l16>>2, its V / scale group is kg
+    auto k_ptr = [&](int step) {
+        const int gs = min(tok_lo + step * kStep + 16 * (l16 >> 2), last_group);
         const int e = bt_row[gs >> p.bs_log2];
-        phys = min(max(e, 0), p.num_blocks - 1);
-        sub = (gs & (bs - 1)) >> 4;
+        const int phys = min(max(e, 0), p.num_blocks - 1);
+        return kc_h + (int64_t)phys * p.s_k_block + ((gs & (bs - 1)) >> 4) * 256 + k_lane_off;
+    };
+    auto v_loc = [&](int step, int64_t &vofs, int64_t &sofs) {
+        const int gs = min(tok_lo + step * kStep + 16 * kg, last_group);
+        const int e = bt_row[gs >> p.bs_log2];
+        const int phys = min(max(e, 0), p.num_blocks - 1);
+        const int sub = (gs & (bs - 1)) >> 4;
+        vofs = (int64_t)phys * p.s_v_block + sub * (D * 16) + v_lane_off;
+        sofs = (int64_t)phys * p.s_ks_block + (int64_t)h * p.s_ks_head + sub * 16;
     };
 
-    auto load_step = [&](int step, StepData<PER_TOKEN> &sd) {
+    uint4 kr[4][2];  // K of the step: [tile][chunk], 16 fp8 each
+    uint4 vr[8];     // V of the step: [dim tile], 16 tokens of one head dim
+    f32x4 ksr[4], vsr[4];
+    auto load_k = [&](const uint8_t *kb) {
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            kr[jt][0] = ld16(kb + jt * 64);
+            kr[jt][1] = ld16(kb + kchunk + jt * 64);
+        }
+    };
+    auto load_v = [&](int64_t vofs) {
+#pragma unroll
+        for (int m = 0; m < 8; ++m) vr[m] = ld16(vc_h + vofs + m * 256);
+    };
+    auto load_scales = [&](int64_t sofs) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            ksr[q4] = *reinterpret_cast<const f32x4 *>(p.ks + sofs + 4 * q4);
+            vsr[q4] = *reinterpret_cast<const f32x4 *>(p.vs + sofs + 4 * q4);
+        }
+    };
+
+    int step = ns;
+    if (step < nsteps) {
+        int64_t vofs, sofs;
+        v_loc(step, vofs, sofs);
+        load_k(k_ptr(step));
+        if constexpr (PER_TOKEN) load_scales(sofs);
+        load_v(vofs);
+    }
+    while (step < nsteps) {
+        const int nxt = step + NS;
+        const bool has_nxt = nxt < nsteps;
+        const uint8_t *nkb = nullptr;
+        int64_t nvofs = 0, nsofs = 0;
+        if (has_nxt) {
+            nkb = k_ptr(nxt);
+            v_loc(nxt, nvofs, nsofs);
+        }
         const int t0 = tok_lo + step * kStep;
-        int pk, sk;
-        group_loc(t0 + 16 * (l16 >> 2), pk, sk);
-        const uint8_t *kb = kc_h + (int64_t)pk * p.s_k_block + sk * 256 + k_lane_off;
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-            sd.k[jt][0] = ld16(kb + jt * 64);
-            sd.k[jt][1] = ld16(kb + kchunk + jt * 64);
-        }
-        int pv, sv;
-        group_loc(t0 + 16 * kg, pv, sv);
-        const uint8_t *vb = vc_h + (int64_t)pv * p.s_v_block + sv * (D * 16) + v_lane_off;
-#pragma unroll
-        for (int m = 0; m < 8; ++m) sd.v[m] = ld16(vb + m * 256);
-        if constexpr (PER_TOKEN) {
-            const int64_t so = (int64_t)pv * p.s_ks_block + (int64_t)h * p.s_ks_head + sv * 16;
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                sd.ks[q4] = *reinterpret_cast<const f32x4 *>(p.ks + so + 4 * q4);
-                sd.vs[q4] = *reinterpret_cast<const f32x4 *>(p.vs + so + 4 * q4);
-            }
-        }
-    };
+        const int trow = t0 + 16 * kg;  // token of (tile jt, i) = trow + 4jt + i
+        const bool interior = t0 >= lo_max && t0 + kStep <= hi_min;
 
-    auto compute_step = [&](int step, const StepData<PER_TOKEN> &sd) {
-        const int trow = tok_lo + step * kStep + 16 * kg;  // token of (tile jt, i) = trow + 4jt + i
-        f32x4 sc[MTP][4];
+        // QK: S[token][qrow] for 4 tiles of 16 tokens
+        f32x4 sc[MTPW][4];
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
-            const bf16x8 a0 = fp8x8_to_bf16x8(sd.k[jt][0].x, sd.k[jt][0].y);
-            const bf16x8 a1 = fp8x8_to_bf16x8(sd.k[jt][0].z, sd.k[jt][0].w);
-            const bf16x8 a2 = fp8x8_to_bf16x8(sd.k[jt][1].x, sd.k[jt][1].y);
-            const bf16x8 a3 = fp8x8_to_bf16x8(sd.k[jt][1].z, sd.k[jt][1].w);
+            const bf16x8 a0 = fp8x8_to_bf16x8(kr[jt][0].x, kr[jt][0].y);
+            const bf16x8 a1 = fp8x8_to_bf16x8(kr[jt][0].z, kr[jt][0].w);
+            const bf16x8 a2 = fp8x8_to_bf16x8(kr[jt][1].x, kr[jt][1].y);
+            const bf16x8 a3 = fp8x8_to_bf16x8(kr[jt][1].z, kr[jt][1].w);
 #pragma unroll
-            for (int mg = 0; mg < MTP; ++mg) {
+            for (int mg = 0; mg < MTPW; ++mg) {
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
                 acc = mfma_bf16(a0, qop[mg][0], acc);
                 acc = mfma_bf16(a1, qop[mg][1], acc);
@@ -230,20 +267,34 @@ __global__ __launch_bounds__(NW * 64) void pa_decode_partition_kernel(const Deco
                 sc[mg][jt] = acc;
             }
         }
-        bf16x8 pop[MTP][2];
+        if (has_nxt) load_k(nkb);  // K registers are free again
+
+        f32x4 kf[4];
 #pragma unroll
-        for (int mg = 0; mg < MTP; ++mg) {
+        for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr[jt] * k_fac : f32x4{k_fac, k_fac, k_fac, k_fac};
+        f32x4 vsc[4];
+        if constexpr (PER_TOKEN) {
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) vsc[jt] = vsr[jt];
+            if (has_nxt) load_scales(nsofs);
+        }
+
+        bf16x8 pop[MTPW][2];
+#pragma unroll
+        for (int mg = 0; mg < MTPW; ++mg) {
             float mx = -INFINITY;
 #pragma unroll
             for (int jt = 0; jt < 4; ++jt) {
+                sc[mg][jt] *= kf[jt];
+                if (!interior) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int t = trow + 4 * jt + i;
-                    float s = sc[mg][jt][i] * (PER_TOKEN ? k_fac * sd.ks[jt][i] : k_fac);
-                    s = (t >= lo_n[mg] && t < hi_n[mg]) ? s : -INFINITY;
-                    sc[mg][jt][i] = s;
-                    mx = fmaxf(mx, s);
+                    for (int i = 0; i < 4; ++i) {
+                        const int t = trow + 4 * jt + i;
+                        sc[mg][jt][i] = (t >= lo_n[mg] && t < hi_n[mg]) ? sc[mg][jt][i] : -INFINITY;
+                    }
                 }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[mg][jt][i]);
             }
             mx = fmaxf(mx, shfl_xor_f(mx, 16));
             mx = fmaxf(mx, shfl_xor_f(mx, 32));
@@ -256,11 +307,11 @@ __global__ __launch_bounds__(NW * 64) void pa_decode_partition_kernel(const Deco
             for (int jt = 0; jt < 4; ++jt) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    float pv = fast_exp2(sc[mg][jt][i] - m_use);
+                    const float pv = fast_exp2(sc[mg][jt][i] - m_use);
                     psum += pv;
-                    if constexpr (PER_TOKEN) pv *= sd.vs[jt][i];
                     sc[mg][jt][i] = pv;
                 }
+                if constexpr (PER_TOKEN) sc[mg][jt] *= vsc[jt];
             }
             l_run[mg] = l_run[mg] * alpha + psum;
 #pragma unroll
@@ -268,44 +319,35 @@ __global__ __launch_bounds__(NW * 64) void pa_decode_partition_kernel(const Deco
             pop[mg][0] = pack_bf16x8(sc[mg][0], sc[mg][1]);
             pop[mg][1] = pack_bf16x8(sc[mg][2], sc[mg][3]);
         }
+
+        // PV: O[dim][qrow] += V^T P^T over the step's 64 tokens
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-            const bf16x8 v0 = fp8x8_to_bf16x8(sd.v[m].x, sd.v[m].y);
-            const bf16x8 v1 = fp8x8_to_bf16x8(sd.v[m].z, sd.v[m].w);
+            const bf16x8 v0 = fp8x8_to_bf16x8(vr[m].x, vr[m].y);
+            const bf16x8 v1 = fp8x8_to_bf16x8(vr[m].z, vr[m].w);
 #pragma unroll
-            for (int mg = 0; mg < MTP; ++mg) {
+            for (int mg = 0; mg < MTPW; ++mg) {
                 o[mg][m] = mfma_bf16(v0, pop[mg][0], o[mg][m]);
                 o[mg][m] = mfma_bf16(v1, pop[mg][1], o[mg][m]);
             }
         }
-    };
-
-    // ---- main loop: prefetch step s+NW while computing step s
-    int step = wave;
-    StepData<PER_TOKEN> cur;
-    if (step < nsteps) load_step(step, cur);
-    while (step < nsteps) {
-        const int nxt_step = step + NW;
-        StepData<PER_TOKEN> nxt;
-        if (nxt_step < nsteps) load_step(nxt_step, nxt);
-        compute_step(step, cur);
-        cur = nxt;
-        step = nxt_step;
+        if (has_nxt) load_v(nvofs);  // V registers are free again
+        step = nxt;
     }
 
     // ---- finish: sum the four kg-lane partial exp sums of each query row
 #pragma unroll
-    for (int mg = 0; mg < MTP; ++mg) {
+    for (int mg = 0; mg < MTPW; ++mg) {
         float lt = l_run[mg];
         lt += shfl_xor_f(lt, 16);
         lt += shfl_xor_f(lt, 32);
         l_run[mg] = lt;
     }
 
-    if constexpr (NW == 1) {
+    if constexpr (NS == 1) {
 #pragma unroll
-        for (int mg = 0; mg < MTP; ++mg) {
-            const int r = mg * 16 + l16;
+        for (int mg = 0; mg < MTPW; ++mg) {
+            const int r = (rs * MTPW + mg) * 16 + l16;
             if (r < p.eqgs) {
                 const float L = l_run[mg];
                 const float inv = L > 0.f ? v_fac / L : 0.f;
@@ -328,12 +370,14 @@ __global__ __launch_bounds__(NW * 64) void pa_decode_partition_kernel(const Deco
         __shared__ float s_o[NW][16][DP];
         __shared__ float s_m[NW][16];
         __shared__ float s_l[NW][16];
-        constexpr int E = 16 * D / (NW * 64);  // outputs per thread in the merge
+        // merge: RS*16 rows x D outputs per pass, E per thread
+        constexpr int E = RS * 16 * D / (NW * 64);
         const int flat = tid * E;
-        const int n = flat / D;
+        const int mrs = flat / (16 * D);  // row split this thread merges
+        const int n = (flat / D) % 16;
         const int d0 = flat % D;
 #pragma unroll
-        for (int mg = 0; mg < MTP; ++mg) {
+        for (int mg = 0; mg < MTPW; ++mg) {
 #pragma unroll
             for (int m = 0; m < 8; ++m) *reinterpret_cast<f32x4 *>(&s_o[wave][l16][16 * m + 4 * kg]) = o[mg][m];
             if (kg == 0) {
@@ -343,30 +387,30 @@ __global__ __launch_bounds__(NW * 64) void pa_decode_partition_kernel(const Deco
             __syncthreads();
             float M = -INFINITY;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][n]);
+            for (int j = 0; j < NS; ++j) M = fmaxf(M, s_m[j * RS + mrs][n]);
             const float Ms = M == -INFINITY ? 0.0f : M;
-            float f[NW];
+            float f[NS];
             float L = 0.f;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                f[w] = fast_exp2(s_m[w][n] - Ms);
-                L += s_l[w][n] * f[w];
+            for (int j = 0; j < NS; ++j) {
+                f[j] = fast_exp2(s_m[j * RS + mrs][n] - Ms);
+                L += s_l[j * RS + mrs][n] * f[j];
             }
             const float inv = L > 0.f ? v_fac / L : 0.f;
-            const int r = mg * 16 + n;
+            const int r = (mrs * MTPW + mg) * 16 + n;
             if (r < p.eqgs) {
 #pragma unroll
                 for (int e0 = 0; e0 < E; e0 += 8) {
                     uint32_t pk[4];
 #pragma unroll
-                    for (int j = 0; j < 8; j += 2) {
+                    for (int j2 = 0; j2 < 8; j2 += 2) {
                         float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-                        for (int w = 0; w < NW; ++w) {
-                            a0 += s_o[w][n][d0 + e0 + j] * f[w];
-                            a1 += s_o[w][n][d0 + e0 + j + 1] * f[w];
+                        for (int j = 0; j < NS; ++j) {
+                            a0 += s_o[j * RS + mrs][n][d0 + e0 + j2] * f[j];
+                            a1 += s_o[j * RS + mrs][n][d0 + e0 + j2 + 1] * f[j];
                         }
-                        pk[j / 2] = uint32_t(f32_to_bf16_bits(a0 * inv)) | (uint32_t(f32_to_bf16_bits(a1 * inv)) << 16);
+                        pk[j2 / 2] = uint32_t(f32_to_bf16_bits(a0 * inv)) | (uint32_t(f32_to_bf16_bits(a1 * inv)) << 16);
                     }
                     *reinterpret_cast<uint4 *>(to + r * p.s_to_group + d0 + e0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
                 }
@@ -428,12 +472,23 @@ __global__ __launch_bounds__(64) void pa_lse_reduce_kernel(const ReduceParams p)
     }
 }
 
-constexpr int kWaves = 4;
-
-template <int MTP, bool PT>
+template <int MTPW, int RS, int NS, bool PT>
 hipError_t launch_decode(const DecodeParams &p, dim3 grid, hipStream_t s) {
-    hipLaunchKernelGGL((pa_decode_partition_kernel<MTP, PT, kWaves>), grid, dim3(kWaves * 64), 0, s, p);
+    hipLaunchKernelGGL((pa_decode_partition_kernel<MTPW, RS, NS, PT>), grid, dim3(RS * NS * 64), 0, s, p);
     return hipGetLastError();
+}
+
+// Wave layout per number of 16-row query groups (ql * group_size / 16, rounded up):
+// one group -> 4 waves split the steps; more groups -> one wave per group (the
+// waves of a workgroup stream the same K/V, which the L2 serves after the first).
+template <bool PT>
+hipError_t dispatch_decode(const DecodeParams &p, int mtp, dim3 grid, hipStream_t s) {
+    switch (mtp) {
+    case 1: return launch_decode<1, 1, 4, PT>(p, grid, s);
+    case 2: return launch_decode<1, 2, 2, PT>(p, grid, s);
+    case 3: return launch_decode<1, 3, 1, PT>(p, grid, s);
+    default: return launch_decode<1, 4, 1, PT>(p, grid, s);
+    }
 }
 
 bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
@@ -537,18 +592,7 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
     const dim3 grid(a->batch_size, a->num_kv_heads, a->max_context_partition_num);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int mtp = (eqgs + 15) / 16;
-    hipError_t err;
-    const bool pt = a->per_token_kv != 0;
-    switch (mtp * 2 + (pt ? 1 : 0)) {
-    case 2: err = launch_decode<1, false>(p, grid, s); break;
-    case 3: err = launch_decode<1, true>(p, grid, s); break;
-    case 4: err = launch_decode<2, false>(p, grid, s); break;
-    case 5: err = launch_decode<2, true>(p, grid, s); break;
-    case 6: err = launch_decode<3, false>(p, grid, s); break;
-    case 7: err = launch_decode<3, true>(p, grid, s); break;
-    case 8: err = launch_decode<4, false>(p, grid, s); break;
-    default: err = launch_decode<4, true>(p, grid, s); break;
-    }
+    const hipError_t err = a->per_token_kv ? dispatch_decode<true>(p, mtp, grid, s) : dispatch_decode<false>(p, mtp, grid, s);
     return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
 }
 

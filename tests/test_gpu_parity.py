@@ -45,6 +45,12 @@ SMALL_CASES = {
     "g1_bs128": dict(base="c2", batch=3, num_q_heads=4, num_kv_heads=4, block_size=128, ctx_kind="uniform",
                      ctx_a=1, ctx_b=900),
     "bs1024_tok": dict(base="c3", batch=3, block_size=1024, ctx_kind="uniform", ctx_a=1, ctx_b=2100),
+    "mtp2_pt": dict(base="c2", batch=3, num_q_heads=16, num_kv_heads=2, query_length=4, ctx_kind="uniform",
+                    ctx_a=4, ctx_b=1500),
+    "mtp2_tok": dict(base="c3", batch=3, num_q_heads=16, num_kv_heads=2, query_length=4, ctx_kind="uniform",
+                     ctx_a=4, ctx_b=1500),
+    "mtp3_tok": dict(base="c5", batch=3, query_length=3, ctx_kind="uniform", ctx_a=3, ctx_b=1500),
+    "mtp4_pt": dict(base="c5", batch=3, per_token=False, ctx_kind="uniform", ctx_a=4, ctx_b=1500),
 }
 
 
