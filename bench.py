@@ -1,0 +1,263 @@
+#!/usr/bin/env python3
+"""Headline benchmark: KV-read HBM GB/s (% of the 8 TB/s peak) and us per decode
+step of the Llama-3-8B-shaped fp8 paged decode on one MI355X.
+
+A step is one ``pa_decode_ps_launch`` over the whole batch (partition kernel +
+log-sum-exp reduce), inputs resident in HBM.  ``--copies`` KV caches are
+rotated step to step so the working set (>= 1.5 GiB for c2) defeats the
+256 MB Infinity Cache.  Prints ONE JSON line.
+
+  value          = algorithmic fp8 K+V bytes per step / us per step (GB/s)
+  roofline       = partition kernel alone: its algorithmic bytes per launch /
+                   its mean duration from HIP events on the launch stream
+  cpu_baseline   = the numpy oracle (restated reference torch path) timed on a
+                   bounded sample of the same workload on this host, one thread
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "KV-read HBM GB/s (% of peak) + µs/decode step, 8B-shaped fp8 paged decode"
+HBM_PEAK_GBS = 8000.0
+
+
+def _parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--copies", type=int, default=3, help="KV-cache copies rotated across steps")
+    ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
+    ap.add_argument("--max-parts", type=int, default=0, help="max_context_partition_num (0 = recommended)")
+    return ap.parse_args()
+
+
+def _events(torch, n):
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def _partition_kernel_bytes(cfg, ctx, max_parts):
+    """Algorithmic bytes one partition-kernel launch moves: K/V (+ per-token
+    scales), Q, block-table entries, context lengths, and the partials it writes."""
+    from flydsl_amd.workloads import algorithmic_bytes, HEAD_DIM
+
+    qo = cfg.batch * cfg.query_length * cfg.num_q_heads * HEAD_DIM * 2
+    inputs = algorithmic_bytes(cfg, ctx) - qo  # drop the final output: the reduce writes it
+    eqgs = cfg.query_length * cfg.group_size
+    partials = cfg.batch * cfg.num_kv_heads * max_parts * eqgs * (HEAD_DIM * 2 + 8)
+    return inputs + partials
+
+
+def cpu_baseline(w, seconds: float):
+    """Time the oracle (numpy restatement of torch_mha_extend) on this host."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import attention as oatt
+
+    cfg = w["config"]
+    kx = w["key_cache"].cpu().numpy()
+    vt = w["value_cache"].cpu().numpy()
+    ks = w["key_scale"].cpu().numpy()
+    vs = w["value_scale"].cpu().numpy()
+    q = w["query"].float().cpu().numpy()
+    bt = w["block_table_np"]
+    ctx = w["context_list"]
+    ql = cfg.query_length
+    done = kv = 0
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        for b in range(cfg.batch):
+            kf, vf = oatt.gather_sequence(kx, vt, bt[b], ctx[b], ks, vs)
+            oatt.reference_masked_attention(
+                q[b * ql : (b + 1) * ql], kf, vf, 1.0 / math.sqrt(q.shape[-1]), True, cfg.sliding_window
+            )
+            done += 1
+            att = min(ctx[b], cfg.sliding_window + ql) if cfg.sliding_window else ctx[b]
+            kv += att * cfg.num_kv_heads * 2 * q.shape[-1]
+            if time.perf_counter() - t0 > seconds:
+                break
+        dt = time.perf_counter() - t0
+    return {
+        "value": round(kv / dt / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{done} of {cfg.batch} sequences of {cfg.name} (all kv heads), numpy oracle, "
+        f"{dt:.1f} s; {dt / done * cfg.batch * 1e6:.0f} us per full step extrapolated; "
+        f"host {platform.processor() or platform.machine()}, {os.cpu_count()} logical CPUs",
+    }
+
+
+def main():
+    args = _parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(
+            f"bench.py measures one GPU only: the decode path runs on a single MI355X here "
+            f"(requested --gpus {args.gpus}, WORLD_SIZE {world}); multi-GPU sharding is design-only.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import torch
+
+    from flydsl_amd import pa_decode_ps_launch
+    from flydsl_amd import _lib
+    from flydsl_amd.pa_decode_fp8 import _PLAN_CACHE, get_recommended_splits
+    from flydsl_amd.workloads import CONFIGS, build_workload, kv_bytes
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    print(f"[bench] building {cfg.name} x{args.copies}: {cfg.description}", file=sys.stderr, flush=True)
+    works = [build_workload(cfg, dev, seed=123 + i * 1000, context_lengths=None) for i in range(args.copies)]
+    # every copy shares the first copy's context lengths / block tables / query
+    base = works[0]
+    for w in works[1:]:
+        w["context_lengths"], w["block_tables"], w["query"] = base["context_lengths"], base["block_tables"], base["query"]
+        w["context_list"], w["block_table_np"] = base["context_list"], base["block_table_np"]
+    ctx = base["context_list"]
+    if args.max_parts:
+        max_parts = args.max_parts
+    elif cfg.sliding_window:
+        max_parts = get_recommended_splits(cfg.batch, cfg.num_kv_heads, sliding_window=cfg.sliding_window,
+                                           query_length=cfg.query_length)
+    else:
+        max_parts = get_recommended_splits(cfg.batch, cfg.num_kv_heads, split_kv_blocks=max(1, 256 // cfg.block_size))
+    eqgs = cfg.query_length * cfg.group_size
+    shape = (cfg.batch, cfg.num_kv_heads, max_parts, eqgs)
+    es = torch.empty(shape, device=dev)
+    ml = torch.empty(shape, device=dev)
+    to = torch.empty(shape + (128,), device=dev, dtype=torch.bfloat16)
+    out = torch.empty_like(base["query"])
+    scale = 1.0 / math.sqrt(128)
+
+    def step(i):
+        w = works[i % len(works)]
+        return pa_decode_ps_launch(
+            out, w["query"], w["key_cache"], w["value_cache"], w["context_lengths"], None, None, scale,
+            w["key_scale"], w["value_scale"], sliding_window=cfg.sliding_window, block_tables=w["block_tables"],
+            max_context_partition_num=max_parts, exp_sums=es, max_logits=ml, temporary_output=to,
+        )
+
+    for i in range(args.warmup):
+        tag = step(i)
+    torch.cuda.synchronize()
+
+    # ---- headline: K steps through the drop-in launcher
+    e0, e1 = _events(torch, 2)
+    torch.cuda.synchronize()
+    t_host = time.perf_counter()
+    e0.record()
+    for i in range(args.steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    host_s = time.perf_counter() - t_host
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+
+    # ---- per-kernel durations: HIP events around each launch on the launch stream
+    plans = [_PLAN_CACHE[k] for k in list(_PLAN_CACHE.keys())[-len(works):]]
+    handle = torch.cuda.current_stream(dev).cuda_stream
+    evs = _events(torch, 3 * args.steps)
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        p = plans[i % len(plans)]
+        evs[3 * i].record()
+        _lib.decode_partitions(p.dargs, handle)
+        evs[3 * i + 1].record()
+        _lib.lse_reduce(p.rargs, handle)
+        evs[3 * i + 2].record()
+    torch.cuda.synchronize()
+    k_ms = sorted(evs[3 * i].elapsed_time(evs[3 * i + 1]) for i in range(args.steps))
+    r_ms = sorted(evs[3 * i + 1].elapsed_time(evs[3 * i + 2]) for i in range(args.steps))
+    k_mean = sum(k_ms) / len(k_ms)
+    r_mean = sum(r_ms) / len(r_ms)
+
+    kvb = kv_bytes(cfg, ctx)
+    us_step = ms_per_step * 1e3
+    gbs = kvb / (us_step * 1e-6) / 1e9
+    kbytes = _partition_kernel_bytes(cfg, ctx, max_parts)
+    achieved = kbytes / (k_mean * 1e-3) / 1e9
+
+    traffic = None
+    tfile = ROOT / "profiles" / f"pa_decode_partition_kernel_{cfg.name}_traffic.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
+        except Exception:
+            traffic = None
+
+    cpu = None
+    if args.cpu_baseline == "on":
+        print("[bench] cpu baseline (numpy oracle, 1 thread)", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(base, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_step": round(us_step, 2),
+        "pct_of_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{cfg.name}: {cfg.description}",
+            "batch": cfg.batch,
+            "query_length": cfg.query_length,
+            "num_q_heads": cfg.num_q_heads,
+            "num_kv_heads": cfg.num_kv_heads,
+            "head_dim": 128,
+            "block_size": cfg.block_size,
+            "kv_dtype": "fp8_e4m3fn",
+            "scales": "per-token" if cfg.per_token else "per-tensor",
+            "sliding_window": cfg.sliding_window,
+            "max_context_partition_num": max_parts,
+            "kv_bytes_per_step": kvb,
+            "kv_cache_copies_rotated": len(works),
+            "path": tag,
+        },
+        "kernels_us": {
+            "pa_decode_partition_kernel": round(k_mean * 1e3, 2),
+            "pa_decode_partition_kernel_median": round(k_ms[len(k_ms) // 2] * 1e3, 2),
+            "pa_lse_reduce_kernel": round(r_mean * 1e3, 2),
+        },
+        "host_us_per_step": round(host_s / args.steps * 1e6, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "pa_decode_partition_kernel",
+            "algorithmic_bytes_per_launch": kbytes,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

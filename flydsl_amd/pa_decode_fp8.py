@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import functools
 import math
+from collections import OrderedDict
 
 import torch
 
@@ -230,7 +231,34 @@ def _validate_scale(name: str, scale: torch.Tensor, per_token: bool, key_cache: 
         raise ValueError(f"per-tensor `{name}` must hold one value, got {tuple(scale.shape)}")
 
 
-def _run_partitioned(
+class _Plan:
+    """Prepared launch of one decode step: the two C-ABI argument blocks plus the
+    tensors they point into that the launcher allocated itself."""
+
+    __slots__ = ("dargs", "rargs", "tag", "keepalive")
+
+    def __init__(self, dargs, rargs, tag, keepalive):
+        self.dargs, self.rargs, self.tag, self.keepalive = dargs, rargs, tag, keepalive
+
+    def launch(self, stream_handle: int) -> str:
+        _lib.decode_partitions(self.dargs, stream_handle)
+        _lib.lse_reduce(self.rargs, stream_handle)
+        return self.tag
+
+
+_PLAN_CACHE: "OrderedDict[tuple, _Plan]" = OrderedDict()
+_PLAN_CACHE_SIZE = 64
+
+
+def _tkey(t):
+    if t is None:
+        return None
+    if isinstance(t, torch.Tensor):
+        return (t.data_ptr(), tuple(t.shape), t.stride(), t.dtype, t.device)
+    return ("scalar", float(t or 1.0))
+
+
+def _partitioned_plan(
     output,
     query,
     key_cache,
@@ -246,17 +274,17 @@ def _run_partitioned(
     exp_sums,
     max_logits,
     temporary_output,
-    stream,
     is_graph_capturing,
     path_name,
-):
+    tag,
+) -> _Plan:
     dev = query.device
     batch_size = context_lengths.shape[0]
     num_query_heads = query.shape[1]
     num_kv_heads = key_cache.shape[1]
     head_size = query.shape[-1]
     query_group_size = num_query_heads // num_kv_heads
-    query_length = query.shape[0] // batch_size if batch_size else 1
+    query_length = query.shape[0] // batch_size
     eqgs = query_length * query_group_size
     shape = (batch_size, num_kv_heads, max_parts, eqgs)
     if is_graph_capturing and (exp_sums is None or max_logits is None or temporary_output is None):
@@ -273,7 +301,7 @@ def _run_partitioned(
         temporary_output = torch.empty(shape + (head_size,), device=dev, dtype=torch.bfloat16)
     _check_intermediates(exp_sums, max_logits, temporary_output, shape, head_size)
     output_5d = output.view(batch_size, query_length, num_kv_heads, query_group_size, head_size)
-    args = _decode_args(
+    dargs = _decode_args(
         query=query,
         key_cache=_u8(key_cache),
         value_cache=_u8(value_cache),
@@ -291,9 +319,8 @@ def _run_partitioned(
         sliding_window=sliding_window,
         softmax_scale=softmax_scale,
     )
-    _lib.decode_partitions(args, stream)
     rargs = _reduce_args(output_5d, exp_sums, max_logits, temporary_output, max_parts, _get_output_dtype_str(output))
-    _lib.lse_reduce(rargs, stream)
+    return _Plan(dargs, rargs, tag, (exp_sums, max_logits, temporary_output, key_scale, value_scale))
 
 
 def pa_decode_ps_launch(
@@ -324,17 +351,66 @@ def pa_decode_ps_launch(
     other block sizes -> partitioned path over the same kernels (the reference
     routes them to its persistent worklist kernel).  Every path is one
     partition kernel plus the log-sum-exp reduce and writes ``output`` in place.
+    ``kv_page_indices`` / ``kv_indptr`` / ``metadata`` are accepted for
+    signature compatibility; the partition kernels read ``block_tables``.
+
+    A call whose tensors (pointers, shapes, strides, dtypes), scalars and stream
+    all match an earlier call reuses that call's prepared argument blocks (and
+    the intermediates it allocated), so steady-state decode pays two C calls.
 
     Returns the path tag: "ps_sw_partitioned" / "ps_sw_fused_partitioned",
     "ps_small_block" or "ps_partitioned".
     """
+    dev = query.device
+    s = stream if stream is not None else torch.cuda.current_stream(dev)
+    stream_handle = s.cuda_stream if hasattr(s, "cuda_stream") else int(s)
+    is_graph_capturing = _is_current_stream_capturing()
+    key = None
+    if not is_graph_capturing:
+        key = (
+            stream_handle,
+            _tkey(output),
+            _tkey(query),
+            _tkey(key_cache),
+            _tkey(value_cache),
+            _tkey(context_lengths),
+            _tkey(block_tables),
+            _tkey(key_scale),
+            _tkey(value_scale),
+            float(softmax_scale),
+            int(sliding_window),
+            int(max_context_partition_num),
+            _tkey(exp_sums),
+            _tkey(max_logits),
+            _tkey(temporary_output),
+        )
+        plan = _PLAN_CACHE.get(key)
+        if plan is not None:
+            _PLAN_CACHE.move_to_end(key)
+            return plan.launch(stream_handle)
+    plan = _build_plan(
+        output, query, key_cache, value_cache, context_lengths, softmax_scale, key_scale, value_scale,
+        sliding_window, block_tables, max_context_partition_num, exp_sums, max_logits, temporary_output,
+        is_graph_capturing,
+    )
+    if key is not None:
+        _PLAN_CACHE[key] = plan
+        if len(_PLAN_CACHE) > _PLAN_CACHE_SIZE:
+            _PLAN_CACHE.popitem(last=False)
+    return plan.launch(stream_handle)
+
+
+def _build_plan(
+    output, query, key_cache, value_cache, context_lengths, softmax_scale, key_scale, value_scale,
+    sliding_window, block_tables, max_context_partition_num, exp_sums, max_logits, temporary_output,
+    is_graph_capturing,
+) -> _Plan:
     if query.dim() != 3:
         raise ValueError(f"query must be [num_seqs*query_length, num_heads, head_dim], got {tuple(query.shape)}")
     num_query_heads = query.shape[1]
     num_kv_heads = key_cache.shape[1]
     query_input_dtype = _get_query_input_dtype(query)
     dev = query.device
-    is_graph_capturing = _is_current_stream_capturing()
     key_scale = _prepare_scale_tensor("key_scale", key_scale, device=dev, is_graph_capturing=is_graph_capturing)
     value_scale = _prepare_scale_tensor("value_scale", value_scale, device=dev, is_graph_capturing=is_graph_capturing)
     if query_input_dtype == "packed_fp8":
@@ -380,8 +456,6 @@ def pa_decode_ps_launch(
     _check_int32("block_tables", block_tables, 2)
     if block_tables.shape[0] != batch_size or block_tables.stride(1) != 1 or block_tables.device != dev:
         raise ValueError("block_tables must be [num_seqs, max_blocks] on the query device with a unit last stride")
-    s = stream if stream is not None else torch.cuda.current_stream(dev)
-    stream_handle = s.cuda_stream if hasattr(s, "cuda_stream") else int(s)
 
     if sliding_window > 0:
         if max_context_partition_num == 0:
@@ -392,20 +466,20 @@ def pa_decode_ps_launch(
                 context_partition_size=KV_COMPUTE_BLOCK,
                 query_length=query_length,
             )
-        _run_partitioned(output, query, key_cache, value_cache, context_lengths, block_tables, softmax_scale,
-                         key_scale, value_scale, per_token_kv, sliding_window, max_context_partition_num,
-                         exp_sums, max_logits, temporary_output, stream_handle, is_graph_capturing, "sliding-window")
-        return "ps_sw_fused_partitioned" if max_context_partition_num <= 1 else "ps_sw_partitioned"
-
-    if max_context_partition_num == 0:
-        max_context_partition_num = get_recommended_splits(
-            batch_size, num_kv_heads, split_kv_blocks=max(1, KV_COMPUTE_BLOCK // block_size)
-        )
-    path = "small-block PS" if block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES else "partitioned"
-    _run_partitioned(output, query, key_cache, value_cache, context_lengths, block_tables, softmax_scale,
-                     key_scale, value_scale, per_token_kv, 0, max_context_partition_num,
-                     exp_sums, max_logits, temporary_output, stream_handle, is_graph_capturing, path)
-    return "ps_small_block" if block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES else "ps_partitioned"
+        tag = "ps_sw_fused_partitioned" if max_context_partition_num <= 1 else "ps_sw_partitioned"
+        path = "sliding-window"
+    else:
+        if max_context_partition_num == 0:
+            max_context_partition_num = get_recommended_splits(
+                batch_size, num_kv_heads, split_kv_blocks=max(1, KV_COMPUTE_BLOCK // block_size)
+            )
+        small = block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES
+        tag = "ps_small_block" if small else "ps_partitioned"
+        path = "small-block PS" if small else "partitioned"
+        sliding_window = 0
+    return _partitioned_plan(output, query, key_cache, value_cache, context_lengths, block_tables, softmax_scale,
+                             key_scale, value_scale, per_token_kv, sliding_window, max_context_partition_num,
+                             exp_sums, max_logits, temporary_output, is_graph_capturing, path, tag)
 
 
 def get_pa_metadata(
