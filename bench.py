@@ -42,7 +42,7 @@ def _parse():
     ap.add_argument("--copies", type=int, default=3, help="KV-cache copies rotated across steps")
     ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
-    ap.add_argument("--max-parts", type=int, default=0, help="max_context_partition_num (0 = recommended)")
+    ap.add_argument("--max-parts", type=int, default=0, help="max_context_partition_num (0 = launcher default)")
     return ap.parse_args()
 
 
@@ -52,14 +52,17 @@ def _events(torch, n):
 
 def _partition_kernel_bytes(cfg, ctx, max_parts):
     """Algorithmic bytes one partition-kernel launch moves: K/V (+ per-token
-    scales), Q, block-table entries, context lengths, and the partials it writes."""
+    scales), Q, block-table entries, context lengths, and either the output
+    (one slot per sequence: written directly) or the partials the reduce reads."""
     from flydsl_amd.workloads import algorithmic_bytes, HEAD_DIM
 
+    total = algorithmic_bytes(cfg, ctx)
+    if max_parts == 1:
+        return total
     qo = cfg.batch * cfg.query_length * cfg.num_q_heads * HEAD_DIM * 2
-    inputs = algorithmic_bytes(cfg, ctx) - qo  # drop the final output: the reduce writes it
     eqgs = cfg.query_length * cfg.group_size
     partials = cfg.batch * cfg.num_kv_heads * max_parts * eqgs * (HEAD_DIM * 2 + 8)
-    return inputs + partials
+    return total - qo + partials
 
 
 def cpu_baseline(w, seconds: float):
@@ -81,23 +84,24 @@ def cpu_baseline(w, seconds: float):
     done = kv = 0
     with threadpool_limits(1):
         t0 = time.perf_counter()
-        for b in range(cfg.batch):
-            kf, vf = oatt.gather_sequence(kx, vt, bt[b], ctx[b], ks, vs)
-            oatt.reference_masked_attention(
-                q[b * ql : (b + 1) * ql], kf, vf, 1.0 / math.sqrt(q.shape[-1]), True, cfg.sliding_window
-            )
-            done += 1
-            att = min(ctx[b], cfg.sliding_window + ql) if cfg.sliding_window else ctx[b]
-            kv += att * cfg.num_kv_heads * 2 * q.shape[-1]
-            if time.perf_counter() - t0 > seconds:
-                break
+        while time.perf_counter() - t0 < seconds:  # whole passes over the batch until the budget is spent
+            for b in range(cfg.batch):
+                kf, vf = oatt.gather_sequence(kx, vt, bt[b], ctx[b], ks, vs)
+                oatt.reference_masked_attention(
+                    q[b * ql : (b + 1) * ql], kf, vf, 1.0 / math.sqrt(q.shape[-1]), True, cfg.sliding_window
+                )
+                done += 1
+                att = min(ctx[b], cfg.sliding_window + ql) if cfg.sliding_window else ctx[b]
+                kv += att * cfg.num_kv_heads * 2 * q.shape[-1]
+                if time.perf_counter() - t0 > 3 * seconds:
+                    break
         dt = time.perf_counter() - t0
     return {
         "value": round(kv / dt / 1e9, 4),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"{done} of {cfg.batch} sequences of {cfg.name} (all kv heads), numpy oracle, "
+        "sample": f"{done} sequence decodes of {cfg.name} (batch {cfg.batch}, all kv heads), numpy oracle, "
         f"{dt:.1f} s; {dt / done * cfg.batch * 1e6:.0f} us per full step extrapolated; "
         f"host {platform.processor() or platform.machine()}, {os.cpu_count()} logical CPUs",
     }
@@ -118,7 +122,7 @@ def main():
 
     from flydsl_amd import pa_decode_ps_launch
     from flydsl_amd import _lib
-    from flydsl_amd.pa_decode_fp8 import _PLAN_CACHE, get_recommended_splits
+    from flydsl_amd.pa_decode_fp8 import _PLAN_CACHE
     from flydsl_amd.workloads import CONFIGS, build_workload, kv_bytes
 
     cfg = CONFIGS[args.config]
@@ -131,18 +135,8 @@ def main():
         w["context_lengths"], w["block_tables"], w["query"] = base["context_lengths"], base["block_tables"], base["query"]
         w["context_list"], w["block_table_np"] = base["context_list"], base["block_table_np"]
     ctx = base["context_list"]
-    if args.max_parts:
-        max_parts = args.max_parts
-    elif cfg.sliding_window:
-        max_parts = get_recommended_splits(cfg.batch, cfg.num_kv_heads, sliding_window=cfg.sliding_window,
-                                           query_length=cfg.query_length)
-    else:
-        max_parts = get_recommended_splits(cfg.batch, cfg.num_kv_heads, split_kv_blocks=max(1, 256 // cfg.block_size))
-    eqgs = cfg.query_length * cfg.group_size
-    shape = (cfg.batch, cfg.num_kv_heads, max_parts, eqgs)
-    es = torch.empty(shape, device=dev)
-    ml = torch.empty(shape, device=dev)
-    to = torch.empty(shape + (128,), device=dev, dtype=torch.bfloat16)
+    max_parts = args.max_parts  # 0: the launcher's default for this kernel
+    # partials are allocated by the launcher and reused across steps through its plan cache
     out = torch.empty_like(base["query"])
     scale = 1.0 / math.sqrt(128)
 
@@ -151,7 +145,7 @@ def main():
         return pa_decode_ps_launch(
             out, w["query"], w["key_cache"], w["value_cache"], w["context_lengths"], None, None, scale,
             w["key_scale"], w["value_scale"], sliding_window=cfg.sliding_window, block_tables=w["block_tables"],
-            max_context_partition_num=max_parts, exp_sums=es, max_logits=ml, temporary_output=to,
+            max_context_partition_num=max_parts,
         )
 
     for i in range(args.warmup):
@@ -170,8 +164,41 @@ def main():
     host_s = time.perf_counter() - t_host
     ms_per_step = e0.elapsed_time(e1) / args.steps
 
+    # ---- secondary: the reference's default partition count (get_recommended_splits)
+    from flydsl_amd import get_recommended_splits
+
+    ref_parts = (
+        get_recommended_splits(cfg.batch, cfg.num_kv_heads, sliding_window=cfg.sliding_window,
+                               query_length=cfg.query_length)
+        if cfg.sliding_window
+        else get_recommended_splits(cfg.batch, cfg.num_kv_heads, split_kv_blocks=max(1, 256 // cfg.block_size))
+    )
+
+    def ref_step(i):
+        w = works[i % len(works)]
+        return pa_decode_ps_launch(
+            out, w["query"], w["key_cache"], w["value_cache"], w["context_lengths"], None, None, scale,
+            w["key_scale"], w["value_scale"], sliding_window=cfg.sliding_window, block_tables=w["block_tables"],
+            max_context_partition_num=ref_parts,
+        )
+
+    for i in range(args.warmup):
+        ref_step(i)
+    r0, r1 = _events(torch, 2)
+    torch.cuda.synchronize()
+    r0.record()
+    for i in range(args.steps):
+        ref_step(i)
+    r1.record()
+    torch.cuda.synchronize()
+    ref_us = r0.elapsed_time(r1) / args.steps * 1e3
+    for i in range(len(works)):  # the default plans become the newest cache entries again
+        step(i)
+    torch.cuda.synchronize()
+
     # ---- per-kernel durations: HIP events around each launch on the launch stream
     plans = [_PLAN_CACHE[k] for k in list(_PLAN_CACHE.keys())[-len(works):]]
+    max_parts = plans[0].max_parts
     handle = torch.cuda.current_stream(dev).cuda_stream
     evs = _events(torch, 3 * args.steps)
     torch.cuda.synchronize()
@@ -180,13 +207,14 @@ def main():
         evs[3 * i].record()
         _lib.decode_partitions(p.dargs, handle)
         evs[3 * i + 1].record()
-        _lib.lse_reduce(p.rargs, handle)
+        if p.rargs is not None:
+            _lib.lse_reduce(p.rargs, handle)
         evs[3 * i + 2].record()
     torch.cuda.synchronize()
     k_ms = sorted(evs[3 * i].elapsed_time(evs[3 * i + 1]) for i in range(args.steps))
     r_ms = sorted(evs[3 * i + 1].elapsed_time(evs[3 * i + 2]) for i in range(args.steps))
     k_mean = sum(k_ms) / len(k_ms)
-    r_mean = sum(r_ms) / len(r_ms)
+    r_mean = sum(r_ms) / len(r_ms) if plans[0].rargs is not None else 0.0
 
     kvb = kv_bytes(cfg, ctx)
     us_step = ms_per_step * 1e3
@@ -244,6 +272,11 @@ def main():
             "pa_lse_reduce_kernel": round(r_mean * 1e3, 2),
         },
         "host_us_per_step": round(host_s / args.steps * 1e6, 2),
+        "reference_default_partitions": {
+            "max_context_partition_num": ref_parts,
+            "us_per_step": round(ref_us, 2),
+            "kv_gbs": round(kvb / (ref_us * 1e-6) / 1e9, 1),
+        },
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),

@@ -63,7 +63,13 @@ class DecodeArgs(ctypes.Structure):
         ("per_token_kv", _i32),
         ("query_dtype", _i32),
         ("softmax_scale", _f32),
-        ("reserved", _i32),
+        ("direct_output", _i32),
+        ("out_dtype", _i32),
+        ("output", _vp),
+        ("stride_o_seq", _i64),
+        ("stride_o_len", _i64),
+        ("stride_o_head", _i64),
+        ("stride_o_group", _i64),
     ]
 
 

@@ -24,6 +24,8 @@
 #include "pa_common.h"
 #include "pa_fp8.h"
 
+#include <stdlib.h>
+
 using namespace pa;
 
 namespace {
@@ -50,7 +52,48 @@ struct DecodeParams {
     int32_t num_blocks, max_blocks, max_parts, sw;
     int32_t q_f16;
     float qk_scale;  // softmax_scale * log2(e)
+    // direct output (one partition slot): final rows go to out[b, qi, h, gi, :]
+    void *out;
+    int64_t s_o_seq, s_o_len, s_o_head, s_o_group;
+    int32_t out_dtype;
+    int32_t direct;
 };
+
+// n consecutive outputs of row r starting at head dim d0: to the bf16 partial
+// row, or (direct mode) converted to the output dtype at out[b, qi, h, gi, d0].
+template <int N>
+__device__ __forceinline__ void emit_row(const DecodeParams &p, uint16_t *to, int b, int h, int r, int d0,
+                                         const float (&v)[N]) {
+    if (!p.direct) {
+        uint32_t pk[N / 2];
+#pragma unroll
+        for (int j = 0; j < N; j += 2)
+            pk[j / 2] = uint32_t(f32_to_bf16_bits(v[j])) | (uint32_t(f32_to_bf16_bits(v[j + 1])) << 16);
+        uint16_t *dst = to + r * p.s_to_group + d0;
+        if constexpr (N == 8) *reinterpret_cast<uint4 *>(dst) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        else *reinterpret_cast<uint2 *>(dst) = make_uint2(pk[0], pk[1]);
+        return;
+    }
+    const int qi = r / p.g, gi = r - (r / p.g) * p.g;
+    const int64_t off = b * p.s_o_seq + qi * p.s_o_len + h * p.s_o_head + gi * p.s_o_group + d0;
+    if (p.out_dtype == PA_FP8_F32) {
+        float *dst = reinterpret_cast<float *>(p.out) + off;
+#pragma unroll
+        for (int j = 0; j < N; j += 4) *reinterpret_cast<float4 *>(dst + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
+        return;
+    }
+    uint32_t pk[N / 2];
+#pragma unroll
+    for (int j = 0; j < N; j += 2) {
+        if (p.out_dtype == PA_FP8_F16)
+            pk[j / 2] = uint32_t(f32_to_f16_bits(v[j])) | (uint32_t(f32_to_f16_bits(v[j + 1])) << 16);
+        else
+            pk[j / 2] = uint32_t(f32_to_bf16_bits(v[j])) | (uint32_t(f32_to_bf16_bits(v[j + 1])) << 16);
+    }
+    uint16_t *dst = reinterpret_cast<uint16_t *>(p.out) + off;
+    if constexpr (N == 8) *reinterpret_cast<uint4 *>(dst) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    else *reinterpret_cast<uint2 *>(dst) = make_uint2(pk[0], pk[1]);
+}
 
 struct ReduceParams {
     void *out;
@@ -121,14 +164,14 @@ __global__ __launch_bounds__(RS * NS * 64) void pa_decode_partition_kernel(const
     uint16_t *to = p.tmp_out + b * p.s_to_seq + h * p.s_to_head + z * p.s_to_part;
 
     if (tok_lo >= tok_hi) {  // empty slot (kernels/pa_decode_fp8.py:2591-2598)
-        for (int r = tid; r < p.eqgs; r += NW * 64) {
-            es[r] = 0.0f;
-            ml[r] = -INFINITY;
+        if (!p.direct) {
+            for (int r = tid; r < p.eqgs; r += NW * 64) {
+                es[r] = 0.0f;
+                ml[r] = -INFINITY;
+            }
         }
-        for (int i = tid; i < p.eqgs * (D / 8); i += NW * 64) {
-            const int r = i / (D / 8), c = i % (D / 8);
-            *reinterpret_cast<uint4 *>(to + r * p.s_to_group + c * 8) = make_uint4(0, 0, 0, 0);
-        }
+        const float zero8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int i = tid; i < p.eqgs * (D / 8); i += NW * 64) emit_row<8>(p, to, b, h, i / (D / 8), (i % (D / 8)) * 8, zero8);
         return;
     }
 
@@ -354,12 +397,10 @@ __global__ __launch_bounds__(RS * NS * 64) void pa_decode_partition_kernel(const
 #pragma unroll
                 for (int m = 0; m < 8; ++m) {
                     const f32x4 v = o[mg][m] * inv;
-                    uint2 pk;
-                    pk.x = uint32_t(f32_to_bf16_bits(v[0])) | (uint32_t(f32_to_bf16_bits(v[1])) << 16);
-                    pk.y = uint32_t(f32_to_bf16_bits(v[2])) | (uint32_t(f32_to_bf16_bits(v[3])) << 16);
-                    *reinterpret_cast<uint2 *>(to + r * p.s_to_group + 16 * m + 4 * kg) = pk;
+                    const float v4[4] = {v[0], v[1], v[2], v[3]};
+                    emit_row<4>(p, to, b, h, r, 16 * m + 4 * kg, v4);
                 }
-                if (kg == 0) {
+                if (kg == 0 && !p.direct) {
                     es[r] = L;
                     ml[r] = L > 0.f ? m_run[mg] * kLn2 : -INFINITY;
                 }
@@ -401,20 +442,17 @@ __global__ __launch_bounds__(RS * NS * 64) void pa_decode_partition_kernel(const
             if (r < p.eqgs) {
 #pragma unroll
                 for (int e0 = 0; e0 < E; e0 += 8) {
-                    uint32_t pk[4];
+                    float v8[8];
 #pragma unroll
-                    for (int j2 = 0; j2 < 8; j2 += 2) {
-                        float a0 = 0.f, a1 = 0.f;
+                    for (int j2 = 0; j2 < 8; ++j2) {
+                        float a = 0.f;
 #pragma unroll
-                        for (int j = 0; j < NS; ++j) {
-                            a0 += s_o[j * RS + mrs][n][d0 + e0 + j2] * f[j];
-                            a1 += s_o[j * RS + mrs][n][d0 + e0 + j2 + 1] * f[j];
-                        }
-                        pk[j2 / 2] = uint32_t(f32_to_bf16_bits(a0 * inv)) | (uint32_t(f32_to_bf16_bits(a1 * inv)) << 16);
+                        for (int j = 0; j < NS; ++j) a += s_o[j * RS + mrs][n][d0 + e0 + j2] * f[j];
+                        v8[j2] = a * inv;
                     }
-                    *reinterpret_cast<uint4 *>(to + r * p.s_to_group + d0 + e0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+                    emit_row<8>(p, to, b, h, r, d0 + e0, v8);
                 }
-                if (d0 == 0) {
+                if (d0 == 0 && !p.direct) {
                     es[r] = L;
                     ml[r] = L > 0.f ? M * kLn2 : -INFINITY;
                 }
@@ -481,10 +519,25 @@ hipError_t launch_decode(const DecodeParams &p, dim3 grid, hipStream_t s) {
 // Wave layout per number of 16-row query groups (ql * group_size / 16, rounded up):
 // one group -> 4 waves split the steps; more groups -> one wave per group (the
 // waves of a workgroup stream the same K/V, which the L2 serves after the first).
+// Tuning knob: PA_FP8_NS overrides the waves per workgroup of the one-group layout.
+int env_ns() {
+    static const int v = [] {
+        const char *e = getenv("PA_FP8_NS");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
 template <bool PT>
 hipError_t dispatch_decode(const DecodeParams &p, int mtp, dim3 grid, hipStream_t s) {
     switch (mtp) {
-    case 1: return launch_decode<1, 1, 4, PT>(p, grid, s);
+    case 1:
+        switch (env_ns()) {
+        case 1: return launch_decode<1, 1, 1, PT>(p, grid, s);
+        case 2: return launch_decode<1, 1, 2, PT>(p, grid, s);
+        case 8: return launch_decode<1, 1, 8, PT>(p, grid, s);
+        default: return launch_decode<1, 1, 4, PT>(p, grid, s);
+        }
     case 2: return launch_decode<1, 2, 2, PT>(p, grid, s);
     case 3: return launch_decode<1, 3, 1, PT>(p, grid, s);
     default: return launch_decode<1, 4, 1, PT>(p, grid, s);
@@ -535,13 +588,28 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
     if (a->max_context_partition_num < 1 || a->max_context_partition_num > 65535) return PA_FP8_ERR_PARTITIONS;
     if (a->query_dtype != PA_FP8_BF16 && a->query_dtype != PA_FP8_F16) return PA_FP8_ERR_DTYPE;
     if (a->num_kv_heads > 65535 || a->sliding_window < 0) return PA_FP8_ERR_SHAPE;
+    if (a->direct_output) {
+        if (a->max_context_partition_num != 1) return PA_FP8_ERR_PARTITIONS;
+        if (a->out_dtype != PA_FP8_BF16 && a->out_dtype != PA_FP8_F16 && a->out_dtype != PA_FP8_F32)
+            return PA_FP8_ERR_DTYPE;
+    }
     if (a->batch_size == 0) return PA_FP8_OK;
-    if (!a->exp_sums || !a->max_logits || !a->tmp_out || !a->query || !a->key_cache || !a->value_cache ||
-        !a->block_tables || !a->context_lengths || !a->key_scale || !a->value_scale)
+    if (!a->query || !a->key_cache || !a->value_cache || !a->block_tables || !a->context_lengths || !a->key_scale ||
+        !a->value_scale)
         return PA_FP8_ERR_NULL_POINTER;
+    if (a->direct_output) {
+        if (!a->output) return PA_FP8_ERR_NULL_POINTER;
+        const int esz = a->out_dtype == PA_FP8_F32 ? 4 : 2;
+        if ((reinterpret_cast<uintptr_t>(a->output) & 15) ||
+            ((a->stride_o_seq | a->stride_o_len | a->stride_o_head | a->stride_o_group) * esz) & 15)
+            return PA_FP8_ERR_SHAPE;
+    } else if (!a->exp_sums || !a->max_logits || !a->tmp_out) {
+        return PA_FP8_ERR_NULL_POINTER;
+    }
     if (a->num_blocks <= 0 || a->max_blocks_per_seq <= 0) return PA_FP8_ERR_SHAPE;
     // 16-byte vector accesses: caches, query rows and partial rows must be 16-byte aligned
-    if (!aligned16(a->key_cache) || !aligned16(a->value_cache) || !aligned16(a->query) || !aligned16(a->tmp_out))
+    if (!aligned16(a->key_cache) || !aligned16(a->value_cache) || !aligned16(a->query) ||
+        (!a->direct_output && !aligned16(a->tmp_out)))
         return PA_FP8_ERR_SHAPE;
     if ((a->stride_k_block | a->stride_k_head | a->stride_v_block | a->stride_v_head) & 15) return PA_FP8_ERR_SHAPE;
     if ((a->stride_q_seq | a->stride_q_head) & 7) return PA_FP8_ERR_SHAPE;
@@ -588,6 +656,13 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
     p.sw = a->sliding_window;
     p.q_f16 = a->query_dtype == PA_FP8_F16;
     p.qk_scale = a->softmax_scale * kLog2e;
+    p.direct = a->direct_output ? 1 : 0;
+    p.out = a->output;
+    p.s_o_seq = a->stride_o_seq;
+    p.s_o_len = a->stride_o_len;
+    p.s_o_head = a->stride_o_head;
+    p.s_o_group = a->stride_o_group;
+    p.out_dtype = a->out_dtype;
 
     const dim3 grid(a->batch_size, a->num_kv_heads, a->max_context_partition_num);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);

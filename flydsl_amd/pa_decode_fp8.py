@@ -172,9 +172,13 @@ def _decode_args(
     softmax_scale,
 ) -> _lib.DecodeArgs:
     a = _lib.DecodeArgs()
-    a.exp_sums = exp_sums.data_ptr()
-    a.max_logits = max_logits.data_ptr()
-    a.tmp_out = temporary_output.data_ptr()
+    if exp_sums is not None:
+        a.exp_sums = exp_sums.data_ptr()
+        a.max_logits = max_logits.data_ptr()
+        a.tmp_out = temporary_output.data_ptr()
+        a.stride_es_seq, a.stride_es_head, a.stride_es_part = exp_sums.stride(0), exp_sums.stride(1), exp_sums.stride(2)
+        a.stride_to_seq, a.stride_to_head = temporary_output.stride(0), temporary_output.stride(1)
+        a.stride_to_part, a.stride_to_group = temporary_output.stride(2), temporary_output.stride(3)
     a.query = query.data_ptr()
     a.key_cache = key_cache.data_ptr()
     a.value_cache = value_cache.data_ptr()
@@ -185,9 +189,6 @@ def _decode_args(
     a.stride_q_seq, a.stride_q_head = query.stride(0), query.stride(1)
     a.stride_k_block, a.stride_k_head = key_cache.stride(0), key_cache.stride(1)
     a.stride_v_block, a.stride_v_head = value_cache.stride(0), value_cache.stride(1)
-    a.stride_es_seq, a.stride_es_head, a.stride_es_part = exp_sums.stride(0), exp_sums.stride(1), exp_sums.stride(2)
-    a.stride_to_seq, a.stride_to_head = temporary_output.stride(0), temporary_output.stride(1)
-    a.stride_to_part, a.stride_to_group = temporary_output.stride(2), temporary_output.stride(3)
     a.stride_bt_seq = block_tables.stride(0)
     if per_token_kv:
         a.stride_ks_block, a.stride_ks_head = key_scale.stride(0), key_scale.stride(1)
@@ -232,18 +233,37 @@ def _validate_scale(name: str, scale: torch.Tensor, per_token: bool, key_cache: 
 
 
 class _Plan:
-    """Prepared launch of one decode step: the two C-ABI argument blocks plus the
-    tensors they point into that the launcher allocated itself."""
+    """Prepared launch of one decode step: the C-ABI argument blocks plus the
+    tensors they point into that the launcher allocated itself.  ``rargs`` is
+    None when the partition kernel writes the output directly (one slot)."""
 
-    __slots__ = ("dargs", "rargs", "tag", "keepalive")
+    __slots__ = ("dargs", "rargs", "tag", "keepalive", "max_parts")
 
-    def __init__(self, dargs, rargs, tag, keepalive):
-        self.dargs, self.rargs, self.tag, self.keepalive = dargs, rargs, tag, keepalive
+    def __init__(self, dargs, rargs, tag, keepalive, max_parts):
+        self.dargs, self.rargs, self.tag, self.keepalive, self.max_parts = dargs, rargs, tag, keepalive, max_parts
 
     def launch(self, stream_handle: int) -> str:
         _lib.decode_partitions(self.dargs, stream_handle)
-        _lib.lse_reduce(self.rargs, stream_handle)
+        if self.rargs is not None:
+            _lib.lse_reduce(self.rargs, stream_handle)
         return self.tag
+
+
+# Default partition count when the caller passes max_context_partition_num=0:
+# enough workgroups to fill the GPU at two waves per SIMD (4 waves each), and
+# slots no longer than _MAX_SLOT_TOKENS of the longest possible sequence, so
+# ragged batches stay balanced.  (get_recommended_splits keeps the reference
+# formula for callers that ask for it.)
+_TARGET_WORKGROUPS_PER_CU = 2
+_MAX_SLOT_TOKENS = 8192
+
+
+def _auto_partitions(dev, batch_size, num_kv_heads, max_tokens, sliding_window, query_length):
+    cus = _device_cu_count(dev)
+    fill = _cdiv(cus * _TARGET_WORKGROUPS_PER_CU, max(1, batch_size * num_kv_heads))
+    span = min(max_tokens, sliding_window + query_length) if sliding_window > 0 else max_tokens
+    tiles = max(1, _cdiv(span, KV_COMPUTE_BLOCK) + (1 if sliding_window > 0 else 0))
+    return max(1, min(max(fill, _cdiv(span, _MAX_SLOT_TOKENS)), tiles))
 
 
 _PLAN_CACHE: "OrderedDict[tuple, _Plan]" = OrderedDict()
@@ -292,15 +312,20 @@ def _partitioned_plan(
             "CUDA graph capture requires preallocated `exp_sums`, `max_logits`, "
             f"and `temporary_output` for the {path_name} path."
         )
-    # every slot (including empty ones) is written by the kernel, so no fill is needed
-    if exp_sums is None:
-        exp_sums = torch.empty(shape, device=dev, dtype=torch.float32)
-    if max_logits is None:
-        max_logits = torch.empty(shape, device=dev, dtype=torch.float32)
-    if temporary_output is None:
-        temporary_output = torch.empty(shape + (head_size,), device=dev, dtype=torch.bfloat16)
-    _check_intermediates(exp_sums, max_logits, temporary_output, shape, head_size)
     output_5d = output.view(batch_size, query_length, num_kv_heads, query_group_size, head_size)
+    direct = max_parts == 1
+    if direct:
+        # one slot per sequence: the partition kernel writes the output itself
+        exp_sums = max_logits = temporary_output = None
+    else:
+        # every slot (including empty ones) is written by the kernel, so no fill is needed
+        if exp_sums is None:
+            exp_sums = torch.empty(shape, device=dev, dtype=torch.float32)
+        if max_logits is None:
+            max_logits = torch.empty(shape, device=dev, dtype=torch.float32)
+        if temporary_output is None:
+            temporary_output = torch.empty(shape + (head_size,), device=dev, dtype=torch.bfloat16)
+        _check_intermediates(exp_sums, max_logits, temporary_output, shape, head_size)
     dargs = _decode_args(
         query=query,
         key_cache=_u8(key_cache),
@@ -319,8 +344,18 @@ def _partitioned_plan(
         sliding_window=sliding_window,
         softmax_scale=softmax_scale,
     )
-    rargs = _reduce_args(output_5d, exp_sums, max_logits, temporary_output, max_parts, _get_output_dtype_str(output))
-    return _Plan(dargs, rargs, tag, (exp_sums, max_logits, temporary_output, key_scale, value_scale))
+    out_dtype = _get_output_dtype_str(output)
+    if direct:
+        dargs.direct_output = 1
+        dargs.out_dtype = {"bf16": _lib.PA_FP8_BF16, "f16": _lib.PA_FP8_F16, "f32": _lib.PA_FP8_F32}[out_dtype]
+        dargs.output = output_5d.data_ptr()
+        dargs.stride_o_seq, dargs.stride_o_len, dargs.stride_o_head, dargs.stride_o_group = (
+            output_5d.stride(i) for i in range(4)
+        )
+        rargs = None
+    else:
+        rargs = _reduce_args(output_5d, exp_sums, max_logits, temporary_output, max_parts, out_dtype)
+    return _Plan(dargs, rargs, tag, (exp_sums, max_logits, temporary_output, key_scale, value_scale), max_parts)
 
 
 def pa_decode_ps_launch(
@@ -457,22 +492,16 @@ def _build_plan(
     if block_tables.shape[0] != batch_size or block_tables.stride(1) != 1 or block_tables.device != dev:
         raise ValueError("block_tables must be [num_seqs, max_blocks] on the query device with a unit last stride")
 
+    if max_context_partition_num == 0:
+        max_context_partition_num = _auto_partitions(
+            dev, batch_size, num_kv_heads, block_tables.shape[1] * block_size, sliding_window, query_length
+        )
+    if max_context_partition_num < 1 or max_context_partition_num > 65535:
+        raise ValueError(f"max_context_partition_num={max_context_partition_num} out of range [1, 65535]")
     if sliding_window > 0:
-        if max_context_partition_num == 0:
-            max_context_partition_num = get_recommended_splits(
-                batch_size,
-                num_kv_heads,
-                sliding_window=sliding_window,
-                context_partition_size=KV_COMPUTE_BLOCK,
-                query_length=query_length,
-            )
         tag = "ps_sw_fused_partitioned" if max_context_partition_num <= 1 else "ps_sw_partitioned"
         path = "sliding-window"
     else:
-        if max_context_partition_num == 0:
-            max_context_partition_num = get_recommended_splits(
-                batch_size, num_kv_heads, split_kv_blocks=max(1, KV_COMPUTE_BLOCK // block_size)
-            )
         small = block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES
         tag = "ps_small_block" if small else "ps_partitioned"
         path = "small-block PS" if small else "partitioned"

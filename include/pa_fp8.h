@@ -93,7 +93,14 @@ typedef struct pa_fp8_decode_args {
     int32_t per_token_kv;        /* 0 = per-tensor scales, 1 = per-token */
     int32_t query_dtype;         /* PA_FP8_BF16 or PA_FP8_F16 */
     float softmax_scale;
-    int32_t reserved;
+    /* direct_output = 1 (only with max_context_partition_num == 1): each workgroup
+     * holds the whole sequence, so it writes the final rows to
+     * output[b, qi, h, gi, :] (5-D view [B, ql, Hkv, g, D], dtype out_dtype) as
+     * pa_fp8_lse_reduce would, and exp_sums / max_logits / tmp_out are not used. */
+    int32_t direct_output;
+    int32_t out_dtype;
+    void *output;
+    int64_t stride_o_seq, stride_o_len, stride_o_head, stride_o_group;
 } pa_fp8_decode_args;
 
 int pa_fp8_decode_partitions(const pa_fp8_decode_args *args, void *hip_stream);

@@ -55,23 +55,37 @@ SMALL_CASES = {
 
 
 @pytest.mark.parametrize("case", sorted(SMALL_CASES))
-@pytest.mark.parametrize("max_parts", [1, 3, 8])
+@pytest.mark.parametrize("max_parts", [1, 2, 3, 8])
 def test_small_cases_with_partials(case, max_parts):
-    """Ragged small shapes, every sequence and every partition slot checked."""
+    """Ragged small shapes, every sequence and every partition slot checked.
+
+    max_parts == 1 runs the direct-output mode (no partials, no reduce)."""
     kw = dict(SMALL_CASES[case])
     cfg = scaled(CONFIGS[kw.pop("base")], name=case, **kw)
     print(f"[parity] {case} P={max_parts}", flush=True)
     w = build_workload(cfg, "cuda", seed=7)
-    out, _, partials = launch(w, max_parts=max_parts, with_partials=True)
+    out, _, partials = launch(w, max_parts=max_parts, with_partials=max_parts > 1)
     compare_outputs(w, out, range(cfg.batch))
-    check_partials(w, partials, max_parts, range(cfg.batch))
+    if max_parts > 1:
+        check_partials(w, partials, max_parts, range(cfg.batch))
+
+
+@pytest.mark.parametrize("name", ["c2", "c4"])
+@pytest.mark.parametrize("max_parts", [1, 8])
+def test_baseline_config_partition_counts(name, max_parts):
+    """Full-size configs at the direct-output and the reference-default partition counts."""
+    cfg = CONFIGS[name]
+    w = build_workload(cfg, "cuda")
+    out, _, _ = launch(w, max_parts=max_parts)
+    compare_outputs(w, out, _spread(cfg.batch, 4))
 
 
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
-def test_output_dtypes(out_dtype):
+@pytest.mark.parametrize("max_parts", [1, 4])
+def test_output_dtypes(out_dtype, max_parts):
     cfg = scaled(CONFIGS["c2"], name="odt", batch=3, ctx_kind="uniform", ctx_a=5, ctx_b=700)
     w = build_workload(cfg, "cuda", seed=3)
-    out, _, _ = launch(w, out_dtype=out_dtype)
+    out, _, _ = launch(w, out_dtype=out_dtype, max_parts=max_parts)
     compare_outputs(w, out, range(cfg.batch))
 
 
