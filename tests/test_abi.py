@@ -1,0 +1,132 @@
+"""The C ABI: libpa_fp8.so loads without a GPU, exports every function
+include/pa_fp8.h declares, its argument structs have the layout the ctypes
+binding assumes, and argument validation returns the documented status codes
+(these calls return before any device work)."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "pa_fp8.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from flydsl_amd import build as fbuild
+
+    if not fbuild.LIB_PATH.exists():
+        fbuild.build()
+    from flydsl_amd import _lib
+
+    return _lib
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^[A-Za-z_][\w \*]*?\b(pa_fp8_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_expected_api():
+    assert declared_functions() == sorted(
+        ["pa_fp8_decode_partitions", "pa_fp8_lse_reduce", "pa_fp8_metadata_v1", "pa_fp8_status_string",
+         "pa_fp8_abi_version"]
+    )
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib.LIB_PATH)], capture_output=True, text=True, check=True)
+    exported = set(re.findall(r"\bT\s+(\w+)$", out.stdout, flags=re.M))
+    for name in declared_functions():
+        assert name in exported, name
+        assert hasattr(lib.LIB, name)
+    assert set(lib.EXPORTED_SYMBOLS) == set(declared_functions())
+
+
+def test_abi_version(lib):
+    assert lib.LIB.pa_fp8_abi_version() == lib.PA_FP8_ABI_VERSION
+    assert f"#define PA_FP8_ABI_VERSION {lib.PA_FP8_ABI_VERSION}" in HEADER.read_text()
+
+
+STRUCTS = {"pa_fp8_decode_args": "DecodeArgs", "pa_fp8_reduce_args": "ReduceArgs", "pa_fp8_metadata_args": "MetadataArgs"}
+
+
+def test_struct_layouts_match_header(lib, tmp_path):
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "pa_fp8.h"', "int main(void) {"]
+    for cname, pyname in STRUCTS.items():
+        cls = getattr(lib, pyname)
+        lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        s, f, v = line.split()
+        got[(s, f)] = int(v)
+    for cname, pyname in STRUCTS.items():
+        cls = getattr(lib, pyname)
+        assert got[(cname, "sizeof")] == ctypes.sizeof(cls), cname
+        for field, _ in cls._fields_:
+            assert got[(cname, field)] == getattr(cls, field).offset, (cname, field)
+
+
+def _decode_args(lib, **over):
+    a = lib.DecodeArgs()
+    a.batch_size, a.num_kv_heads, a.query_group_size, a.query_length = 0, 8, 4, 1
+    a.head_dim, a.block_size, a.max_context_partition_num = 128, 16, 8
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "over,status",
+    [
+        ({}, 0),  # an empty batch is a no-op
+        ({"head_dim": 64}, 2),
+        ({"block_size": 8}, 3),
+        ({"block_size": 48}, 3),
+        ({"query_group_size": 65}, 4),
+        ({"query_length": 5, "query_group_size": 16}, 4),
+        ({"max_context_partition_num": 0}, 7),
+        ({"query_dtype": 2}, 6),
+        ({"num_kv_heads": 0}, 5),
+        ({"direct_output": 1}, 7),
+        ({"batch_size": 3}, 1),  # null pointers
+    ],
+)
+def test_decode_validation_codes(lib, over, status):
+    assert lib.LIB.pa_fp8_decode_partitions(ctypes.byref(_decode_args(lib, **over)), None) == status
+
+
+def test_null_args_and_status_strings(lib):
+    assert lib.LIB.pa_fp8_decode_partitions(None, None) == 1
+    assert lib.LIB.pa_fp8_lse_reduce(None, None) == 1
+    assert lib.LIB.pa_fp8_metadata_v1(None, None) == 1
+    for code in range(0, 9):
+        assert lib.LIB.pa_fp8_status_string(code)
+    with pytest.raises(lib.PaFp8Error, match="status 2"):
+        lib.check("pa_fp8_decode_partitions", 2)
+
+
+def test_reduce_and_metadata_validation(lib):
+    r = lib.ReduceArgs()
+    r.batch_size, r.num_kv_heads, r.query_group_size, r.query_length, r.head_dim = 0, 8, 4, 1, 128
+    r.max_context_partition_num, r.out_dtype = 8, 0
+    assert lib.LIB.pa_fp8_lse_reduce(ctypes.byref(r), None) == 0
+    r.out_dtype = 7
+    assert lib.LIB.pa_fp8_lse_reduce(ctypes.byref(r), None) == 6
+    m = lib.MetadataArgs()
+    m.num_batches, m.gqa, m.num_heads_k, m.num_cu, m.kv_granularity, m.query_length = 4, 4, 8, 12, 256, 1
+    assert lib.LIB.pa_fp8_metadata_v1(ctypes.byref(m), None) == 5  # 12 bins not a multiple of 8 heads
+    m.num_cu, m.kv_granularity = 16, 100
+    assert lib.LIB.pa_fp8_metadata_v1(ctypes.byref(m), None) == 5  # granularity not a power of two
+    m.kv_granularity = 256
+    assert lib.LIB.pa_fp8_metadata_v1(ctypes.byref(m), None) == 1  # null buffers

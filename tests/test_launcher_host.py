@@ -1,0 +1,165 @@
+"""Host logic of the drop-in launcher, exercised on CPU tensors (no kernel runs):
+routing and return tags, argument blocks handed to the C ABI, the default
+partition policy, the direct-output mode and the reference's error behaviour."""
+
+import math
+
+import pytest
+import torch
+
+from flydsl_amd import _lib
+from flydsl_amd import pa_decode_fp8 as pdf
+from flydsl_amd.pa_decode_swa import get_sw_max_context_partition_num
+from flydsl_amd.pa_metadata import get_pa_metadata_info_v1
+
+
+def make(batch=3, hq=8, hkv=2, bs=16, ql=1, nb=20, per_token=False, max_blocks=8):
+    d = 128
+    t = dict(
+        output=torch.empty(batch * ql, hq, d, dtype=torch.bfloat16),
+        query=torch.zeros(batch * ql, hq, d, dtype=torch.bfloat16),
+        key_cache=torch.zeros(nb, hkv, d // 16, bs, 16, dtype=torch.uint8),
+        value_cache=torch.zeros(nb, hkv, bs // 16, d, 16, dtype=torch.uint8),
+        context_lengths=torch.full((batch,), 17, dtype=torch.int32),
+        block_tables=torch.zeros(batch, max_blocks, dtype=torch.int32),
+    )
+    if per_token:
+        t["key_scale"] = torch.ones(nb, hkv, bs, 1)
+        t["value_scale"] = torch.ones(nb, hkv, bs, 1)
+    else:
+        t["key_scale"] = torch.ones(1)
+        t["value_scale"] = torch.ones(1)
+    return t
+
+
+def plan(t, sliding_window=0, max_parts=4, **over):
+    t = {**t, **over}
+    return pdf._build_plan(
+        t["output"], t["query"], t["key_cache"], t["value_cache"], t["context_lengths"], 1 / math.sqrt(128),
+        t["key_scale"], t["value_scale"], sliding_window, t["block_tables"], max_parts,
+        t.get("exp_sums"), t.get("max_logits"), t.get("temporary_output"), False,
+    )
+
+
+def test_small_block_routing_and_args():
+    t = make()
+    p = plan(t, max_parts=4)
+    assert p.tag == "ps_small_block" and p.max_parts == 4 and p.rargs is not None
+    a = p.dargs
+    assert (a.batch_size, a.num_kv_heads, a.query_group_size, a.query_length) == (3, 2, 4, 1)
+    assert (a.head_dim, a.block_size, a.num_blocks, a.max_blocks_per_seq) == (128, 16, 20, 8)
+    assert a.stride_k_block == 2 * 8 * 16 * 16 and a.stride_k_head == 8 * 16 * 16
+    assert a.stride_v_block == 2 * 1 * 128 * 16 and a.stride_v_head == 128 * 16
+    assert a.stride_q_seq == 8 * 128 and a.stride_q_head == 128 and a.stride_bt_seq == 8
+    assert a.per_token_kv == 0 and a.stride_ks_block == 0 and a.direct_output == 0
+    assert abs(a.softmax_scale - 1 / math.sqrt(128)) < 1e-7
+    es, to = p.keepalive[0], p.keepalive[2]
+    assert tuple(es.shape) == (3, 2, 4, 4) and tuple(to.shape) == (3, 2, 4, 4, 128)
+    assert a.exp_sums == es.data_ptr() and a.tmp_out == to.data_ptr()
+    r = p.rargs
+    assert (r.batch_size, r.query_length, r.num_kv_heads, r.query_group_size, r.max_context_partition_num) == (3, 1, 2, 4, 4)
+    assert r.stride_o_seq == 8 * 128 and r.stride_o_head == 4 * 128 and r.stride_o_group == 128
+
+
+def test_per_token_strides_and_mtp():
+    t = make(batch=2, hq=16, hkv=2, bs=64, ql=4, per_token=True)
+    p = plan(t, max_parts=3)
+    assert p.dargs.per_token_kv == 1
+    assert p.dargs.stride_ks_block == 2 * 64 and p.dargs.stride_ks_head == 64
+    assert p.dargs.query_length == 4 and p.dargs.query_group_size == 8
+    r = p.rargs
+    assert r.stride_o_seq == 4 * 16 * 128 and r.stride_o_len == 16 * 128
+
+
+def test_direct_output_mode_for_one_slot():
+    t = make()
+    p = plan(t, max_parts=1)
+    assert p.rargs is None and p.dargs.direct_output == 1 and p.dargs.exp_sums is None
+    assert p.dargs.output == t["output"].data_ptr() and p.dargs.out_dtype == _lib.PA_FP8_BF16
+    p32 = plan(t, max_parts=1, output=torch.empty(3, 8, 128))
+    assert p32.dargs.out_dtype == _lib.PA_FP8_F32
+
+
+def test_sliding_window_routing():
+    t = make()
+    assert plan(t, sliding_window=300, max_parts=3).tag == "ps_sw_partitioned"
+    p = plan(t, sliding_window=300, max_parts=1)
+    assert p.tag == "ps_sw_fused_partitioned" and p.dargs.sliding_window == 300
+    assert plan(make(bs=1024, max_blocks=2), max_parts=2).tag == "ps_partitioned"
+
+
+def test_caller_intermediates_are_used():
+    t = make()
+    shape = (3, 2, 5, 4)
+    es, ml = torch.empty(shape), torch.empty(shape)
+    to = torch.empty(shape + (128,), dtype=torch.bfloat16)
+    p = plan(t, max_parts=5, exp_sums=es, max_logits=ml, temporary_output=to)
+    assert p.dargs.exp_sums == es.data_ptr() and p.dargs.max_logits == ml.data_ptr() and p.dargs.tmp_out == to.data_ptr()
+    with pytest.raises(ValueError, match="exp_sums"):
+        plan(t, max_parts=4, exp_sums=es, max_logits=ml, temporary_output=to)
+
+
+@pytest.mark.parametrize(
+    "over,exc,match",
+    [
+        ({"query": torch.zeros(3, 8, 128, dtype=torch.uint8)}, ValueError, "no longer accepts"),
+        ({"query": torch.zeros(3, 8, 128, dtype=torch.float32)}, ValueError, "Unsupported query dtype"),
+        ({"output": torch.empty(3, 8, 128, dtype=torch.int32)}, ValueError, "Unsupported output dtype"),
+        ({"block_tables": None}, ValueError, "requires `block_tables`"),
+        ({"value_cache": torch.zeros(20, 2, 128, 16, dtype=torch.uint8)}, NotImplementedError, "trans_v"),
+        ({"value_cache": torch.zeros(20, 2, 2, 128, 16, dtype=torch.uint8)}, ValueError, "trans_v layout"),
+        ({"key_cache": torch.zeros(20, 2, 8, 24, 16, dtype=torch.uint8),
+          "value_cache": torch.zeros(20, 2, 1, 128, 16, dtype=torch.uint8)}, ValueError, "power of two"),
+        ({"context_lengths": torch.full((3,), 17, dtype=torch.int64)}, ValueError, "int32"),
+        ({"query": torch.zeros(3, 7, 128, dtype=torch.bfloat16), "output": torch.empty(3, 7, 128, dtype=torch.bfloat16)},
+         ValueError, "divisible"),
+        ({"key_scale": torch.ones(2)}, ValueError, "per-tensor"),
+    ],
+)
+def test_validation_errors(over, exc, match):
+    with pytest.raises(exc, match=match):
+        plan(make(), max_parts=4, **over)
+
+
+def test_eqgs_limit():
+    with pytest.raises(ValueError, match="<= 64"):
+        plan(make(batch=1, hq=40, hkv=2, ql=4), max_parts=2)
+
+
+def test_graph_capture_requires_preallocated_partials():
+    t = make()
+    with pytest.raises(ValueError, match="graph capture requires"):
+        pdf._prepare_scale_tensor("key_scale", 0.5, device=torch.device("cpu"), is_graph_capturing=True)
+    with pytest.raises(ValueError, match="CUDA graph capture requires preallocated"):
+        pdf._build_plan(t["output"], t["query"], t["key_cache"], t["value_cache"], t["context_lengths"], 0.1,
+                        t["key_scale"], t["value_scale"], 0, t["block_tables"], 4, None, None, None, True)
+
+
+def test_auto_partition_policy(monkeypatch):
+    monkeypatch.setattr(pdf, "_device_cu_count", lambda dev: 256)
+    # c2: 64 x 8 (b, h) pairs already fill 256 CUs x 2 workgroups -> one slot, direct output
+    assert pdf._auto_partitions(None, 64, 8, 4096, 0, 1) == 1
+    # c3: sequences up to 32768 tokens -> slots of at most 8192 tokens
+    assert pdf._auto_partitions(None, 128, 8, 32768, 0, 1) == 4
+    # c4: 32 x 8 pairs -> 2 slots to fill the GPU; never more slots than window tiles
+    assert pdf._auto_partitions(None, 32, 8, 32768, 4096, 1) == 2
+    assert pdf._auto_partitions(None, 1, 1, 300, 0, 1) == 2
+    assert pdf._auto_partitions(None, 1, 1, 100, 0, 1) == 1
+
+
+def test_recommended_splits_reference_formula(monkeypatch):
+    monkeypatch.setattr(pdf, "_cu_count", lambda idx: 256)
+    monkeypatch.setattr(torch.cuda, "current_device", lambda: 0)
+    assert pdf.get_recommended_splits(64, 8, 16) == 8
+    assert pdf.get_recommended_splits(256, 4, 4) == 4
+    assert pdf.get_recommended_splits(32, 8, sliding_window=4096) == 17
+    assert get_sw_max_context_partition_num(4096) == 17
+
+
+def test_metadata_info_matches_oracle():
+    from oracle import planners as op
+
+    ours = get_pa_metadata_info_v1(128, 8, num_cu=768)
+    ref = op.get_pa_metadata_info_v1(128, 8, 768)
+    assert [s for s, _ in ours] == [s for s, _ in ref]
+    assert [str(d).split(".")[-1] for _, d in ours] == [d for _, d in ref]

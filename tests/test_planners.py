@@ -1,0 +1,250 @@
+"""Integer planners of the decode path: split counts, partition ranges,
+sliding-window tiles, page data and the get_pa_metadata_v1 worklist.
+
+Pinned by brute-force enumeration, invariants and a hand-worked example; the
+Python and plain-C restatements of the scheduler are cross-checked bit-exact."""
+
+import ctypes
+import math
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import planners as op
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+# ------------------------------------------------------------- split counts
+def test_recommended_splits_baseline_values():
+    # MI355X: 256 CUs. Values of the five benchmark configurations.
+    assert op.get_recommended_splits(4, 2, 16, num_cu=256) == 8
+    assert op.get_recommended_splits(64, 8, 16, num_cu=256) == 8
+    assert op.get_recommended_splits(128, 8, 16, num_cu=256) == 8
+    assert op.get_recommended_splits(256, 4, 4, num_cu=256) == 4
+    assert op.get_recommended_splits(32, 8, sliding_window=4096, query_length=1) == 17
+    # the harness passes (sliding_window, 256, ql) positionally: seqs=0 -> denominator 1 -> 8
+    assert op.get_recommended_splits(0, 256, 1, num_cu=256) == 8
+
+
+def test_recommended_splits_clamp_and_form():
+    for seqs in (0, 1, 3, 17, 64, 1000):
+        for heads in (1, 2, 8):
+            for split in (1, 4, 16):
+                n = op.get_recommended_splits(seqs, heads, split, num_cu=256)
+                assert 4 <= n <= 8
+                raw = -(-512 // max(1, seqs * heads * split)) * split
+                assert n == max(4, min(raw, 8))
+
+
+def test_sw_partition_count_bounds_visible_tiles():
+    for sw in (1, 100, 255, 256, 257, 4096):
+        for ql in (1, 2, 4):
+            bound = op.get_sw_max_context_partition_num(sw, 256, ql)
+            assert bound == op.get_recommended_splits(1, 1, sliding_window=sw, query_length=ql)
+            worst = 0
+            for ctx in range(1, sw + ql + 2 * 256 + 3):
+                tail = op.sw_tail_start_tile(ctx, ql, sw)
+                worst = max(worst, op.cdiv(ctx, 256) - tail)
+            assert worst <= bound  # every visible tile gets a slot
+            assert worst >= bound - 1
+    assert op.get_sw_max_context_partition_num(0) == 0
+
+
+# --------------------------------------------------------- partition ranges
+@pytest.mark.parametrize("max_parts", [1, 2, 3, 5, 8, 16])
+def test_small_block_ranges_tile_exactly(max_parts):
+    for ctx in list(range(0, 1200, 7)) + [4096, 4097, 32768]:
+        t = op.cdiv(ctx, 256)
+        covered = []
+        pps = op.cdiv(t, max_parts) if t else 0
+        seen_empty = False
+        for z in range(max_parts):
+            lo, hi = op.small_block_partition_range(ctx, z, max_parts)
+            if lo == hi:
+                seen_empty = True
+                continue
+            assert not seen_empty, "non-empty slot after an empty one"
+            assert hi - lo <= pps
+            covered.extend(range(lo, hi))
+        assert covered == list(range(t))
+
+
+def test_token_ranges_cover_visible_keys_once():
+    for sw in (0, 50, 300):
+        for ql in (1, 3):
+            for ctx in range(ql, 900, 13):
+                for parts in (1, 2, 4, 17):
+                    toks = []
+                    for z in range(parts):
+                        lo, hi = op.partition_token_range(ctx, z, parts, ql, sw)
+                        toks.extend(range(lo, hi))
+                    assert len(toks) == len(set(toks))
+                    need = set()
+                    for qi in range(ql):
+                        from oracle.attention import visible_token_bounds
+
+                        a, b = visible_token_bounds(ctx, ql, qi, sw)
+                        need.update(range(a, b))
+                    assert need <= set(toks)
+                    assert all(t < ctx for t in toks)
+
+
+def test_sw_slots_match_reference_tile_mapping():
+    """With the recommended slot count the mapping is tile tail+z, one tile each
+    (kernels/pa_decode_swa.py:1359-1368)."""
+    sw, ql = 4096, 1
+    parts = op.get_sw_max_context_partition_num(sw, 256, ql)
+    for ctx in (8192, 8193, 9000, 20000, 32768, 100, 4096, 4097):
+        tail = op.sw_tail_start_tile(ctx, ql, sw)
+        t = op.cdiv(ctx, 256)
+        for z in range(parts):
+            lo, hi = op.sw_partition_range(ctx, z, parts, ql, sw)
+            if tail + z < t:
+                assert (lo, hi) == (tail + z, tail + z + 1)
+            else:
+                assert lo == hi
+
+
+def test_token_physical_slot():
+    row = [7, 3, 9]
+    assert op.token_physical_slot(row, 0, 16) == (7, 0)
+    assert op.token_physical_slot(row, 17, 16) == (3, 1)
+    assert op.token_physical_slot(row, 47, 16) == (9, 15)
+
+
+def test_build_ps_page_data():
+    tables = [[5, 6, 7, 8], [1, 2, 3, 4], [9, 10, 11, 12]]
+    pages, indptr = op.build_ps_page_data(tables, [17, 1, 48], 16)
+    assert indptr.tolist() == [0, 2, 3, 6]
+    assert pages.tolist() == [5, 6, 1, 9, 10, 11]
+
+
+# ----------------------------------------------------------- worklist
+def test_metadata_info_shapes():
+    info = op.get_pa_metadata_info_v1(128, 8, 768)
+    assert [s for s, _ in info] == [(2,), (769,), (7160, 8), (129,), (128, 2), (895,)]
+
+
+def test_metadata_hand_worked_example():
+    """num_cu 4, 2 kv heads (2 bins each), ctx [300, 1000, 100] -> partitions
+    [2, 4, 1] (sum 7, quota 4/3 by bin parity); worked by hand from the
+    scheduler rules (kernels/pa_metadata.py:203-399)."""
+    md = op.get_pa_metadata_v1([0, 1, 2, 3], [300, 1000, 100], 4, 2, 4, 256, 1)
+    v = op.metadata_valid_prefixes(md)
+    q0, q1 = (4 << 16) | 0, (8 << 16) | 4
+    assert v["work_indptr"].tolist() == [0, 2, 4, 6, 8]
+    assert v["work_info"].tolist() == [
+        [0, -1, 0, 1, 0, 2, 0, q0],
+        [1, 0, 1, 2, 2, 4, 0, q0],
+        [1, 1, 1, 2, 4, 6, 0, q0],
+        [2, -1, 2, 3, 6, 7, 0, q0],
+        [0, -1, 0, 1, 0, 2, 0, q1],
+        [1, 0, 1, 2, 2, 4, 0, q1],
+        [1, 1, 1, 2, 4, 6, 0, q1],
+        [2, -1, 2, 3, 6, 7, 0, q1],
+    ]
+    assert v["reduce_indptr"].tolist() == [0, 2, 2, 2]
+    assert v["reduce_final_map"].tolist() == [[1, 2]]
+    assert v["reduce_partial_map"].tolist() == [0, 1]
+
+
+def _check_invariants(md, ctx, gqa, nhk, num_cu, gran, ql):
+    v = op.metadata_valid_prefixes(md)
+    wi = v["work_indptr"]
+    assert wi[0] == 0 and np.all(np.diff(wi) >= 0)
+    works = v["work_info"]
+    assert len(works) == wi[-1]
+    parts = [op.cdiv(c, gran) for c in ctx]
+    starts = np.concatenate([[0], np.cumsum(parts)])
+    total = int(starts[-1])
+    nspk = num_cu // nhk
+    avg, rem = total // nspk, total % nspk
+    for cid in range(num_cu):
+        load = sum(int(w[5] - w[4]) for w in works[wi[cid] : wi[cid + 1]])
+        assert load <= avg + (1 if cid % nspk < rem else 0)
+    for kh in range(nhk):
+        qhr = (((kh + 1) * gqa) << 16) | ((kh * gqa) & 0xFFFF)
+        hw = [w for w in works if w[7] == qhr]
+        cover = []
+        for w in hw:
+            b = int(w[0])
+            assert (w[2], w[3]) == (b * ql, (b + 1) * ql)
+            assert starts[b] <= w[4] < w[5] <= starts[b + 1]
+            cover.extend(range(int(w[4]), int(w[5])))
+            nworks_b = sum(1 for x in hw if x[0] == b)
+            assert (w[1] == -1) == (nworks_b == 1)
+        assert cover == [t for b in range(len(ctx)) for t in range(int(starts[b]), int(starts[b + 1]))]
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_metadata_invariants_random(seed):
+    rng = np.random.default_rng(seed)
+    nhk = int(rng.choice([1, 2, 4, 8]))
+    num_cu = nhk * int(rng.integers(1, 40))
+    b = int(rng.integers(1, 60))
+    ctx = [int(x) for x in rng.integers(1, 9000, size=b)]
+    ql = int(rng.integers(1, 5))
+    gqa = int(rng.choice([1, 4, 8]))
+    md = op.get_pa_metadata_v1([i * ql for i in range(b + 1)], ctx, gqa, nhk, num_cu, 256, ql)
+    _check_invariants(md, ctx, gqa, nhk, num_cu, 256, ql)
+
+
+# ------------------------------------------------ C restatement agreement
+@pytest.fixture(scope="module")
+def c_oracle():
+    so = ROOT / "oracle" / "_build" / "libpa_oracle.so"
+    subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+    lib = ctypes.CDLL(str(so))
+    P = ctypes.POINTER(ctypes.c_int32)
+    lib.pa_metadata_v1_ref.argtypes = [P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_int, P, P, ctypes.c_int, P, P, P, ctypes.c_int, P]
+    lib.pa_metadata_v1_ref.restype = ctypes.c_int
+    return lib
+
+
+def run_c_metadata(lib, sq, ctx, gqa, nhk, num_cu, gran, ql):
+    info = op.get_pa_metadata_info_v1(len(ctx), nhk, num_cu)
+    arr = lambda shape: np.full(shape, op.POISON, dtype=np.int32)  # noqa: E731
+    wi, winfo, ri, rfm, rpm = arr(info[1][0]), arr(info[2][0]), arr(info[3][0]), arr(info[4][0]), arr(info[5][0])
+    ng = np.zeros(1, np.int32)
+    P = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))  # noqa: E731
+    sqa, ca = np.asarray(sq, np.int32), np.asarray(ctx, np.int32)
+    rc = lib.pa_metadata_v1_ref(P(sqa), P(ca), len(ctx), gqa, nhk, num_cu, gran, ql, P(wi), P(winfo),
+                                info[2][0][0], P(ri), P(rfm), P(rpm), info[5][0][0], P(ng))
+    assert rc == 0
+    return {"work_indptr": wi, "work_info": winfo, "reduce_indptr": ri, "reduce_final_map": rfm,
+            "reduce_partial_map": rpm, "num_reduce_groups": ng[0]}
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_c_and_python_schedulers_agree(c_oracle, seed):
+    rng = np.random.default_rng(100 + seed)
+    nhk = int(rng.choice([1, 2, 4, 8]))
+    num_cu = nhk * int(rng.integers(1, 100))
+    b = int(rng.integers(1, 140))
+    hi = int(rng.choice([300, 5000, 33000]))
+    ctx = [int(x) for x in rng.integers(1, hi, size=b)]
+    ql = int(rng.integers(1, 5))
+    gqa = int(rng.choice([1, 4, 16]))
+    gran = int(rng.choice([16, 256, 1024]))
+    sq = [i * ql for i in range(b + 1)]
+    py = op.metadata_valid_prefixes(op.get_pa_metadata_v1(sq, ctx, gqa, nhk, num_cu, gran, ql))
+    cc = op.metadata_valid_prefixes(run_c_metadata(c_oracle, sq, ctx, gqa, nhk, num_cu, gran, ql))
+    for key in py:
+        np.testing.assert_array_equal(py[key], cc[key], err_msg=key)
+
+
+def test_c3_shaped_schedule(c_oracle):
+    """The benchmark's ragged shape: 128 sequences, 8 kv heads, 768 bins."""
+    from flydsl_amd.workloads import CONFIGS, context_lengths_for
+
+    ctx = context_lengths_for(CONFIGS["c3"])
+    sq = list(range(129))
+    md = op.get_pa_metadata_v1(sq, ctx, 4, 8, 768, 256, 1)
+    _check_invariants(md, ctx, 4, 8, 768, 256, 1)
+    cc = run_c_metadata(c_oracle, sq, ctx, 4, 8, 768, 256, 1)
+    for key, val in op.metadata_valid_prefixes(md).items():
+        np.testing.assert_array_equal(val, op.metadata_valid_prefixes(cc)[key])
