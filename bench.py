@@ -43,6 +43,8 @@ def _parse():
     ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
     ap.add_argument("--max-parts", type=int, default=0, help="max_context_partition_num (0 = launcher default)")
+    ap.add_argument("--traffic-run", action="store_true",
+                    help="for rocprofv3 --pmc passes: a 256 MiB copy (counter calibration) then --steps decode steps")
     return ap.parse_args()
 
 
@@ -147,6 +149,19 @@ def main():
             w["key_scale"], w["value_scale"], sliding_window=cfg.sliding_window, block_tables=w["block_tables"],
             max_context_partition_num=max_parts,
         )
+
+    if args.traffic_run:
+        # calibration: a plain copy of known size, then the decode steps to count
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            tag = step(i)
+        torch.cuda.synchronize()
+        print(json.dumps({"traffic_run": cfg.name, "copy_bytes": src.numel(), "steps": args.steps, "path": tag}))
+        return
 
     for i in range(args.warmup):
         tag = step(i)
