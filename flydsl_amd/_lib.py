@@ -141,7 +141,7 @@ class PaFp8Error(RuntimeError):
 def _load() -> ctypes.CDLL:
     if not LIB_PATH.exists():
         raise ImportError(
-            f"libpa_fp8.so not found at {LIB_PATH}; build it with `python -m flydsl_amd.build` "
+            f"libpa_fp8.so not found at {LIB_PATH}; build it with `python flydsl_amd/build.py` "
             "(there is no fallback implementation)"
         )
     lib = ctypes.CDLL(str(LIB_PATH))

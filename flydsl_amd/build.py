@@ -1,6 +1,7 @@
 """Build recipe for libpa_fp8.so (hand-written gfx950 HIP kernels + C ABI).
 
-``python -m flydsl_amd.build`` compiles the library in-tree next to this file.
+``python flydsl_amd/build.py`` compiles the library in-tree next to this file (run it
+by path: importing the package first would try to load the library).
 hipcc cross-compiles for gfx950 without a GPU, so this runs anywhere the ROCm
 toolchain is installed.
 """

@@ -16,8 +16,13 @@ HEADER = ROOT / "include" / "pa_fp8.h"
 
 @pytest.fixture(scope="module")
 def lib():
-    from flydsl_amd import build as fbuild
+    import importlib.util
 
+    # The recipe is loaded by path: importing it through the package would run
+    # flydsl_amd/__init__.py, which needs the library it builds.
+    spec = importlib.util.spec_from_file_location("_flydsl_amd_build", ROOT / "flydsl_amd" / "build.py")
+    fbuild = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(fbuild)
     if not fbuild.LIB_PATH.exists():
         fbuild.build()
     from flydsl_amd import _lib
