@@ -13,6 +13,7 @@ from .pa_decode_fp8 import (  # noqa: F401
 )
 from .pa_decode_swa import get_sw_max_context_partition_num, pa_decode_sw_reduce  # noqa: F401
 from .pa_metadata import get_pa_metadata_info_v1, get_pa_metadata_v1  # noqa: F401
+from .pa_reduce import pa_reduce_v1  # noqa: F401
 
 __all__ = [
     "KV_COMPUTE_BLOCK",
@@ -23,4 +24,5 @@ __all__ = [
     "get_sw_max_context_partition_num",
     "pa_decode_ps_launch",
     "pa_decode_sw_reduce",
+    "pa_reduce_v1",
 ]

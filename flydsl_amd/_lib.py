@@ -13,7 +13,7 @@ from pathlib import Path
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("PA_FP8_LIB", str(_HERE / "libpa_fp8.so")))
 
-PA_FP8_ABI_VERSION = 1
+PA_FP8_ABI_VERSION = 2
 PA_FP8_BF16, PA_FP8_F16, PA_FP8_F32 = 0, 1, 2
 
 _vp = ctypes.c_void_p
@@ -101,6 +101,81 @@ class ReduceArgs(ctypes.Structure):
     ]
 
 
+class WorklistArgs(ctypes.Structure):
+    _fields_ = [
+        ("output", _vp),
+        ("partial_output", _vp),
+        ("partial_lse", _vp),
+        ("query", _vp),
+        ("key_cache", _vp),
+        ("value_cache", _vp),
+        ("context_lengths", _vp),
+        ("key_scale", _vp),
+        ("value_scale", _vp),
+        ("work_indptr", _vp),
+        ("work_info", _vp),
+        ("kv_page_indices", _vp),
+        ("kv_indptr", _vp),
+        ("partition_indptr", _vp),
+        ("stride_q_seq", _i64),
+        ("stride_q_head", _i64),
+        ("stride_k_block", _i64),
+        ("stride_k_head", _i64),
+        ("stride_v_block", _i64),
+        ("stride_v_head", _i64),
+        ("stride_out_seq", _i64),
+        ("stride_out_head", _i64),
+        ("stride_po_row", _i64),
+        ("stride_pl_row", _i64),
+        ("stride_ks_block", _i64),
+        ("stride_ks_head", _i64),
+        ("batch_size", _i32),
+        ("num_kv_heads", _i32),
+        ("query_group_size", _i32),
+        ("query_length", _i32),
+        ("head_dim", _i32),
+        ("block_size", _i32),
+        ("num_blocks", _i32),
+        ("num_pages", _i32),
+        ("num_cu", _i32),
+        ("max_work", _i32),
+        ("partial_rows", _i32),
+        ("output_rows", _i32),
+        ("per_token_kv", _i32),
+        ("query_dtype", _i32),
+        ("out_dtype", _i32),
+        ("softmax_scale", _f32),
+    ]
+
+
+class ReduceV1Args(ctypes.Structure):
+    _fields_ = [
+        ("output", _vp),
+        ("final_lse", _vp),
+        ("partial_output", _vp),
+        ("partial_lse", _vp),
+        ("reduce_indptr", _vp),
+        ("reduce_final_map", _vp),
+        ("reduce_partial_map", _vp),
+        ("stride_po_row", _i64),
+        ("stride_po_head", _i64),
+        ("stride_pl_row", _i64),
+        ("stride_pl_head", _i64),
+        ("stride_out_row", _i64),
+        ("stride_out_head", _i64),
+        ("stride_lse_row", _i64),
+        ("stride_lse_head", _i64),
+        ("num_groups", _i32),
+        ("num_heads", _i32),
+        ("head_dim", _i32),
+        ("max_qlen", _i32),
+        ("partial_rows", _i32),
+        ("output_rows", _i32),
+        ("partial_map_len", _i32),
+        ("out_dtype", _i32),
+    ]
+
+
 class MetadataArgs(ctypes.Structure):
     _fields_ = [
         ("seqlens_qo_indptr", _vp),
@@ -124,6 +199,8 @@ class MetadataArgs(ctypes.Structure):
 EXPORTED_SYMBOLS = (
     "pa_fp8_decode_partitions",
     "pa_fp8_lse_reduce",
+    "pa_fp8_decode_worklist",
+    "pa_fp8_reduce_v1",
     "pa_fp8_metadata_v1",
     "pa_fp8_status_string",
     "pa_fp8_abi_version",
@@ -145,19 +222,23 @@ def _load() -> ctypes.CDLL:
             "(there is no fallback implementation)"
         )
     lib = ctypes.CDLL(str(LIB_PATH))
-    lib.pa_fp8_decode_partitions.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
-    lib.pa_fp8_decode_partitions.restype = ctypes.c_int
-    lib.pa_fp8_lse_reduce.argtypes = [ctypes.POINTER(ReduceArgs), _vp]
-    lib.pa_fp8_lse_reduce.restype = ctypes.c_int
-    lib.pa_fp8_metadata_v1.argtypes = [ctypes.POINTER(MetadataArgs), _vp]
-    lib.pa_fp8_metadata_v1.restype = ctypes.c_int
-    lib.pa_fp8_status_string.argtypes = [ctypes.c_int]
-    lib.pa_fp8_status_string.restype = ctypes.c_char_p
     lib.pa_fp8_abi_version.argtypes = []
     lib.pa_fp8_abi_version.restype = ctypes.c_int
     ver = lib.pa_fp8_abi_version()
     if ver != PA_FP8_ABI_VERSION:
         raise ImportError(f"libpa_fp8.so ABI version {ver} != expected {PA_FP8_ABI_VERSION}; rebuild the library")
+    lib.pa_fp8_decode_partitions.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
+    lib.pa_fp8_decode_partitions.restype = ctypes.c_int
+    lib.pa_fp8_lse_reduce.argtypes = [ctypes.POINTER(ReduceArgs), _vp]
+    lib.pa_fp8_lse_reduce.restype = ctypes.c_int
+    lib.pa_fp8_decode_worklist.argtypes = [ctypes.POINTER(WorklistArgs), _vp]
+    lib.pa_fp8_decode_worklist.restype = ctypes.c_int
+    lib.pa_fp8_reduce_v1.argtypes = [ctypes.POINTER(ReduceV1Args), _vp]
+    lib.pa_fp8_reduce_v1.restype = ctypes.c_int
+    lib.pa_fp8_metadata_v1.argtypes = [ctypes.POINTER(MetadataArgs), _vp]
+    lib.pa_fp8_metadata_v1.restype = ctypes.c_int
+    lib.pa_fp8_status_string.argtypes = [ctypes.c_int]
+    lib.pa_fp8_status_string.restype = ctypes.c_char_p
     return lib
 
 
@@ -175,6 +256,14 @@ def decode_partitions(args: DecodeArgs, stream: int) -> None:
 
 def lse_reduce(args: ReduceArgs, stream: int) -> None:
     check("pa_fp8_lse_reduce", LIB.pa_fp8_lse_reduce(ctypes.byref(args), _vp(stream)))
+
+
+def decode_worklist(args: WorklistArgs, stream: int) -> None:
+    check("pa_fp8_decode_worklist", LIB.pa_fp8_decode_worklist(ctypes.byref(args), _vp(stream)))
+
+
+def reduce_v1(args: ReduceV1Args, stream: int) -> None:
+    check("pa_fp8_reduce_v1", LIB.pa_fp8_reduce_v1(ctypes.byref(args), _vp(stream)))
 
 
 def metadata_v1(args: MetadataArgs, stream: int) -> None:

@@ -59,25 +59,12 @@ struct DecodeParams {
     int32_t direct;
 };
 
-// n consecutive outputs of row r starting at head dim d0: to the bf16 partial
-// row, or (direct mode) converted to the output dtype at out[b, qi, h, gi, d0].
+// N consecutive values to the output tensor at element offset off, converted to
+// out_dtype (bf16 / f16 round to nearest even, f32 stored as is).
 template <int N>
-__device__ __forceinline__ void emit_row(const DecodeParams &p, uint16_t *to, int b, int h, int r, int d0,
-                                         const float (&v)[N]) {
-    if (!p.direct) {
-        uint32_t pk[N / 2];
-#pragma unroll
-        for (int j = 0; j < N; j += 2)
-            pk[j / 2] = uint32_t(f32_to_bf16_bits(v[j])) | (uint32_t(f32_to_bf16_bits(v[j + 1])) << 16);
-        uint16_t *dst = to + r * p.s_to_group + d0;
-        if constexpr (N == 8) *reinterpret_cast<uint4 *>(dst) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        else *reinterpret_cast<uint2 *>(dst) = make_uint2(pk[0], pk[1]);
-        return;
-    }
-    const int qi = r / p.g, gi = r - (r / p.g) * p.g;
-    const int64_t off = b * p.s_o_seq + qi * p.s_o_len + h * p.s_o_head + gi * p.s_o_group + d0;
-    if (p.out_dtype == PA_FP8_F32) {
-        float *dst = reinterpret_cast<float *>(p.out) + off;
+__device__ __forceinline__ void store_out(void *out, int out_dtype, int64_t off, const float (&v)[N]) {
+    if (out_dtype == PA_FP8_F32) {
+        float *dst = reinterpret_cast<float *>(out) + off;
 #pragma unroll
         for (int j = 0; j < N; j += 4) *reinterpret_cast<float4 *>(dst + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
         return;
@@ -85,15 +72,48 @@ __device__ __forceinline__ void emit_row(const DecodeParams &p, uint16_t *to, in
     uint32_t pk[N / 2];
 #pragma unroll
     for (int j = 0; j < N; j += 2) {
-        if (p.out_dtype == PA_FP8_F16)
+        if (out_dtype == PA_FP8_F16)
             pk[j / 2] = uint32_t(f32_to_f16_bits(v[j])) | (uint32_t(f32_to_f16_bits(v[j + 1])) << 16);
         else
             pk[j / 2] = uint32_t(f32_to_bf16_bits(v[j])) | (uint32_t(f32_to_bf16_bits(v[j + 1])) << 16);
     }
-    uint16_t *dst = reinterpret_cast<uint16_t *>(p.out) + off;
+    uint16_t *dst = reinterpret_cast<uint16_t *>(out) + off;
     if constexpr (N == 8) *reinterpret_cast<uint4 *>(dst) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
     else *reinterpret_cast<uint2 *>(dst) = make_uint2(pk[0], pk[1]);
 }
+
+// Where the partition kernel puts the result of one slot: the bf16 partial row
+// plus (exp_sum, max_logit), or (direct mode) the final row out[b, qi, h, gi, :].
+struct SlotSink {
+    const DecodeParams &p;
+    uint16_t *to;
+    float *es;
+    float *ml;
+    int b, h;
+
+    template <int N>
+    __device__ __forceinline__ void row(int r, int d0, const float (&v)[N]) const {
+        if (!p.direct) {
+            uint32_t pk[N / 2];
+#pragma unroll
+            for (int j = 0; j < N; j += 2)
+                pk[j / 2] = uint32_t(f32_to_bf16_bits(v[j])) | (uint32_t(f32_to_bf16_bits(v[j + 1])) << 16);
+            uint16_t *dst = to + r * p.s_to_group + d0;
+            if constexpr (N == 8) *reinterpret_cast<uint4 *>(dst) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            else *reinterpret_cast<uint2 *>(dst) = make_uint2(pk[0], pk[1]);
+            return;
+        }
+        const int qi = r / p.g, gi = r - (r / p.g) * p.g;
+        store_out<N>(p.out, p.out_dtype, b * p.s_o_seq + qi * p.s_o_len + h * p.s_o_head + gi * p.s_o_group + d0, v);
+    }
+    // L = sum of exp2(logit2 - m2) over the slot, m2 = running max in log2 units
+    __device__ __forceinline__ void stats(int r, float L, float m2) const {
+        if (!p.direct) {
+            es[r] = L;
+            ml[r] = L > 0.f ? m2 * kLn2 : -INFINITY;
+        }
+    }
+};
 
 struct ReduceParams {
     void *out;
@@ -122,12 +142,20 @@ __device__ __forceinline__ bf16x8 pack_bf16x8(f32x4 a, f32x4 b) {
     return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// Rows: a workgroup has NW = RS * NS waves.  Wave w owns query-row groups
+// Attention of the query rows of (sequence b, kv head h) over the keys
+// [tok_lo, tok_hi) of the sequence; the result of each row r = qi*g + gi goes to
+// sink.row (normalised output) and sink.stats (exp sum and log2-domain max).
+// ctx is already clamped to the page row's capacity; bt_row is the sequence's
+// page row (block-table row or kv_page_indices window).  Every thread of the
+// workgroup calls this with the same arguments (it synchronises internally).
+// The workgroup has NW = RS * NS waves.  Wave w owns query-row groups
 // [rs*MTPW, (rs+1)*MTPW) (rs = w % RS, 16 rows per group) and the steps
-// ns, ns+NS, ... of the slot (ns = w / RS).  Waves of the same rs merge their
+// ns, ns+NS, ... of the range (ns = w / RS).  Waves of the same rs merge their
 // online-softmax states through LDS at the end.
-template <int MTPW, int RS, int NS, bool PER_TOKEN>
-__global__ __launch_bounds__(RS * NS * 64) void pa_decode_partition_kernel(const DecodeParams p) {
+template <int MTPW, int RS, int NS, bool PER_TOKEN, class Sink>
+__device__ __forceinline__ void attend_range(const DecodeParams &p, const int b, const int h, const int ctx,
+                                             const int tok_lo, const int tok_hi, const int32_t *bt_row,
+                                             const Sink &sink) {
     constexpr int D = kHeadDim;
     constexpr int NW = RS * NS;
     const int tid = threadIdx.x;
@@ -137,41 +165,12 @@ __global__ __launch_bounds__(RS * NS * 64) void pa_decode_partition_kernel(const
     const int ns = wave / RS;
     const int l16 = lane & 15;
     const int kg = lane >> 4;
-    const int b = blockIdx.x;
-    const int h = blockIdx.y;
-    const int z = blockIdx.z;
     const int bs = 1 << p.bs_log2;
 
-    // ---- slot -> token range (integer planner, bit-exact with the oracle)
-    int64_t ctx64 = p.ctx[b];
-    const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
-    ctx64 = ctx64 < 0 ? 0 : (ctx64 > cap ? cap : ctx64);
-    const int ctx = (int)ctx64;
-    const int T = (ctx + kPartition - 1) / kPartition;
-    int seq_start = 0;
-    if (p.sw > 0) seq_start = max(ctx - p.ql - p.sw, 0);
-    const int first_tile = seq_start / kPartition;
-    const int vis = T - first_tile;
-    const int pps = vis > 0 ? (vis + p.max_parts - 1) / p.max_parts : 0;
-    const int plo = first_tile + z * pps;
-    const int phi = min(plo + pps, T);
-    int tok_lo = plo * kPartition;
-    const int tok_hi = min(phi * kPartition, ctx);
-    if (tok_lo < seq_start) tok_lo = seq_start & ~(kGroup - 1);
-
-    float *es = p.exp_sums + b * p.s_es_seq + h * p.s_es_head + z * p.s_es_part;
-    float *ml = p.max_logits + b * p.s_es_seq + h * p.s_es_head + z * p.s_es_part;
-    uint16_t *to = p.tmp_out + b * p.s_to_seq + h * p.s_to_head + z * p.s_to_part;
-
-    if (tok_lo >= tok_hi) {  // empty slot (kernels/pa_decode_fp8.py:2591-2598)
-        if (!p.direct) {
-            for (int r = tid; r < p.eqgs; r += NW * 64) {
-                es[r] = 0.0f;
-                ml[r] = -INFINITY;
-            }
-        }
+    if (tok_lo >= tok_hi) {  // empty range (kernels/pa_decode_fp8.py:2591-2598)
+        for (int r = tid; r < p.eqgs; r += NW * 64) sink.stats(r, 0.0f, -INFINITY);
         const float zero8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int i = tid; i < p.eqgs * (D / 8); i += NW * 64) emit_row<8>(p, to, b, h, i / (D / 8), (i % (D / 8)) * 8, zero8);
+        for (int i = tid; i < p.eqgs * (D / 8); i += NW * 64) sink.row(i / (D / 8), (i % (D / 8)) * 8, zero8);
         return;
     }
 
@@ -226,7 +225,6 @@ __global__ __launch_bounds__(RS * NS * 64) void pa_decode_partition_kernel(const
     const int ngroups = (tok_hi - tok_lo + kGroup - 1) / kGroup;
     const int nsteps = (ngroups + 3) / 4;
     const int last_group = tok_lo + (ngroups - 1) * kGroup;
-    const int32_t *bt_row = p.bt + (int64_t)b * p.s_bt_seq;
     const uint8_t *kc_h = p.kc + (int64_t)h * p.s_k_head;
     const uint8_t *vc_h = p.vc + (int64_t)h * p.s_v_head;
     const int kchunk = bs * 16;  // bytes between 16-dim chunks of one (block, head)
@@ -398,12 +396,9 @@ __global__ __launch_bounds__(RS * NS * 64) void pa_decode_partition_kernel(const
                 for (int m = 0; m < 8; ++m) {
                     const f32x4 v = o[mg][m] * inv;
                     const float v4[4] = {v[0], v[1], v[2], v[3]};
-                    emit_row<4>(p, to, b, h, r, 16 * m + 4 * kg, v4);
+                    sink.row(r, 16 * m + 4 * kg, v4);
                 }
-                if (kg == 0 && !p.direct) {
-                    es[r] = L;
-                    ml[r] = L > 0.f ? m_run[mg] * kLn2 : -INFINITY;
-                }
+                if (kg == 0) sink.stats(r, L, m_run[mg]);
             }
         }
     } else {
@@ -450,16 +445,197 @@ __global__ __launch_bounds__(RS * NS * 64) void pa_decode_partition_kernel(const
                         for (int j = 0; j < NS; ++j) a += s_o[j * RS + mrs][n][d0 + e0 + j2] * f[j];
                         v8[j2] = a * inv;
                     }
-                    emit_row<8>(p, to, b, h, r, d0 + e0, v8);
+                    sink.row(r, d0 + e0, v8);
                 }
-                if (d0 == 0 && !p.direct) {
-                    es[r] = L;
-                    ml[r] = L > 0.f ? M * kLn2 : -INFINITY;
-                }
+                if (d0 == 0) sink.stats(r, L, M);
             }
             __syncthreads();
         }
     }
+}
+
+// Split-context decode: one workgroup per (sequence, kv head, partition slot).
+template <int MTPW, int RS, int NS, bool PER_TOKEN>
+__global__ __launch_bounds__(RS * NS * 64) void pa_decode_partition_kernel(const DecodeParams p) {
+    const int b = blockIdx.x;
+    const int h = blockIdx.y;
+    const int z = blockIdx.z;
+
+    // ---- slot -> token range (integer planner, bit-exact with the oracle)
+    int64_t ctx64 = p.ctx[b];
+    const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
+    ctx64 = ctx64 < 0 ? 0 : (ctx64 > cap ? cap : ctx64);
+    const int ctx = (int)ctx64;
+    const int T = (ctx + kPartition - 1) / kPartition;
+    int seq_start = 0;
+    if (p.sw > 0) seq_start = max(ctx - p.ql - p.sw, 0);
+    const int first_tile = seq_start / kPartition;
+    const int vis = T - first_tile;
+    const int pps = vis > 0 ? (vis + p.max_parts - 1) / p.max_parts : 0;
+    const int plo = first_tile + z * pps;
+    const int phi = min(plo + pps, T);
+    int tok_lo = plo * kPartition;
+    const int tok_hi = min(phi * kPartition, ctx);
+    if (tok_lo < seq_start) tok_lo = seq_start & ~(kGroup - 1);
+
+    const SlotSink sink{p,
+                        p.tmp_out + b * p.s_to_seq + h * p.s_to_head + z * p.s_to_part,
+                        p.exp_sums + b * p.s_es_seq + h * p.s_es_head + z * p.s_es_part,
+                        p.max_logits + b * p.s_es_seq + h * p.s_es_head + z * p.s_es_part,
+                        b,
+                        h};
+    attend_range<MTPW, RS, NS, PER_TOKEN>(p, b, h, ctx, tok_lo, tok_hi, p.bt + (int64_t)b * p.s_bt_seq, sink);
+}
+
+// ---------------------------------------------------------------- worklist path
+struct WorklistParams {
+    DecodeParams kv;  // caches, query, scales, shape; bt / max_blocks / partials unused
+    const int32_t *work_indptr;
+    const int32_t *work_info;
+    const int32_t *kv_page_indices;
+    const int32_t *kv_indptr;
+    const int32_t *partition_indptr;
+    float *po;
+    float *pl;
+    void *out;
+    int64_t s_out_seq, s_out_head;
+    int64_t s_po_row, s_pl_row;
+    int32_t batch, num_kv_heads, num_pages, max_work, partial_rows, output_rows, out_dtype;
+};
+
+// Where a work's rows go: output[qo_start + qi, qhead] when the work holds its
+// whole sequence (pidx < 0), else the f32 partial row pidx + ql + qi plus its
+// log-sum-exp (kernels/pa_decode_fp8.py:1612-1643).
+struct WorkSink {
+    const WorklistParams &w;
+    int h, qo_start, pidx;
+
+    template <int N>
+    __device__ __forceinline__ void row(int r, int d0, const float (&v)[N]) const {
+        const int g = w.kv.g;
+        const int qi = r / g, qhead = h * g + (r - qi * g);
+        if (pidx < 0) {
+            store_out<N>(w.out, w.out_dtype, (int64_t)(qo_start + qi) * w.s_out_seq + qhead * w.s_out_head + d0, v);
+            return;
+        }
+        float *dst = w.po + (int64_t)(pidx + w.kv.ql + qi) * w.s_po_row + qhead * kHeadDim + d0;
+#pragma unroll
+        for (int j = 0; j < N; j += 4) *reinterpret_cast<float4 *>(dst + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
+    }
+    __device__ __forceinline__ void stats(int r, float L, float m2) const {
+        if (pidx < 0) return;
+        const int g = w.kv.g;
+        const int qi = r / g, qhead = h * g + (r - qi * g);
+        w.pl[(int64_t)(pidx + w.kv.ql + qi) * w.s_pl_row + qhead] = L > 0.f ? m2 * kLn2 + __logf(L) : -INFINITY;
+    }
+};
+
+// Persistent decode over the get_pa_metadata_v1 worklist: workgroup c runs the
+// works [work_indptr[c], work_indptr[c+1]) one after another
+// (kernels/pa_decode_fp8.py:941-1721).  Every field read from the worklist is
+// range-checked, so a malformed or overflowed worklist skips work instead of
+// touching memory outside the tensors.
+template <int MTPW, int RS, int NS, bool PER_TOKEN>
+__global__ __launch_bounds__(RS * NS * 64, 2) void pa_decode_worklist_kernel(const WorklistParams w) {
+    const DecodeParams &p = w.kv;
+    const int c = blockIdx.x;
+    const int wbeg = max(__builtin_amdgcn_readfirstlane(w.work_indptr[c]), 0);
+    const int wend = min(__builtin_amdgcn_readfirstlane(w.work_indptr[c + 1]), w.max_work);
+    for (int wi = wbeg; wi < wend; ++wi) {
+        const int32_t *info = w.work_info + (int64_t)wi * 8;
+        const int b = __builtin_amdgcn_readfirstlane(info[0]);
+        const int pidx = __builtin_amdgcn_readfirstlane(info[1]);
+        const int qo_start = __builtin_amdgcn_readfirstlane(info[2]);
+        const int kv_start = __builtin_amdgcn_readfirstlane(info[4]);
+        const int kv_end = __builtin_amdgcn_readfirstlane(info[5]);
+        const int qh_start = __builtin_amdgcn_readfirstlane(info[7]) & 0xffff;
+        const int h = qh_start / p.g;
+        if (b < 0 || b >= w.batch || h >= w.num_kv_heads) continue;
+        if (pidx < 0 ? (qo_start < 0 || qo_start > w.output_rows - p.ql)
+                     : (pidx > w.partial_rows - 2 * p.ql))
+            continue;
+        const int page0 = __builtin_amdgcn_readfirstlane(w.kv_indptr[b]);
+        const int page1 = __builtin_amdgcn_readfirstlane(w.kv_indptr[b + 1]);
+        if (page0 < 0 || page1 < page0 || page1 > w.num_pages) continue;
+        int64_t ctx64 = p.ctx[b];
+        const int64_t cap = (int64_t)(page1 - page0) << p.bs_log2;
+        ctx64 = ctx64 < 0 ? 0 : (ctx64 > cap ? cap : ctx64);
+        const int ctx = (int)ctx64;
+        const int pbase = __builtin_amdgcn_readfirstlane(w.partition_indptr[b]);
+        const int64_t lp0 = max((int64_t)kv_start - pbase, (int64_t)0);
+        const int64_t lp1 = (int64_t)kv_end - pbase;
+        const int tok_lo = (int)min(lp0 * kPartition, (int64_t)ctx);
+        const int tok_hi = (int)max(min(lp1 * kPartition, (int64_t)ctx), (int64_t)tok_lo);
+        const WorkSink sink{w, h, qo_start, pidx};
+        attend_range<MTPW, RS, NS, PER_TOKEN>(p, b, h, ctx, tok_lo, tok_hi, w.kv_page_indices + page0, sink);
+    }
+}
+
+struct ReduceV1Params {
+    void *out;
+    float *final_lse;
+    const float *po;
+    const float *pl;
+    const int32_t *reduce_indptr;
+    const int32_t *final_map;
+    const int32_t *partial_map;
+    int64_t s_po_row, s_po_head, s_pl_row, s_pl_head, s_out_row, s_out_head, s_lse_row, s_lse_head;
+    int32_t num_groups, num_heads, max_qlen, partial_rows, output_rows, partial_map_len, out_dtype;
+};
+
+// Merge of the partials of one (reduce group, query row, head): one wave, lane owns
+// head dims 2*lane and 2*lane+1.  Weights exp(lse_j - LSE) with LSE the
+// log-sum-exp of the partials' log-sum-exps.
+__global__ __launch_bounds__(64) void pa_reduce_v1_kernel(const ReduceV1Params p) {
+    const int lane = threadIdx.x;
+    const int grp = blockIdx.x, hd = blockIdx.y, qi = blockIdx.z;
+    const int j0 = max(p.reduce_indptr[grp], 0);
+    const int j1 = min(p.reduce_indptr[grp + 1], p.partial_map_len);
+    if (j0 >= j1) return;
+    const int qo_start = p.final_map[2 * grp];
+    const int qo_end = p.final_map[2 * grp + 1];
+    if (qi >= qo_end - qo_start || qo_start < 0 || qo_start + qi >= p.output_rows) return;
+
+    float mloc = -INFINITY;
+    for (int j = j0 + lane; j < j1; j += 64) {
+        const int row = p.partial_map[j] + qi;
+        if (row >= 0 && row < p.partial_rows) mloc = fmaxf(mloc, p.pl[row * p.s_pl_row + hd * p.s_pl_head]);
+    }
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) mloc = fmaxf(mloc, shfl_xor_f(mloc, sh));
+    const float Ms = mloc == -INFINITY ? 0.0f : mloc;
+    float wl = 0.f;
+    for (int j = j0 + lane; j < j1; j += 64) {
+        const int row = p.partial_map[j] + qi;
+        if (row >= 0 && row < p.partial_rows) wl += fast_exp2((p.pl[row * p.s_pl_row + hd * p.s_pl_head] - Ms) * kLog2e);
+    }
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) wl += shfl_xor_f(wl, sh);
+    const float inv = wl > 0.f ? 1.0f / wl : 0.0f;
+
+    float a0 = 0.f, a1 = 0.f;
+    for (int j = j0; j < j1; ++j) {
+        const int row = p.partial_map[j] + qi;
+        if (row < 0 || row >= p.partial_rows) continue;
+        const float wgt = fast_exp2((p.pl[row * p.s_pl_row + hd * p.s_pl_head] - Ms) * kLog2e) * inv;
+        if (wgt != 0.f) {
+            const float2 two = *reinterpret_cast<const float2 *>(p.po + row * p.s_po_row + hd * p.s_po_head + 2 * lane);
+            a0 += wgt * two.x;
+            a1 += wgt * two.y;
+        }
+    }
+    const int64_t orow = qo_start + qi;
+    const int64_t off = orow * p.s_out_row + hd * p.s_out_head + 2 * lane;
+    if (p.out_dtype == PA_FP8_F32) {
+        *reinterpret_cast<float2 *>(reinterpret_cast<float *>(p.out) + off) = make_float2(a0, a1);
+    } else {
+        const uint32_t pk = p.out_dtype == PA_FP8_F16
+                                ? uint32_t(f32_to_f16_bits(a0)) | (uint32_t(f32_to_f16_bits(a1)) << 16)
+                                : uint32_t(f32_to_bf16_bits(a0)) | (uint32_t(f32_to_bf16_bits(a1)) << 16);
+        *reinterpret_cast<uint32_t *>(reinterpret_cast<uint16_t *>(p.out) + off) = pk;
+    }
+    if (p.final_lse != nullptr && lane == 0)
+        p.final_lse[orow * p.s_lse_row + hd * p.s_lse_head] = wl > 0.f ? Ms + __logf(wl) : -INFINITY;
 }
 
 // Log-sum-exp merge of the P partials of one (sequence, kv head, query row):
@@ -541,6 +717,22 @@ hipError_t dispatch_decode(const DecodeParams &p, int mtp, dim3 grid, hipStream_
     case 2: return launch_decode<1, 2, 2, PT>(p, grid, s);
     case 3: return launch_decode<1, 3, 1, PT>(p, grid, s);
     default: return launch_decode<1, 4, 1, PT>(p, grid, s);
+    }
+}
+
+template <int MTPW, int RS, int NS, bool PT>
+hipError_t launch_worklist(const WorklistParams &w, dim3 grid, hipStream_t s) {
+    hipLaunchKernelGGL((pa_decode_worklist_kernel<MTPW, RS, NS, PT>), grid, dim3(RS * NS * 64), 0, s, w);
+    return hipGetLastError();
+}
+
+template <bool PT>
+hipError_t dispatch_worklist(const WorklistParams &w, int mtp, dim3 grid, hipStream_t s) {
+    switch (mtp) {
+    case 1: return launch_worklist<1, 1, 4, PT>(w, grid, s);
+    case 2: return launch_worklist<1, 2, 2, PT>(w, grid, s);
+    case 3: return launch_worklist<1, 3, 1, PT>(w, grid, s);
+    default: return launch_worklist<1, 4, 1, PT>(w, grid, s);
     }
 }
 
@@ -714,6 +906,138 @@ int pa_fp8_lse_reduce(const pa_fp8_reduce_args *a, void *stream) {
     case PA_FP8_F16: hipLaunchKernelGGL(pa_lse_reduce_kernel<PA_FP8_F16>, grid, dim3(64), 0, s, p); break;
     default: hipLaunchKernelGGL(pa_lse_reduce_kernel<PA_FP8_BF16>, grid, dim3(64), 0, s, p); break;
     }
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
+}
+
+int pa_fp8_decode_worklist(const pa_fp8_worklist_args *a, void *stream) {
+    if (!a) return PA_FP8_ERR_NULL_POINTER;
+    if (a->batch_size < 0 || a->num_kv_heads <= 0 || a->query_group_size <= 0 || a->query_length <= 0)
+        return PA_FP8_ERR_SHAPE;
+    if (a->head_dim != kHeadDim) return PA_FP8_ERR_HEAD_DIM;
+    const int bs_log2 = log2_pow2(a->block_size);
+    if (bs_log2 < 4) return PA_FP8_ERR_BLOCK_SIZE;
+    const int eqgs = a->query_length * a->query_group_size;
+    if (eqgs < 1 || eqgs > 64) return PA_FP8_ERR_GROUP;
+    if (a->query_dtype != PA_FP8_BF16 && a->query_dtype != PA_FP8_F16) return PA_FP8_ERR_DTYPE;
+    if (a->out_dtype != PA_FP8_BF16 && a->out_dtype != PA_FP8_F16 && a->out_dtype != PA_FP8_F32) return PA_FP8_ERR_DTYPE;
+    if (a->num_cu < 0 || a->max_work < 0 || a->partial_rows < 0 || a->output_rows < 0 || a->num_pages < 0)
+        return PA_FP8_ERR_SHAPE;
+    if (a->batch_size == 0 || a->num_cu == 0) return PA_FP8_OK;
+    if (!a->output || !a->query || !a->key_cache || !a->value_cache || !a->context_lengths || !a->key_scale ||
+        !a->value_scale || !a->work_indptr || !a->work_info || !a->kv_indptr || !a->partition_indptr)
+        return PA_FP8_ERR_NULL_POINTER;
+    if (a->num_pages > 0 && !a->kv_page_indices) return PA_FP8_ERR_NULL_POINTER;
+    if (a->partial_rows > 0 && (!a->partial_output || !a->partial_lse)) return PA_FP8_ERR_NULL_POINTER;
+    if (a->num_blocks <= 0) return PA_FP8_ERR_SHAPE;
+    if (!aligned16(a->key_cache) || !aligned16(a->value_cache) || !aligned16(a->query) || !aligned16(a->output))
+        return PA_FP8_ERR_SHAPE;
+    if (a->partial_rows > 0 && (!aligned16(a->partial_output) || (a->stride_po_row & 3))) return PA_FP8_ERR_SHAPE;
+    if ((a->stride_k_block | a->stride_k_head | a->stride_v_block | a->stride_v_head) & 15) return PA_FP8_ERR_SHAPE;
+    if ((a->stride_q_seq | a->stride_q_head) & 7) return PA_FP8_ERR_SHAPE;
+    const int esz = a->out_dtype == PA_FP8_F32 ? 4 : 2;
+    if (((a->stride_out_seq | a->stride_out_head) * esz) & 15) return PA_FP8_ERR_SHAPE;
+    if (a->per_token_kv) {
+        if (!aligned16(a->key_scale) || !aligned16(a->value_scale)) return PA_FP8_ERR_SHAPE;
+        if ((a->stride_ks_block | a->stride_ks_head) & 3) return PA_FP8_ERR_SHAPE;
+    }
+
+    WorklistParams w = {};
+    DecodeParams &p = w.kv;
+    p.query = reinterpret_cast<const uint16_t *>(a->query);
+    p.kc = a->key_cache;
+    p.vc = a->value_cache;
+    p.ctx = a->context_lengths;
+    p.ks = a->key_scale;
+    p.vs = a->value_scale;
+    p.s_q_seq = a->stride_q_seq;
+    p.s_q_head = a->stride_q_head;
+    p.s_k_block = a->stride_k_block;
+    p.s_k_head = a->stride_k_head;
+    p.s_v_block = a->stride_v_block;
+    p.s_v_head = a->stride_v_head;
+    p.s_ks_block = a->per_token_kv ? a->stride_ks_block : 0;
+    p.s_ks_head = a->per_token_kv ? a->stride_ks_head : 0;
+    p.g = a->query_group_size;
+    p.ql = a->query_length;
+    p.eqgs = eqgs;
+    p.bs_log2 = bs_log2;
+    p.num_blocks = a->num_blocks;
+    p.max_parts = 1;
+    p.sw = 0;
+    p.q_f16 = a->query_dtype == PA_FP8_F16;
+    p.qk_scale = a->softmax_scale * kLog2e;
+    w.work_indptr = a->work_indptr;
+    w.work_info = a->work_info;
+    w.kv_page_indices = a->kv_page_indices;
+    w.kv_indptr = a->kv_indptr;
+    w.partition_indptr = a->partition_indptr;
+    w.po = a->partial_output;
+    w.pl = a->partial_lse;
+    w.out = a->output;
+    w.s_out_seq = a->stride_out_seq;
+    w.s_out_head = a->stride_out_head;
+    w.s_po_row = a->stride_po_row;
+    w.s_pl_row = a->stride_pl_row;
+    w.batch = a->batch_size;
+    w.num_kv_heads = a->num_kv_heads;
+    w.num_pages = a->num_pages;
+    w.max_work = a->max_work;
+    w.partial_rows = a->partial_rows;
+    w.output_rows = a->output_rows;
+    w.out_dtype = a->out_dtype;
+
+    const dim3 grid(a->num_cu);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int mtp = (eqgs + 15) / 16;
+    const hipError_t err =
+        a->per_token_kv ? dispatch_worklist<true>(w, mtp, grid, s) : dispatch_worklist<false>(w, mtp, grid, s);
+    return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
+}
+
+int pa_fp8_reduce_v1(const pa_fp8_reduce_v1_args *a, void *stream) {
+    if (!a) return PA_FP8_ERR_NULL_POINTER;
+    if (a->head_dim != kHeadDim) return PA_FP8_ERR_HEAD_DIM;
+    if (a->num_groups < 0 || a->num_heads <= 0 || a->num_heads > 65535 || a->max_qlen <= 0 || a->max_qlen > 65535 ||
+        a->partial_rows < 0 || a->output_rows < 0 || a->partial_map_len < 0)
+        return PA_FP8_ERR_SHAPE;
+    if (a->out_dtype != PA_FP8_BF16 && a->out_dtype != PA_FP8_F16 && a->out_dtype != PA_FP8_F32) return PA_FP8_ERR_DTYPE;
+    // nothing to merge (an empty partial tensor also reports a NULL data pointer)
+    if (a->num_groups == 0 || a->partial_map_len == 0 || a->partial_rows == 0) return PA_FP8_OK;
+    if (!a->output || !a->partial_output || !a->partial_lse || !a->reduce_indptr || !a->reduce_final_map ||
+        !a->reduce_partial_map)
+        return PA_FP8_ERR_NULL_POINTER;
+    const int esz = a->out_dtype == PA_FP8_F32 ? 4 : 2;
+    if ((reinterpret_cast<uintptr_t>(a->output) & (2 * esz - 1)) || (reinterpret_cast<uintptr_t>(a->partial_output) & 7))
+        return PA_FP8_ERR_SHAPE;
+    if (((a->stride_out_row | a->stride_out_head) & 1) || ((a->stride_po_row | a->stride_po_head) & 1))
+        return PA_FP8_ERR_SHAPE;
+
+    ReduceV1Params p;
+    p.out = a->output;
+    p.final_lse = a->final_lse;
+    p.po = a->partial_output;
+    p.pl = a->partial_lse;
+    p.reduce_indptr = a->reduce_indptr;
+    p.final_map = a->reduce_final_map;
+    p.partial_map = a->reduce_partial_map;
+    p.s_po_row = a->stride_po_row;
+    p.s_po_head = a->stride_po_head;
+    p.s_pl_row = a->stride_pl_row;
+    p.s_pl_head = a->stride_pl_head;
+    p.s_out_row = a->stride_out_row;
+    p.s_out_head = a->stride_out_head;
+    p.s_lse_row = a->stride_lse_row;
+    p.s_lse_head = a->stride_lse_head;
+    p.num_groups = a->num_groups;
+    p.num_heads = a->num_heads;
+    p.max_qlen = a->max_qlen;
+    p.partial_rows = a->partial_rows;
+    p.output_rows = a->output_rows;
+    p.partial_map_len = a->partial_map_len;
+    p.out_dtype = a->out_dtype;
+    hipLaunchKernelGGL(pa_reduce_v1_kernel, dim3(a->num_groups, a->num_heads, a->max_qlen), dim3(64), 0,
+                       reinterpret_cast<hipStream_t>(stream), p);
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
 }

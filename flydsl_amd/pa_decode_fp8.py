@@ -22,6 +22,7 @@ import torch
 from . import _lib
 from .pa_decode_swa import _reduce_args, get_sw_max_context_partition_num  # noqa: F401
 from .pa_metadata import get_pa_metadata_info_v1, get_pa_metadata_v1
+from .pa_reduce import _reduce_v1_args
 
 KV_COMPUTE_BLOCK = 256  # tokens per context partition (kernels/pa_decode_fp8.py:36)
 _PA_METADATA_GRID_OVERSUB = 3  # kernels/pa_decode_fp8.py:37-40
@@ -234,18 +235,29 @@ def _validate_scale(name: str, scale: torch.Tensor, per_token: bool, key_cache: 
 
 class _Plan:
     """Prepared launch of one decode step: the C-ABI argument blocks plus the
-    tensors they point into that the launcher allocated itself.  ``rargs`` is
-    None when the partition kernel writes the output directly (one slot)."""
+    tensors they point into that the launcher allocated itself.
 
-    __slots__ = ("dargs", "rargs", "tag", "keepalive", "max_parts")
+    Split-context paths: ``dargs`` (partition kernel) and ``rargs`` (LSE reduce;
+    None when the partition kernel writes the output directly).  Persistent
+    path: ``wargs`` (worklist kernel) and ``vargs`` (reduce of split works).
+    ``cacheable`` is False when the plan holds metadata the launcher derived from
+    context-length values, which a later call with the same tensors may change."""
 
-    def __init__(self, dargs, rargs, tag, keepalive, max_parts):
-        self.dargs, self.rargs, self.tag, self.keepalive, self.max_parts = dargs, rargs, tag, keepalive, max_parts
+    __slots__ = ("dargs", "rargs", "wargs", "vargs", "tag", "keepalive", "max_parts", "cacheable", "launches")
+
+    def __init__(self, tag, keepalive, max_parts=None, dargs=None, rargs=None, wargs=None, vargs=None, cacheable=True):
+        self.dargs, self.rargs, self.wargs, self.vargs = dargs, rargs, wargs, vargs
+        self.tag, self.keepalive, self.max_parts, self.cacheable = tag, keepalive, max_parts, cacheable
+        self.launches = [
+            (fn, a)
+            for fn, a in ((_lib.decode_partitions, dargs), (_lib.lse_reduce, rargs), (_lib.decode_worklist, wargs),
+                          (_lib.reduce_v1, vargs))
+            if a is not None
+        ]
 
     def launch(self, stream_handle: int) -> str:
-        _lib.decode_partitions(self.dargs, stream_handle)
-        if self.rargs is not None:
-            _lib.lse_reduce(self.rargs, stream_handle)
+        for fn, a in self.launches:
+            fn(a, stream_handle)
         return self.tag
 
 
@@ -355,7 +367,130 @@ def _partitioned_plan(
         rargs = None
     else:
         rargs = _reduce_args(output_5d, exp_sums, max_logits, temporary_output, max_parts, out_dtype)
-    return _Plan(dargs, rargs, tag, (exp_sums, max_logits, temporary_output, key_scale, value_scale), max_parts)
+    return _Plan(tag, (exp_sums, max_logits, temporary_output, key_scale, value_scale), max_parts, dargs=dargs,
+                 rargs=rargs)
+
+
+_METADATA_KEYS = ("work_indptr", "work_info_flat", "partition_indptr", "reduce_indptr", "reduce_final_map",
+                  "reduce_partial_map", "partial_output", "partial_lse")
+
+
+def _worklist_plan(
+    output,
+    query,
+    key_cache,
+    value_cache,
+    context_lengths,
+    kv_page_indices,
+    kv_indptr,
+    metadata,
+    softmax_scale,
+    key_scale,
+    value_scale,
+    per_token_kv,
+    is_graph_capturing,
+) -> _Plan:
+    """Persistent path (kernels/pa_decode_fp8.py:3123-3202): the worklist decode
+    over ``metadata`` and the merge of the split works' partials."""
+    dev = query.device
+    batch_size = context_lengths.shape[0]
+    num_query_heads = query.shape[1]
+    num_kv_heads = key_cache.shape[1]
+    head_size = query.shape[-1]
+    query_length = query.shape[0] // batch_size
+    block_size = key_cache.shape[-2]
+    if kv_page_indices is None or kv_indptr is None:
+        raise ValueError(
+            f"pa_decode_ps_launch: block_size={block_size} runs the persistent worklist path, which reads pages "
+            "through `kv_page_indices` and `kv_indptr`."
+        )
+    _check_int32("kv_page_indices", kv_page_indices, 1)
+    _check_int32("kv_indptr", kv_indptr, 1)
+    if kv_indptr.shape[0] != batch_size + 1 or not kv_indptr.is_contiguous() or not kv_page_indices.is_contiguous():
+        raise ValueError(f"kv_indptr must be a contiguous [{batch_size + 1}] tensor and kv_page_indices contiguous")
+    cacheable = True
+    if metadata is None:
+        if is_graph_capturing:
+            raise ValueError(
+                "CUDA graph capture requires precomputed `metadata`; "
+                "call `get_pa_metadata()` before capture and pass it via `metadata=`."
+            )
+        metadata = get_pa_metadata(query, key_cache, context_lengths, kv_indptr, num_query_heads, num_kv_heads)
+        cacheable = False
+    missing = [k for k in _METADATA_KEYS + ("num_sm",) if k not in metadata]
+    if missing:
+        raise ValueError(f"metadata is missing {missing}; build it with get_pa_metadata()")
+    num_sm = int(metadata["num_sm"])
+    work_indptr, work_info = metadata["work_indptr"], metadata["work_info_flat"]
+    partition_indptr = metadata["partition_indptr"]
+    po, pl = metadata["partial_output"], metadata["partial_lse"]
+    for name in ("work_indptr", "work_info_flat", "partition_indptr", "reduce_indptr", "reduce_final_map",
+                 "reduce_partial_map"):
+        t = metadata[name]
+        if t.dtype != torch.int32 or not t.is_contiguous() or t.device != dev:
+            raise ValueError(f"metadata[{name!r}] must be a contiguous int32 tensor on {dev}")
+    if work_indptr.numel() != num_sm + 1 or work_info.numel() % 8 != 0:
+        raise ValueError(f"metadata work_indptr has {work_indptr.numel()} entries for num_sm={num_sm}")
+    if partition_indptr.numel() != batch_size + 1:
+        raise ValueError(f"metadata partition_indptr must have {batch_size + 1} entries")
+    if (po.dim() != 4 or po.dtype != torch.float32 or tuple(po.shape[1:]) != (1, num_query_heads, head_size)
+            or po.stride()[1:] != (num_query_heads * head_size, head_size, 1) or po.shape[0] < query_length):
+        raise ValueError(f"metadata partial_output must be float32 [rows, 1, {num_query_heads}, {head_size}], rows >= ql")
+    if pl.dim() != 4 or pl.dtype != torch.float32 or tuple(pl.shape) != (po.shape[0], 1, num_query_heads, 1):
+        raise ValueError(f"metadata partial_lse must be float32 [{po.shape[0]}, 1, {num_query_heads}, 1]")
+    out_dtype = _get_output_dtype_str(output)
+
+    w = _lib.WorklistArgs()
+    w.output = output.data_ptr()
+    w.partial_output = po.data_ptr()
+    w.partial_lse = pl.data_ptr()
+    w.query = query.data_ptr()
+    w.key_cache = key_cache.data_ptr()
+    w.value_cache = value_cache.data_ptr()
+    w.context_lengths = context_lengths.data_ptr()
+    w.key_scale = key_scale.data_ptr()
+    w.value_scale = value_scale.data_ptr()
+    w.work_indptr = work_indptr.data_ptr()
+    w.work_info = work_info.data_ptr()
+    w.kv_page_indices = kv_page_indices.data_ptr()
+    w.kv_indptr = kv_indptr.data_ptr()
+    w.partition_indptr = partition_indptr.data_ptr()
+    w.stride_q_seq, w.stride_q_head = query.stride(0), query.stride(1)
+    w.stride_k_block, w.stride_k_head = key_cache.stride(0), key_cache.stride(1)
+    w.stride_v_block, w.stride_v_head = value_cache.stride(0), value_cache.stride(1)
+    w.stride_out_seq, w.stride_out_head = output.stride(0), output.stride(1)
+    w.stride_po_row, w.stride_pl_row = po.stride(0), pl.stride(0)
+    if per_token_kv:
+        w.stride_ks_block, w.stride_ks_head = key_scale.stride(0), key_scale.stride(1)
+    w.batch_size = batch_size
+    w.num_kv_heads = num_kv_heads
+    w.query_group_size = num_query_heads // num_kv_heads
+    w.query_length = query_length
+    w.head_dim = head_size
+    w.block_size = block_size
+    w.num_blocks = key_cache.shape[0]
+    w.num_pages = kv_page_indices.shape[0]
+    w.num_cu = num_sm
+    w.max_work = work_info.numel() // 8
+    w.partial_rows = po.shape[0]
+    w.output_rows = output.shape[0]
+    w.per_token_kv = 1 if per_token_kv else 0
+    w.query_dtype = _lib.PA_FP8_F16 if query.dtype == torch.float16 else _lib.PA_FP8_BF16
+    w.out_dtype = {"bf16": _lib.PA_FP8_BF16, "f16": _lib.PA_FP8_F16, "f32": _lib.PA_FP8_F32}[out_dtype]
+    w.softmax_scale = float(softmax_scale)
+    # no partial rows past the first query_length: nothing was split, so there is nothing to merge
+    v = None
+    if po.shape[0] > query_length:
+        v = _reduce_v1_args(po[query_length:], pl[query_length:], metadata["reduce_indptr"],
+                            metadata["reduce_final_map"], metadata["reduce_partial_map"], query_length, output)
+    keep = (metadata, key_scale, value_scale, kv_page_indices, kv_indptr)
+    return _Plan("ps_split_reduce", keep, wargs=w, vargs=v, cacheable=cacheable)
+
+
+def _mkey(metadata):
+    if metadata is None:
+        return None
+    return tuple((k, _tkey(metadata[k])) for k in _METADATA_KEYS if k in metadata) + (("num_sm", metadata.get("num_sm")),)
 
 
 def pa_decode_ps_launch(
@@ -381,20 +516,25 @@ def pa_decode_ps_launch(
 ) -> str:
     """Paged-attention decode over an fp8 e4m3fn KV cache (kernels/pa_decode_fp8.py:2812-3202).
 
-    Routing follows the reference: ``sliding_window > 0`` -> sliding-window
-    split-context path; block sizes 16 / 64 -> small-block split-context path;
-    other block sizes -> partitioned path over the same kernels (the reference
-    routes them to its persistent worklist kernel).  Every path is one
-    partition kernel plus the log-sum-exp reduce and writes ``output`` in place.
-    ``kv_page_indices`` / ``kv_indptr`` / ``metadata`` are accepted for
-    signature compatibility; the partition kernels read ``block_tables``.
+    Routing follows the reference:
 
-    A call whose tensors (pointers, shapes, strides, dtypes), scalars and stream
-    all match an earlier call reuses that call's prepared argument blocks (and
-    the intermediates it allocated), so steady-state decode pays two C calls.
+    * ``sliding_window > 0``: sliding-window split-context path (partition
+      kernel + log-sum-exp reduce; every block size), reading ``block_tables``;
+    * block sizes 16 / 64: small-block split-context path, reading ``block_tables``;
+    * other block sizes: the persistent path -- the worklist kernel over
+      ``metadata`` (computed with ``get_pa_metadata`` when absent, which
+      synchronises once) reading pages through ``kv_page_indices`` /
+      ``kv_indptr``, then the merge of the split works' partials.
+
+    ``output`` is written in place.  A call whose tensors (pointers, shapes,
+    strides, dtypes), metadata tensors, scalars and stream all match an earlier
+    call reuses that call's prepared argument blocks (and the intermediates it
+    allocated), so steady-state decode pays two C calls.  Plans built on
+    metadata the launcher computed itself are not reused, because that metadata
+    depends on the context-length values.
 
     Returns the path tag: "ps_sw_partitioned" / "ps_sw_fused_partitioned",
-    "ps_small_block" or "ps_partitioned".
+    "ps_small_block" or "ps_split_reduce".
     """
     dev = query.device
     s = stream if stream is not None else torch.cuda.current_stream(dev)
@@ -418,6 +558,9 @@ def pa_decode_ps_launch(
             _tkey(exp_sums),
             _tkey(max_logits),
             _tkey(temporary_output),
+            _tkey(kv_page_indices),
+            _tkey(kv_indptr),
+            _mkey(metadata),
         )
         plan = _PLAN_CACHE.get(key)
         if plan is not None:
@@ -426,9 +569,9 @@ def pa_decode_ps_launch(
     plan = _build_plan(
         output, query, key_cache, value_cache, context_lengths, softmax_scale, key_scale, value_scale,
         sliding_window, block_tables, max_context_partition_num, exp_sums, max_logits, temporary_output,
-        is_graph_capturing,
+        is_graph_capturing, kv_page_indices=kv_page_indices, kv_indptr=kv_indptr, metadata=metadata,
     )
-    if key is not None:
+    if key is not None and plan.cacheable:
         _PLAN_CACHE[key] = plan
         if len(_PLAN_CACHE) > _PLAN_CACHE_SIZE:
             _PLAN_CACHE.popitem(last=False)
@@ -438,7 +581,7 @@ def pa_decode_ps_launch(
 def _build_plan(
     output, query, key_cache, value_cache, context_lengths, softmax_scale, key_scale, value_scale,
     sliding_window, block_tables, max_context_partition_num, exp_sums, max_logits, temporary_output,
-    is_graph_capturing,
+    is_graph_capturing, kv_page_indices=None, kv_indptr=None, metadata=None,
 ) -> _Plan:
     if query.dim() != 3:
         raise ValueError(f"query must be [num_seqs*query_length, num_heads, head_dim], got {tuple(query.shape)}")
@@ -483,6 +626,10 @@ def _build_plan(
                     ("context_lengths", context_lengths), ("key_scale", key_scale), ("value_scale", value_scale)):
         if t.device != dev:
             raise ValueError(f"`{name}` is on {t.device}, expected {dev}")
+    small = block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES
+    if sliding_window <= 0 and not small:
+        return _worklist_plan(output, query, key_cache, value_cache, context_lengths, kv_page_indices, kv_indptr,
+                              metadata, softmax_scale, key_scale, value_scale, per_token_kv, is_graph_capturing)
     if block_tables is None:
         raise ValueError(
             f"pa_decode_ps_launch: block_size={block_size} requires `block_tables` "
@@ -502,10 +649,7 @@ def _build_plan(
         tag = "ps_sw_fused_partitioned" if max_context_partition_num <= 1 else "ps_sw_partitioned"
         path = "sliding-window"
     else:
-        small = block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES
-        tag = "ps_small_block" if small else "ps_partitioned"
-        path = "small-block PS" if small else "partitioned"
-        sliding_window = 0
+        tag, path = "ps_small_block", "small-block PS"
     return _partitioned_plan(output, query, key_cache, value_cache, context_lengths, block_tables, softmax_scale,
                              key_scale, value_scale, per_token_kv, sliding_window, max_context_partition_num,
                              exp_sums, max_logits, temporary_output, is_graph_capturing, path, tag)

@@ -8,6 +8,8 @@ Builds seeded inputs in the tensor formats ``pa_decode_ps_launch`` consumes:
 * key/value scales: per-tensor [1] (amax/448) or per-token [nb, Hkv, bs, 1]
 * block_tables int32 [B, max_blocks]: a random permutation of the physical
   blocks, handed to the sequences in order; context_lengths int32 [B]
+* kv_page_indices / kv_indptr int32: the same pages as one flat list
+  (tests/kernels/test_pa.py:545-559), read by the persistent path
 
 K and V are drawn N(0,1) in float32 and quantised with scale = amax/448 and
 ``(x / scale).to(torch.float8_e4m3fn)`` -- the quantisers of
@@ -187,6 +189,10 @@ def build_workload(cfg: DecodeConfig, device, seed: int = 123, context_lengths: 
     q = torch.randn((cfg.batch * cfg.query_length, cfg.num_q_heads, HEAD_DIM), generator=gen, device=dev,
                     dtype=torch.float32).to(torch.bfloat16)
     kx, vt, ks, vs = build_kv_cache(nphys, cfg.num_kv_heads, cfg.block_size, cfg.per_token, dev, seed)
+    # flat page list of the persistent path (tests/kernels/test_pa.py:545-559)
+    pages = [(c + cfg.block_size - 1) // cfg.block_size for c in ctx]
+    kv_indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    kv_page_indices = np.concatenate([bt[b, : pages[b]] for b in range(cfg.batch)] + [np.zeros(0, np.int64)])
     return {
         "config": cfg,
         "query": q,
@@ -195,6 +201,8 @@ def build_workload(cfg: DecodeConfig, device, seed: int = 123, context_lengths: 
         "key_scale": ks,
         "value_scale": vs,
         "block_tables": torch.as_tensor(bt, dtype=torch.int32).to(dev),
+        "kv_page_indices": torch.as_tensor(kv_page_indices.astype(np.int32)).to(dev),
+        "kv_indptr": torch.as_tensor(kv_indptr).to(dev),
         "context_lengths": torch.as_tensor(ctx, dtype=torch.int32).to(dev),
         "context_list": list(ctx),
         "block_table_np": bt,

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define PA_FP8_ABI_VERSION 1
+#define PA_FP8_ABI_VERSION 2
 
 enum pa_fp8_status {
     PA_FP8_OK = 0,
@@ -134,6 +134,106 @@ typedef struct pa_fp8_reduce_args {
 } pa_fp8_reduce_args;
 
 int pa_fp8_lse_reduce(const pa_fp8_reduce_args *args, void *hip_stream);
+
+/*
+ * Persistent worklist decode: workgroup c (grid = num_cu) runs the works
+ * [work_indptr[c], work_indptr[c+1]) of the get_pa_metadata_v1 schedule.  Work w
+ * is work_info[w] = {batch, partial_qo_loc, qo_start, qo_end, kv_start, kv_end, 0,
+ * (qh_end << 16) | qh_start}; kv_start / kv_end are cumulative 256-token partition
+ * indices (sequence b's partitions start at partition_indptr[b]) and the kv head
+ * is qh_start / query_group_size.  A work attends its partitions' keys under the
+ * causal bound tok < ctx + 1 - ql + qi, reading sequence b's pages from
+ * kv_page_indices[kv_indptr[b] .. kv_indptr[b+1]).
+ *   partial_qo_loc <  0: the normalised rows go to output[qo_start + qi, qhead, :]
+ *                        (dtype out_dtype);
+ *   partial_qo_loc >= 0: f32 normalised rows go to
+ *                        partial_output[(partial_qo_loc + ql + qi) * stride_po_row + qhead * D + d]
+ *                        and the row's log-sum-exp (natural log; -inf when nothing is
+ *                        visible) to partial_lse[(partial_qo_loc + ql + qi) * stride_pl_row + qhead].
+ * Works whose batch, head or partial row fall outside the given sizes are skipped.
+ * Q rows are batch * ql + qi.  Caches, scales and query as for
+ * pa_fp8_decode_partitions (trans_v V layout, any power-of-two block size >= 16).
+ *
+ * Replaces the launcher of `compile_pa_decode_metadata`
+ * (kernels/pa_decode_fp8.py:941-1721, called at :3155-3187).
+ */
+typedef struct pa_fp8_worklist_args {
+    void *output;
+    float *partial_output;
+    float *partial_lse;
+    const void *query;
+    const uint8_t *key_cache;
+    const uint8_t *value_cache;
+    const int32_t *context_lengths;
+    const float *key_scale;
+    const float *value_scale;
+    const int32_t *work_indptr;      /* [num_cu + 1] */
+    const int32_t *work_info;        /* [max_work, 8] */
+    const int32_t *kv_page_indices;  /* flat pages of every sequence */
+    const int32_t *kv_indptr;        /* [B + 1] */
+    const int32_t *partition_indptr; /* [B + 1] cumulative ceil(ctx / 256) */
+    int64_t stride_q_seq, stride_q_head;
+    int64_t stride_k_block, stride_k_head;
+    int64_t stride_v_block, stride_v_head;
+    int64_t stride_out_seq, stride_out_head;
+    int64_t stride_po_row, stride_pl_row;
+    int64_t stride_ks_block, stride_ks_head;
+    int32_t batch_size;
+    int32_t num_kv_heads;
+    int32_t query_group_size;
+    int32_t query_length;
+    int32_t head_dim;
+    int32_t block_size;
+    int32_t num_blocks;          /* physical blocks in the caches (page entries are clamped into range) */
+    int32_t num_pages;           /* entries of kv_page_indices */
+    int32_t num_cu;              /* workgroups = work_indptr entries - 1 */
+    int32_t max_work;            /* rows of work_info */
+    int32_t partial_rows;        /* rows of partial_output / partial_lse */
+    int32_t output_rows;         /* rows of output (B * ql) */
+    int32_t per_token_kv;
+    int32_t query_dtype;
+    int32_t out_dtype;
+    float softmax_scale;
+} pa_fp8_worklist_args;
+
+int pa_fp8_decode_worklist(const pa_fp8_worklist_args *args, void *hip_stream);
+
+/*
+ * Merge of split works' partials (the role of aiter's pa_reduce_v1, called at
+ * kernels/pa_decode_fp8.py:3189-3200).  For every reduce group g with
+ * reduce_indptr[g] < reduce_indptr[g+1], qo range reduce_final_map[g] = {qo_start, qo_end},
+ * query row qi < min(qo_end - qo_start, max_qlen) and head h < num_heads:
+ *   rows s_j = reduce_partial_map[j] + qi, j in [reduce_indptr[g], reduce_indptr[g+1])
+ *   LSE = log sum_j exp(partial_lse[s_j, h]),  w_j = exp(partial_lse[s_j, h] - LSE)
+ *   output[qo_start + qi, h, :] = sum_j w_j * partial_output[s_j, h, :]
+ *   final_lse[qo_start + qi, h] = LSE (when final_lse is not NULL)
+ * A row whose partials are all -inf gets 0 (and LSE -inf).  partial_output /
+ * partial_lse point at the row the map's 0 refers to (the launcher passes
+ * partial_output[query_length:]).
+ */
+typedef struct pa_fp8_reduce_v1_args {
+    void *output;
+    float *final_lse;
+    const float *partial_output;
+    const float *partial_lse;
+    const int32_t *reduce_indptr;       /* [num_groups + 1] */
+    const int32_t *reduce_final_map;    /* [num_groups, 2] */
+    const int32_t *reduce_partial_map;  /* [partial_map_len] */
+    int64_t stride_po_row, stride_po_head;
+    int64_t stride_pl_row, stride_pl_head;
+    int64_t stride_out_row, stride_out_head;
+    int64_t stride_lse_row, stride_lse_head;
+    int32_t num_groups;
+    int32_t num_heads;
+    int32_t head_dim;
+    int32_t max_qlen;
+    int32_t partial_rows;        /* rows reachable from partial_output */
+    int32_t output_rows;
+    int32_t partial_map_len;
+    int32_t out_dtype;
+} pa_fp8_reduce_v1_args;
+
+int pa_fp8_reduce_v1(const pa_fp8_reduce_v1_args *args, void *hip_stream);
 
 /*
  * get_pa_metadata_v1 worklist scheduler, run on the device by one thread

@@ -12,7 +12,15 @@ expose to callers:
   ``(exp_sum, max_logit, normalised bf16 output)`` written by the small-block
   kernel (kernels/pa_decode_fp8.py:2291-2305, empty slot :2591-2598);
 * ``lse_reduce`` -- the log-sum-exp merge of those partials
-  (kernels/pa_decode_swa.py:954-1022).
+  (kernels/pa_decode_swa.py:954-1022);
+
+and the two halves of the persistent (worklist) path:
+
+* ``worklist_decode`` -- per-work semantics of ``pa_decode_metadata_kenrel``
+  (kernels/pa_decode_fp8.py:941-1721): direct rows or f32 partial rows plus
+  their log-sum-exp;
+* ``reduce_v1`` -- the merge of split works' partials that the reference
+  delegates to aiter's ``pa_reduce_v1`` (call site kernels/pa_decode_fp8.py:3189-3200).
 """
 
 from __future__ import annotations
@@ -211,6 +219,117 @@ def lse_reduce(exp_sums: np.ndarray, max_logits: np.ndarray, tmp_out: np.ndarray
     tot = w.sum(axis=0)
     tot = np.where(tot > 0, tot, 1.0)
     return (np.einsum("pr,prd->rd", w / tot[None, :], to)).astype(np.float32)
+
+
+# ---------------------------------------------------------- worklist path
+def range_attention(q_row, k_seq, v_seq, lo: int, hi: int, softmax_scale: float):
+    """Softmax attention of one query row over keys [lo, hi), float64.
+
+    Returns (l, m, o): exp sum relative to the max logit m (natural log units)
+    and the normalised output; (0, -inf, zeros) when the range is empty.
+    """
+    d = v_seq.shape[-1]
+    if hi <= lo:
+        return 0.0, -np.inf, np.zeros(d, dtype=np.float64)
+    s = (k_seq[lo:hi].astype(np.float64) @ np.asarray(q_row, dtype=np.float64)) * softmax_scale
+    m = float(s.max())
+    p = np.exp(s - m)
+    l = float(p.sum())
+    return l, m, (p @ v_seq[lo:hi].astype(np.float64)) / l
+
+
+def worklist_decode(
+    query: np.ndarray,
+    seq_kv,
+    context_lengths,
+    query_length: int,
+    group_size: int,
+    softmax_scale: float,
+    work_indptr,
+    work_info,
+    partition_indptr,
+    partial_rows: int,
+    partition_size: int = 256,
+):
+    """What the persistent decode writes for a worklist (kernels/pa_decode_fp8.py:941-1721).
+
+    ``seq_kv(b)`` returns the dequantised (K, V) [ctx, Hkv, D] of sequence b.
+    Workgroup c runs works [work_indptr[c], work_indptr[c+1]); work
+    ``[batch, ploc, qo_start, qo_end, kv_start, kv_end, _, qhr]`` attends the
+    keys of partitions [kv_start - partition_indptr[batch], kv_end - ...) of its
+    sequence (256 tokens each, :1150-1166) under the causal bound
+    tok < ctx + 1 - ql + qi (:1338-1341), for every query head of kv head
+    ``(qhr & 0xffff) // g`` (:1168-1170).  ploc < 0 writes the normalised row to
+    out[qo_start + qi, qhead]; ploc >= 0 writes it (f32) to partial row
+    ploc + ql + qi with lse = m + log(l) (:1612-1643; l = 0 gives -inf).
+
+    Returns (out [B*ql, Hq, D], partial_output [partial_rows, Hq, D],
+    partial_lse [partial_rows, Hq]) as float64, NaN where nothing was written.
+    """
+    q = np.asarray(query, dtype=np.float64)
+    rows, hq, d = q.shape
+    out = np.full((rows, hq, d), np.nan)
+    po = np.full((partial_rows, hq, d), np.nan)
+    pl = np.full((partial_rows, hq), np.nan)
+    wi = np.asarray(work_indptr, dtype=np.int64)
+    winfo = np.asarray(work_info, dtype=np.int64).reshape(-1, 8)
+    pind = np.asarray(partition_indptr, dtype=np.int64)
+    cache = {}
+    for c in range(len(wi) - 1):
+        for w in range(int(wi[c]), int(wi[c + 1])):
+            b, ploc, qo_start, _, kv_start, kv_end, _, qhr = (int(x) for x in winfo[w])
+            h = (qhr & 0xFFFF) // group_size
+            ctx = int(context_lengths[b])
+            if b not in cache:
+                cache[b] = seq_kv(b)
+            k_seq, v_seq = cache[b]
+            tok_lo = (kv_start - int(pind[b])) * partition_size
+            tok_hi = min((kv_end - int(pind[b])) * partition_size, ctx)
+            for qi in range(query_length):
+                bound = ctx + 1 - query_length + qi
+                for gi in range(group_size):
+                    qhead = h * group_size + gi
+                    l, m, o = range_attention(q[b * query_length + qi, qhead], k_seq[:, h], v_seq[:, h],
+                                              max(tok_lo, 0), min(tok_hi, bound), softmax_scale)
+                    if ploc < 0:
+                        out[qo_start + qi, qhead] = o
+                    else:
+                        po[ploc + query_length + qi, qhead] = o
+                        pl[ploc + query_length + qi, qhead] = m + math.log(l) if l > 0 else -np.inf
+    return out, po, pl
+
+
+def reduce_v1(partial_output, partial_lse, reduce_indptr, reduce_final_map, reduce_partial_map, max_qlen: int, out):
+    """Merge of split works' partials into ``out`` in place (the role of aiter's
+    pa_reduce_v1, called at kernels/pa_decode_fp8.py:3189-3200 on
+    ``partial_output[ql:]``).  For group g with partials j in
+    [reduce_indptr[g], reduce_indptr[g+1]) and rows s_j = reduce_partial_map[j] + qi:
+    out[qo_start + qi, h] = sum_j exp(lse_j - LSE) * partial_j, LSE = log sum_j exp(lse_j);
+    a row whose partials are all -inf gets 0.  Returns the merged LSE per written
+    (row, head) as a dict.
+    """
+    po = np.asarray(partial_output, dtype=np.float64)
+    pl = np.asarray(partial_lse, dtype=np.float64)
+    ri = np.asarray(reduce_indptr, dtype=np.int64)
+    fm = np.asarray(reduce_final_map, dtype=np.int64).reshape(-1, 2)
+    pm = np.asarray(reduce_partial_map, dtype=np.int64)
+    lses = {}
+    for g in range(len(ri) - 1):
+        j0, j1 = int(ri[g]), int(ri[g + 1])
+        if j0 >= j1:
+            continue
+        qo_start, qo_end = int(fm[g, 0]), int(fm[g, 1])
+        for qi in range(min(qo_end - qo_start, max_qlen)):
+            srows = pm[j0:j1] + qi
+            lse = pl[srows]  # [n, Hq]
+            mx = lse.max(axis=0)
+            safe = np.where(np.isfinite(mx), mx, 0.0)
+            wgt = np.where(np.isfinite(lse), np.exp(lse - safe[None, :]), 0.0)
+            tot = wgt.sum(axis=0)
+            inv = np.where(tot > 0, 1.0 / np.where(tot > 0, tot, 1.0), 0.0)
+            out[qo_start + qi] = np.einsum("nh,nhd->hd", wgt * inv[None, :], po[srows])
+            lses[qo_start + qi] = np.where(tot > 0, safe + np.log(np.where(tot > 0, tot, 1.0)), -np.inf)
+    return lses
 
 
 def softmax_scale_for(head_dim: int) -> float:

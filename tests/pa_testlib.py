@@ -46,7 +46,8 @@ def oracle_output(w: Dict, b: int) -> np.ndarray:
     return ofp8.bf16_round(o)
 
 
-def launch(w: Dict, max_parts: int = 0, out_dtype=torch.bfloat16, query=None, with_partials: bool = False):
+def launch(w: Dict, max_parts: int = 0, out_dtype=torch.bfloat16, query=None, with_partials: bool = False,
+           metadata=None):
     from flydsl_amd import pa_decode_ps_launch
 
     cfg = w["config"]
@@ -69,12 +70,13 @@ def launch(w: Dict, max_parts: int = 0, out_dtype=torch.bfloat16, query=None, wi
         w["key_cache"],
         w["value_cache"],
         w["context_lengths"],
-        None,
-        None,
+        w["kv_page_indices"],
+        w["kv_indptr"],
         1.0 / math.sqrt(128),
         w["key_scale"],
         w["value_scale"],
         sliding_window=cfg.sliding_window,
+        metadata=metadata,
         block_tables=w["block_tables"],
         max_context_partition_num=max_parts,
         **partials,
@@ -137,3 +139,62 @@ def check_partials(w: Dict, partials: Dict, max_parts: int, batches: Iterable[in
                     np.testing.assert_allclose(g_ml[live], e_ml[live], atol=2e-3, rtol=1e-3, err_msg=f"ml {b},{h},{z}")
                     np.testing.assert_allclose(g_es[live], e_es[live], rtol=1e-2, atol=1e-3, err_msg=f"es {b},{h},{z}")
                     np.testing.assert_allclose(g_to[live], e_to[live], atol=ATOL, rtol=RTOL, err_msg=f"to {b},{h},{z}")
+
+
+def metadata_with_bins(w: Dict, num_cu: int) -> Dict:
+    """get_pa_metadata's dict, but scheduled over ``num_cu`` bins (few bins force many splits)."""
+    from flydsl_amd import get_pa_metadata_info_v1, get_pa_metadata_v1
+
+    cfg = w["config"]
+    dev = w["query"].device
+    b, ql, hq, hkv = cfg.batch, cfg.query_length, cfg.num_q_heads, cfg.num_kv_heads
+    infos = get_pa_metadata_info_v1(b, hkv, num_cu=num_cu)
+    ptrs, wi, winfo, ri, rfm, rpm = [torch.empty(shape, dtype=dtype, device=dev) for shape, dtype in infos]
+    sq = torch.arange(b + 1, dtype=torch.int32, device=dev) * ql
+    get_pa_metadata_v1(sq, w["kv_indptr"], w["context_lengths"], hq // hkv, hkv, True, ptrs, wi, winfo, ri, rfm, rpm,
+                       kv_granularity=256, block_size=cfg.block_size, max_seqlen_qo=ql, uni_seqlen_qo=ql,
+                       num_cu=num_cu)
+    parts = (w["context_lengths"] + 255) // 256
+    pind = torch.zeros(b + 1, dtype=torch.int32, device=dev)
+    pind[1:] = torch.cumsum(parts, 0).to(torch.int32)
+    nparts = int(ri[-1].item())
+    return {
+        "work_indptr": wi, "work_info_flat": winfo.reshape(-1).contiguous(), "partition_indptr": pind,
+        "reduce_indptr": ri, "reduce_final_map": rfm, "reduce_partial_map": rpm, "num_sm": num_cu,
+        "partial_output": torch.full(((nparts + 1) * ql, 1, hq, 128), float("nan"), device=dev),
+        "partial_lse": torch.full(((nparts + 1) * ql, 1, hq, 1), float("nan"), device=dev),
+    }
+
+
+def check_worklist_partials(w: Dict, md: Dict) -> int:
+    """Every partial row the worklist kernel wrote vs the oracle's per-work
+    restatement (oatt.worklist_decode) on the same worklist: the work -> token
+    range mapping is exact, so an empty row must be (-inf, 0) bit-for-bit and a
+    live row must match the oracle's lse to 2e-3 and its f32 output to the bf16
+    tolerance.  Returns the number of partial rows checked."""
+    cfg = w["config"]
+    ql, g = cfg.query_length, cfg.group_size
+    cache = {}
+
+    def seq_kv(b):
+        if b not in cache:
+            _, kf, vf = sequence_inputs(w, b)
+            cache[b] = (kf, vf)
+        return cache[b]
+
+    po_gpu = md["partial_output"].cpu().numpy()[:, 0]
+    pl_gpu = md["partial_lse"].cpu().numpy()[:, 0, :, 0]
+    _, po, pl = oatt.worklist_decode(
+        w["query"].float().cpu().numpy(), seq_kv, w["context_list"], ql, g, 1.0 / math.sqrt(128),
+        md["work_indptr"].cpu().numpy(), md["work_info_flat"].cpu().numpy(), md["partition_indptr"].cpu().numpy(),
+        po_gpu.shape[0],
+    )
+    written = ~np.isnan(pl)
+    assert np.array_equal(written, ~np.isnan(pl_gpu)), "the kernel wrote other partial rows than the worklist names"
+    empty = written & np.isneginf(pl)
+    assert np.all(np.isneginf(pl_gpu[empty])), "empty partial row without -inf lse"
+    assert np.all(po_gpu[empty] == 0.0), "empty partial row with non-zero output"
+    live = written & ~np.isneginf(pl)
+    np.testing.assert_allclose(pl_gpu[live], pl[live], atol=2e-3, rtol=1e-4, err_msg="partial lse")
+    np.testing.assert_allclose(po_gpu[live], po[live], atol=ATOL, rtol=RTOL, err_msg="partial output")
+    return int(written.sum())

@@ -37,8 +37,8 @@ def declared_functions():
 
 def test_header_declares_the_expected_api():
     assert declared_functions() == sorted(
-        ["pa_fp8_decode_partitions", "pa_fp8_lse_reduce", "pa_fp8_metadata_v1", "pa_fp8_status_string",
-         "pa_fp8_abi_version"]
+        ["pa_fp8_decode_partitions", "pa_fp8_lse_reduce", "pa_fp8_decode_worklist", "pa_fp8_reduce_v1",
+         "pa_fp8_metadata_v1", "pa_fp8_status_string", "pa_fp8_abi_version"]
     )
 
 
@@ -56,7 +56,13 @@ def test_abi_version(lib):
     assert f"#define PA_FP8_ABI_VERSION {lib.PA_FP8_ABI_VERSION}" in HEADER.read_text()
 
 
-STRUCTS = {"pa_fp8_decode_args": "DecodeArgs", "pa_fp8_reduce_args": "ReduceArgs", "pa_fp8_metadata_args": "MetadataArgs"}
+STRUCTS = {
+    "pa_fp8_decode_args": "DecodeArgs",
+    "pa_fp8_reduce_args": "ReduceArgs",
+    "pa_fp8_worklist_args": "WorklistArgs",
+    "pa_fp8_reduce_v1_args": "ReduceV1Args",
+    "pa_fp8_metadata_args": "MetadataArgs",
+}
 
 
 def test_struct_layouts_match_header(lib, tmp_path):
@@ -115,6 +121,8 @@ def test_null_args_and_status_strings(lib):
     assert lib.LIB.pa_fp8_decode_partitions(None, None) == 1
     assert lib.LIB.pa_fp8_lse_reduce(None, None) == 1
     assert lib.LIB.pa_fp8_metadata_v1(None, None) == 1
+    assert lib.LIB.pa_fp8_decode_worklist(None, None) == 1
+    assert lib.LIB.pa_fp8_reduce_v1(None, None) == 1
     for code in range(0, 9):
         assert lib.LIB.pa_fp8_status_string(code)
     with pytest.raises(lib.PaFp8Error, match="status 2"):
@@ -135,3 +143,46 @@ def test_reduce_and_metadata_validation(lib):
     assert lib.LIB.pa_fp8_metadata_v1(ctypes.byref(m), None) == 5  # granularity not a power of two
     m.kv_granularity = 256
     assert lib.LIB.pa_fp8_metadata_v1(ctypes.byref(m), None) == 1  # null buffers
+
+
+def _worklist_args(lib, **over):
+    a = lib.WorklistArgs()
+    a.batch_size, a.num_kv_heads, a.query_group_size, a.query_length = 0, 1, 8, 1
+    a.head_dim, a.block_size, a.num_cu, a.num_blocks = 128, 1024, 8, 4
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "over,status",
+    [
+        ({}, 0),  # an empty batch is a no-op
+        ({"batch_size": 2, "num_cu": 0}, 0),  # no workgroups: nothing to launch
+        ({"head_dim": 96}, 2),
+        ({"block_size": 1000}, 3),
+        ({"query_length": 5, "query_group_size": 16}, 4),
+        ({"query_dtype": 2}, 6),
+        ({"out_dtype": 5}, 6),
+        ({"num_cu": -1}, 5),
+        ({"batch_size": 2}, 1),  # null pointers
+    ],
+)
+def test_worklist_validation_codes(lib, over, status):
+    assert lib.LIB.pa_fp8_decode_worklist(ctypes.byref(_worklist_args(lib, **over)), None) == status
+
+
+def test_reduce_v1_validation(lib):
+    r = lib.ReduceV1Args()
+    r.num_groups, r.num_heads, r.head_dim, r.max_qlen, r.partial_map_len = 0, 8, 128, 1, 4
+    assert lib.LIB.pa_fp8_reduce_v1(ctypes.byref(r), None) == 0  # no groups: no-op
+    r.head_dim = 64
+    assert lib.LIB.pa_fp8_reduce_v1(ctypes.byref(r), None) == 2
+    r.head_dim, r.num_groups, r.out_dtype = 128, 3, 9
+    assert lib.LIB.pa_fp8_reduce_v1(ctypes.byref(r), None) == 6
+    r.out_dtype = 0
+    assert lib.LIB.pa_fp8_reduce_v1(ctypes.byref(r), None) == 0  # no partial rows: nothing to merge
+    r.partial_rows = 4
+    assert lib.LIB.pa_fp8_reduce_v1(ctypes.byref(r), None) == 1  # null buffers
+    r.max_qlen = 0
+    assert lib.LIB.pa_fp8_reduce_v1(ctypes.byref(r), None) == 5

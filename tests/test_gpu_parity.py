@@ -40,11 +40,14 @@ SMALL_CASES = {
     "bs64_tok_mtp4_g16": dict(base="c5", batch=3, ctx_kind="uniform", ctx_a=4, ctx_b=1500),
     "sw_small": dict(base="c4", batch=4, sliding_window=300, ctx_kind="uniform", ctx_a=1, ctx_b=2000),
     "sw_mtp": dict(base="c4", batch=4, sliding_window=100, query_length=3, ctx_kind="uniform", ctx_a=3, ctx_b=900),
-    "ql2_g8_bs32": dict(base="c2", batch=3, num_q_heads=16, num_kv_heads=2, block_size=32, query_length=2,
-                        ctx_kind="uniform", ctx_a=2, ctx_b=1200),
-    "g1_bs128": dict(base="c2", batch=3, num_q_heads=4, num_kv_heads=4, block_size=128, ctx_kind="uniform",
-                     ctx_a=1, ctx_b=900),
-    "bs1024_tok": dict(base="c3", batch=3, block_size=1024, ctx_kind="uniform", ctx_a=1, ctx_b=2100),
+    # block sizes other than 16 / 64 reach the partition kernel through a window
+    # (without one they run the worklist path, tests/test_gpu_worklist.py)
+    "sw_ql2_g8_bs32": dict(base="c4", batch=3, num_q_heads=16, num_kv_heads=2, block_size=32, query_length=2,
+                           sliding_window=700, ctx_kind="uniform", ctx_a=2, ctx_b=1200),
+    "sw_g1_bs128": dict(base="c4", batch=3, num_q_heads=4, num_kv_heads=4, block_size=128, sliding_window=500,
+                        ctx_kind="uniform", ctx_a=1, ctx_b=900),
+    "sw_bs1024_tok": dict(base="c3", batch=3, block_size=1024, sliding_window=1500, ctx_kind="uniform", ctx_a=1,
+                          ctx_b=2100),
     "mtp2_pt": dict(base="c2", batch=3, num_q_heads=16, num_kv_heads=2, query_length=4, ctx_kind="uniform",
                     ctx_a=4, ctx_b=1500),
     "mtp2_tok": dict(base="c3", batch=3, num_q_heads=16, num_kv_heads=2, query_length=4, ctx_kind="uniform",

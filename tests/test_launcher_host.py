@@ -32,13 +32,96 @@ def make(batch=3, hq=8, hkv=2, bs=16, ql=1, nb=20, per_token=False, max_blocks=8
     return t
 
 
-def plan(t, sliding_window=0, max_parts=4, **over):
+def plan(t, sliding_window=0, max_parts=4, capturing=False, **over):
     t = {**t, **over}
     return pdf._build_plan(
         t["output"], t["query"], t["key_cache"], t["value_cache"], t["context_lengths"], 1 / math.sqrt(128),
         t["key_scale"], t["value_scale"], sliding_window, t["block_tables"], max_parts,
-        t.get("exp_sums"), t.get("max_logits"), t.get("temporary_output"), False,
+        t.get("exp_sums"), t.get("max_logits"), t.get("temporary_output"), capturing,
+        kv_page_indices=t.get("kv_page_indices"), kv_indptr=t.get("kv_indptr"), metadata=t.get("metadata"),
     )
+
+
+def cpu_metadata(t, num_cu):
+    """get_pa_metadata's dict built on the CPU from the oracle scheduler (no device)."""
+    from oracle import planners as oplan
+
+    ctx = t["context_lengths"].tolist()
+    b, ql = len(ctx), t["query"].shape[0] // len(ctx)
+    hq, hkv = t["query"].shape[1], t["key_cache"].shape[1]
+    md = oplan.get_pa_metadata_v1([i * ql for i in range(b + 1)], ctx, hq // hkv, hkv, num_cu, 256, ql)
+    parts = [(c + 255) // 256 for c in ctx]
+    nparts = int(md["reduce_indptr"][-1])
+    i32 = lambda a: torch.from_numpy(a.astype("int32")).contiguous()  # noqa: E731
+    return {
+        "work_indptr": i32(md["work_indptr"]),
+        "work_info_flat": i32(md["work_info"].reshape(-1)),
+        "partition_indptr": torch.tensor([0] + list(torch.tensor(parts).cumsum(0).tolist()), dtype=torch.int32),
+        "reduce_indptr": i32(md["reduce_indptr"]),
+        "reduce_final_map": i32(md["reduce_final_map"]),
+        "reduce_partial_map": i32(md["reduce_partial_map"]),
+        "num_sm": num_cu,
+        "partial_output": torch.empty(((nparts + 1) * ql, 1, hq, 128)),
+        "partial_lse": torch.empty(((nparts + 1) * ql, 1, hq, 1)),
+    }
+
+
+def make_paged(bs=1024, batch=3, hq=16, hkv=1, ql=2, ctx=(1027, 300, 700), per_token=False, num_cu=4):
+    t = make(batch=batch, hq=hq, hkv=hkv, bs=bs, ql=ql, nb=8, per_token=per_token, max_blocks=2)
+    t["context_lengths"] = torch.tensor(ctx, dtype=torch.int32)
+    pages = [(c + bs - 1) // bs for c in ctx]
+    t["kv_indptr"] = torch.tensor([0] + list(torch.tensor(pages).cumsum(0).tolist()), dtype=torch.int32)
+    t["kv_page_indices"] = torch.arange(sum(pages), dtype=torch.int32) % 8
+    t["metadata"] = cpu_metadata(t, num_cu)
+    return t
+
+
+def test_persistent_path_routing_and_args():
+    t = make_paged(per_token=True)
+    p = plan(t, max_parts=0)
+    assert p.tag == "ps_split_reduce" and p.dargs is None and p.rargs is None
+    assert [fn.__name__ for fn, _ in p.launches] == ["decode_worklist", "reduce_v1"]
+    w, v, md = p.wargs, p.vargs, t["metadata"]
+    assert (w.batch_size, w.num_kv_heads, w.query_group_size, w.query_length, w.block_size) == (3, 1, 16, 2, 1024)
+    assert w.num_cu == 4 and w.max_work == md["work_info_flat"].numel() // 8 and w.num_pages == 4
+    assert w.work_indptr == md["work_indptr"].data_ptr() and w.kv_indptr == t["kv_indptr"].data_ptr()
+    assert w.partial_rows == md["partial_output"].shape[0] and w.output_rows == 6
+    assert w.stride_po_row == 16 * 128 and w.stride_pl_row == 16
+    assert w.per_token_kv == 1 and w.stride_ks_block == 1024 and w.stride_ks_head == 1024
+    # the reduce reads the partials from row query_length on (kernels/pa_decode_fp8.py:3190-3191)
+    assert v.partial_output == md["partial_output"].data_ptr() + 2 * 16 * 128 * 4
+    assert v.partial_lse == md["partial_lse"].data_ptr() + 2 * 16 * 4
+    assert v.partial_rows == md["partial_output"].shape[0] - 2 and v.max_qlen == 2
+    assert v.num_groups == 3 and v.num_heads == 16 and v.output == t["output"].data_ptr()
+    assert int(md["reduce_indptr"][-1]) > 0  # the shape above does split
+
+
+@pytest.mark.parametrize("bs", [32, 128, 256, 1024])
+def test_persistent_path_for_other_block_sizes(bs):
+    assert plan(make_paged(bs=bs), max_parts=0).tag == "ps_split_reduce"
+
+
+def test_persistent_path_without_splits_skips_the_reduce():
+    t = make_paged(num_cu=1)  # one bin holds every sequence whole
+    assert int(t["metadata"]["reduce_indptr"][-1]) == 0
+    p = plan(t, max_parts=0)
+    assert p.vargs is None and [fn.__name__ for fn, _ in p.launches] == ["decode_worklist"]
+
+
+def test_persistent_path_errors():
+    t = make_paged()
+    with pytest.raises(ValueError, match="kv_page_indices"):
+        plan(t, kv_page_indices=None)
+    with pytest.raises(ValueError, match="precomputed `metadata`"):
+        plan(t, metadata=None, capturing=True)
+    bad = dict(t["metadata"], work_indptr=t["metadata"]["work_indptr"][:-1].contiguous())
+    with pytest.raises(ValueError, match="work_indptr"):
+        plan(t, metadata=bad)
+    with pytest.raises(ValueError, match="missing"):
+        plan(t, metadata={"num_sm": 4})
+    bad = dict(t["metadata"], partial_output=torch.empty(1, 1, 16, 128))
+    with pytest.raises(ValueError, match="partial_output"):
+        plan(t, metadata=bad)
 
 
 def test_small_block_routing_and_args():
@@ -85,7 +168,8 @@ def test_sliding_window_routing():
     assert plan(t, sliding_window=300, max_parts=3).tag == "ps_sw_partitioned"
     p = plan(t, sliding_window=300, max_parts=1)
     assert p.tag == "ps_sw_fused_partitioned" and p.dargs.sliding_window == 300
-    assert plan(make(bs=1024, max_blocks=2), max_parts=2).tag == "ps_partitioned"
+    # a window routes every block size to the split-context kernel
+    assert plan(make(bs=1024, max_blocks=2), sliding_window=300, max_parts=2).tag == "ps_sw_partitioned"
 
 
 def test_caller_intermediates_are_used():
