@@ -2,13 +2,17 @@
 """Headline benchmark: KV-read HBM GB/s (% of the 8 TB/s peak) and us per decode
 step of the Llama-3-8B-shaped fp8 paged decode on one MI355X.
 
-A step is one ``pa_decode_ps_launch`` over the whole batch (partition kernel +
-log-sum-exp reduce), inputs resident in HBM.  ``--copies`` KV caches are
-rotated step to step so the working set (>= 1.5 GiB for c2) defeats the
+A step is one ``pa_decode_ps_launch`` over the whole batch, inputs resident in
+HBM.  Like the reference harness (tests/kernels/test_pa.py:840-850) the
+worklist metadata is built once with ``get_pa_metadata`` before the timed
+steps and passed to every launch, so 16 / 64-token pages run the worklist
+kernel (plus the merge of split works) and sliding-window configs the
+split-context partition kernel (plus its LSE reduce).  ``--copies`` KV caches
+are rotated step to step so the working set (>= 1.5 GiB for c2) defeats the
 256 MB Infinity Cache.  Prints ONE JSON line.
 
   value          = algorithmic fp8 K+V bytes per step / us per step (GB/s)
-  roofline       = partition kernel alone: its algorithmic bytes per launch /
+  roofline       = the decode kernel alone: its algorithmic bytes per launch /
                    its mean duration from HIP events on the launch stream
   cpu_baseline   = the numpy oracle (restated reference torch path) timed on a
                    bounded sample of the same workload on this host, one thread
@@ -43,6 +47,8 @@ def _parse():
     ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
     ap.add_argument("--max-parts", type=int, default=0, help="max_context_partition_num (0 = launcher default)")
+    ap.add_argument("--no-metadata", action="store_true",
+                    help="launch without get_pa_metadata's schedule (16 / 64-token pages then run the partition kernel)")
     ap.add_argument("--traffic-run", action="store_true",
                     help="for rocprofv3 --pmc passes: a 256 MiB copy (counter calibration) then --steps decode steps")
     return ap.parse_args()
@@ -65,6 +71,37 @@ def _partition_kernel_bytes(cfg, ctx, max_parts):
     eqgs = cfg.query_length * cfg.group_size
     partials = cfg.batch * cfg.num_kv_heads * max_parts * eqgs * (HEAD_DIM * 2 + 8)
     return total - qo + partials
+
+
+def _worklist_kernel_bytes(cfg, ctx, metadata):
+    """Algorithmic bytes one worklist-kernel launch moves: K/V (+ per-token
+    scales), Q, page entries, context lengths, the rows of unsplit sequences
+    (written to the output directly) and the f32 partial rows plus their
+    log-sum-exps of split works; the worklist itself (work_indptr, 32 B per work)."""
+    import numpy as np
+
+    from flydsl_amd.workloads import algorithmic_bytes, HEAD_DIM
+
+    total = algorithmic_bytes(cfg, ctx)
+    winfo = metadata["work_info_flat"].cpu().numpy()
+    nw = int(metadata["work_indptr"][-1].item())
+    ploc = winfo[: nw * 8].reshape(nw, 8)[:, 1]
+    eqgs = cfg.query_length * cfg.group_size
+    split_works = int(np.count_nonzero(ploc >= 0))
+    split_seqs = len({int(b) for b, p in zip(winfo[: nw * 8].reshape(nw, 8)[:, 0], ploc) if p >= 0})
+    # the output rows of split sequences are written by the merge, not by this kernel
+    total -= split_seqs * cfg.query_length * cfg.num_q_heads * HEAD_DIM * 2
+    total += split_works * eqgs * (HEAD_DIM * 4 + 4)
+    total += nw * 32 + metadata["work_indptr"].numel() * 4
+    return total
+
+
+_KERNEL_NAMES = {
+    "decode_partitions": "pa_decode_partition_kernel",
+    "lse_reduce": "pa_lse_reduce_kernel",
+    "decode_worklist": "pa_decode_worklist_kernel",
+    "reduce_v1": "pa_reduce_v1_kernel",
+}
 
 
 def cpu_baseline(w, seconds: float):
@@ -122,8 +159,7 @@ def main():
 
     import torch
 
-    from flydsl_amd import pa_decode_ps_launch
-    from flydsl_amd import _lib
+    from flydsl_amd import get_pa_metadata, pa_decode_ps_launch
     from flydsl_amd.pa_decode_fp8 import _PLAN_CACHE
     from flydsl_amd.workloads import CONFIGS, build_workload, kv_bytes
 
@@ -134,20 +170,32 @@ def main():
     # every copy shares the first copy's context lengths / block tables / query
     base = works[0]
     for w in works[1:]:
-        w["context_lengths"], w["block_tables"], w["query"] = base["context_lengths"], base["block_tables"], base["query"]
-        w["context_list"], w["block_table_np"] = base["context_list"], base["block_table_np"]
+        for k in ("context_lengths", "block_tables", "query", "context_list", "block_table_np", "kv_page_indices",
+                  "kv_indptr"):
+            w[k] = base[k]
     ctx = base["context_list"]
     max_parts = args.max_parts  # 0: the launcher's default for this kernel
     # partials are allocated by the launcher and reused across steps through its plan cache
     out = torch.empty_like(base["query"])
     scale = 1.0 / math.sqrt(128)
 
-    def step(i):
+    # the worklist schedule, built once for the batch as the reference harness does
+    metadata, metadata_us = None, None
+    if not cfg.sliding_window and not args.no_metadata:
+        m0, m1 = _events(torch, 2)
+        m0.record()
+        metadata = get_pa_metadata(base["query"], base["key_cache"], base["context_lengths"], base["kv_indptr"],
+                                   cfg.num_q_heads, cfg.num_kv_heads)
+        m1.record()
+        torch.cuda.synchronize()
+        metadata_us = m0.elapsed_time(m1) * 1e3
+
+    def step(i, md=metadata, parts=None):
         w = works[i % len(works)]
         return pa_decode_ps_launch(
-            out, w["query"], w["key_cache"], w["value_cache"], w["context_lengths"], None, None, scale,
-            w["key_scale"], w["value_scale"], sliding_window=cfg.sliding_window, block_tables=w["block_tables"],
-            max_context_partition_num=max_parts,
+            out, w["query"], w["key_cache"], w["value_cache"], w["context_lengths"], w["kv_page_indices"],
+            w["kv_indptr"], scale, w["key_scale"], w["value_scale"], sliding_window=cfg.sliding_window, metadata=md,
+            block_tables=w["block_tables"], max_context_partition_num=max_parts if parts is None else parts,
         )
 
     if args.traffic_run:
@@ -163,23 +211,26 @@ def main():
         print(json.dumps({"traffic_run": cfg.name, "copy_bytes": src.numel(), "steps": args.steps, "path": tag}))
         return
 
-    for i in range(args.warmup):
-        tag = step(i)
-    torch.cuda.synchronize()
+    def timed(fn):
+        for i in range(args.warmup):
+            fn(i)
+        e0, e1 = _events(torch, 2)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record()
+        for i in range(args.steps):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps, (time.perf_counter() - t0) / args.steps
 
     # ---- headline: K steps through the drop-in launcher
-    e0, e1 = _events(torch, 2)
-    torch.cuda.synchronize()
-    t_host = time.perf_counter()
-    e0.record()
-    for i in range(args.steps):
-        step(i)
-    e1.record()
-    torch.cuda.synchronize()
-    host_s = time.perf_counter() - t_host
-    ms_per_step = e0.elapsed_time(e1) / args.steps
+    for i in range(args.warmup):
+        tag = step(i)
+    ms_per_step, host_s = timed(step)
 
-    # ---- secondary: the reference's default partition count (get_recommended_splits)
+    # ---- secondary: the split-context partition kernel at the launcher's default
+    # partition count and at the reference's default (get_recommended_splits)
     from flydsl_amd import get_recommended_splits
 
     ref_parts = (
@@ -188,57 +239,49 @@ def main():
         if cfg.sliding_window
         else get_recommended_splits(cfg.batch, cfg.num_kv_heads, split_kv_blocks=max(1, 256 // cfg.block_size))
     )
-
-    def ref_step(i):
-        w = works[i % len(works)]
-        return pa_decode_ps_launch(
-            out, w["query"], w["key_cache"], w["value_cache"], w["context_lengths"], None, None, scale,
-            w["key_scale"], w["value_scale"], sliding_window=cfg.sliding_window, block_tables=w["block_tables"],
-            max_context_partition_num=ref_parts,
-        )
-
-    for i in range(args.warmup):
-        ref_step(i)
-    r0, r1 = _events(torch, 2)
-    torch.cuda.synchronize()
-    r0.record()
-    for i in range(args.steps):
-        ref_step(i)
-    r1.record()
-    torch.cuda.synchronize()
-    ref_us = r0.elapsed_time(r1) / args.steps * 1e3
+    others = {}
+    if metadata is not None and cfg.block_size in (16, 64):
+        others["partition_kernel_auto_partitions"] = timed(lambda i: step(i, md=None))[0] * 1e3
+    ref_us = timed(lambda i: step(i, md=None, parts=ref_parts))[0] * 1e3 if cfg.block_size in (16, 64) or cfg.sliding_window else None
     for i in range(len(works)):  # the default plans become the newest cache entries again
         step(i)
     torch.cuda.synchronize()
 
     # ---- per-kernel durations: HIP events around each launch on the launch stream
     plans = [_PLAN_CACHE[k] for k in list(_PLAN_CACHE.keys())[-len(works):]]
-    max_parts = plans[0].max_parts
+    names = [fn.__name__ for fn, _ in plans[0].launches]
     handle = torch.cuda.current_stream(dev).cuda_stream
-    evs = _events(torch, 3 * args.steps)
+    nl = len(names)
+    evs = _events(torch, (nl + 1) * args.steps)
     torch.cuda.synchronize()
     for i in range(args.steps):
         p = plans[i % len(plans)]
-        evs[3 * i].record()
-        _lib.decode_partitions(p.dargs, handle)
-        evs[3 * i + 1].record()
-        if p.rargs is not None:
-            _lib.lse_reduce(p.rargs, handle)
-        evs[3 * i + 2].record()
+        evs[(nl + 1) * i].record()
+        for j, (fn, a) in enumerate(p.launches):
+            fn(a, handle)
+            evs[(nl + 1) * i + j + 1].record()
     torch.cuda.synchronize()
-    k_ms = sorted(evs[3 * i].elapsed_time(evs[3 * i + 1]) for i in range(args.steps))
-    r_ms = sorted(evs[3 * i + 1].elapsed_time(evs[3 * i + 2]) for i in range(args.steps))
+    kernel_ms = {}
+    for j, n in enumerate(names):
+        kernel_ms[_KERNEL_NAMES[n]] = sorted(
+            evs[(nl + 1) * i + j].elapsed_time(evs[(nl + 1) * i + j + 1]) for i in range(args.steps)
+        )
+    main_kernel = _KERNEL_NAMES[names[0]]
+    k_ms = kernel_ms[main_kernel]
     k_mean = sum(k_ms) / len(k_ms)
-    r_mean = sum(r_ms) / len(r_ms) if plans[0].rargs is not None else 0.0
+    max_parts = plans[0].max_parts
 
     kvb = kv_bytes(cfg, ctx)
     us_step = ms_per_step * 1e3
     gbs = kvb / (us_step * 1e-6) / 1e9
-    kbytes = _partition_kernel_bytes(cfg, ctx, max_parts)
+    if main_kernel == "pa_decode_worklist_kernel":
+        kbytes = _worklist_kernel_bytes(cfg, ctx, metadata)
+    else:
+        kbytes = _partition_kernel_bytes(cfg, ctx, max_parts)
     achieved = kbytes / (k_mean * 1e-3) / 1e9
 
     traffic = None
-    tfile = ROOT / "profiles" / f"pa_decode_partition_kernel_{cfg.name}_traffic.json"
+    tfile = ROOT / "profiles" / f"{main_kernel}_{cfg.name}_traffic.json"
     if tfile.exists():
         try:
             traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
@@ -280,14 +323,17 @@ def main():
             "kv_bytes_per_step": kvb,
             "kv_cache_copies_rotated": len(works),
             "path": tag,
+            "kernels": [_KERNEL_NAMES[n] for n in names],
+            "metadata": "get_pa_metadata once per batch, outside the timed steps" if metadata is not None else None,
         },
         "kernels_us": {
-            "pa_decode_partition_kernel": round(k_mean * 1e3, 2),
-            "pa_decode_partition_kernel_median": round(k_ms[len(k_ms) // 2] * 1e3, 2),
-            "pa_lse_reduce_kernel": round(r_mean * 1e3, 2),
+            **{k: round(sum(v) / len(v) * 1e3, 2) for k, v in kernel_ms.items()},
+            f"{main_kernel}_median": round(k_ms[len(k_ms) // 2] * 1e3, 2),
         },
-        "host_us_per_step": round(host_s / args.steps * 1e6, 2),
-        "reference_default_partitions": {
+        "metadata_us": round(metadata_us, 2) if metadata_us is not None else None,
+        "host_us_per_step": round(host_s * 1e6, 2),
+        "other_paths_us_per_step": {k: round(v, 2) for k, v in others.items()},
+        "reference_default_partitions": None if ref_us is None else {
             "max_context_partition_num": ref_parts,
             "us_per_step": round(ref_us, 2),
             "kv_gbs": round(kvb / (ref_us * 1e-6) / 1e9, 1),
@@ -299,7 +345,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "pa_decode_partition_kernel",
+            "kernel": main_kernel,
             "algorithmic_bytes_per_launch": kbytes,
         },
         "cpu_baseline": cpu,

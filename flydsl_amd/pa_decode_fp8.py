@@ -25,7 +25,11 @@ from .pa_metadata import get_pa_metadata_info_v1, get_pa_metadata_v1
 from .pa_reduce import _reduce_v1_args
 
 KV_COMPUTE_BLOCK = 256  # tokens per context partition (kernels/pa_decode_fp8.py:36)
-_PA_METADATA_GRID_OVERSUB = 3  # kernels/pa_decode_fp8.py:37-40
+# Worklist bins per CU.  The reference schedules 3 (kernels/pa_decode_fp8.py:37-40)
+# because about three of its workgroups fit a CU; two of ours fit (two 4-wave
+# workgroups per CU at two waves per SIMD), and one bin per resident workgroup
+# keeps every bin's share of the batch running from start to end.
+_PA_METADATA_GRID_OVERSUB = 2
 _PA_DECODE_PS_SMALL_BLOCK_SIZES = (16, 64)  # kernels/pa_decode_fp8.py:1955
 HEAD_DIM = 128
 
@@ -520,7 +524,10 @@ def pa_decode_ps_launch(
 
     * ``sliding_window > 0``: sliding-window split-context path (partition
       kernel + log-sum-exp reduce; every block size), reading ``block_tables``;
-    * block sizes 16 / 64: small-block split-context path, reading ``block_tables``;
+    * block sizes 16 / 64: small-block path.  Given ``metadata`` (from
+      ``get_pa_metadata``) and ``kv_page_indices`` / ``kv_indptr`` it runs the
+      worklist kernel over that schedule, which balances ragged batches;
+      otherwise the split-context partition kernel reading ``block_tables``;
     * other block sizes: the persistent path -- the worklist kernel over
       ``metadata`` (computed with ``get_pa_metadata`` when absent, which
       synchronises once) reading pages through ``kv_page_indices`` /
@@ -627,7 +634,24 @@ def _build_plan(
         if t.device != dev:
             raise ValueError(f"`{name}` is on {t.device}, expected {dev}")
     small = block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES
-    if sliding_window <= 0 and not small:
+    # Block sizes other than 16 / 64 take the persistent path, as in the reference.
+    # The small-block path also runs the worklist kernel when the caller hands
+    # in get_pa_metadata's schedule with the flat page list: the schedule balances
+    # ragged batches across CUs, which fixed partition slots cannot.  The tag
+    # stays "ps_small_block" and exp_sums / max_logits / temporary_output are
+    # not touched (they are scratch of the split-context kernels).
+    if sliding_window <= 0 and (not small or (metadata is not None and kv_page_indices is not None
+                                              and kv_indptr is not None)):
+        if small:
+            if is_graph_capturing and (exp_sums is None or max_logits is None or temporary_output is None):
+                raise ValueError(  # the reference's small-block rule (kernels/pa_decode_fp8.py:3030-3034)
+                    "CUDA graph capture requires preallocated `exp_sums`, `max_logits`, "
+                    "and `temporary_output` for the small-block PS path."
+                )
+            plan = _worklist_plan(output, query, key_cache, value_cache, context_lengths, kv_page_indices, kv_indptr,
+                                  metadata, softmax_scale, key_scale, value_scale, per_token_kv, is_graph_capturing)
+            plan.tag = "ps_small_block"
+            return plan
         return _worklist_plan(output, query, key_cache, value_cache, context_lengths, kv_page_indices, kv_indptr,
                               metadata, softmax_scale, key_scale, value_scale, per_token_kv, is_graph_capturing)
     if block_tables is None:

@@ -48,7 +48,7 @@ def test_device_scheduler_matches_oracle(seed):
 
 
 def test_get_pa_metadata_c3_shape():
-    """The host entry point on the ragged benchmark shape (768 bins on 256 CUs)."""
+    """The host entry point on the ragged benchmark shape (512 bins on 256 CUs)."""
     from flydsl_amd import get_pa_metadata
     from flydsl_amd.workloads import CONFIGS, context_lengths_for
 
@@ -59,7 +59,7 @@ def test_get_pa_metadata_c3_shape():
     md = get_pa_metadata(q, kc, torch.tensor(ctx, dtype=torch.int32, device=dev),
                          torch.zeros(129, dtype=torch.int32, device=dev), 32, 8)
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    num_sm = (cus * 3 // 8) * 8
+    num_sm = (cus * 2 // 8) * 8  # two bins per CU: two worklist workgroups fit a CU
     assert md["num_sm"] == num_sm
     ref = op.get_pa_metadata_v1(list(range(129)), ctx, 4, 8, num_sm, 256, 1)
     v = op.metadata_valid_prefixes(ref)

@@ -49,7 +49,27 @@ def test_reference_normal_accuracy_cases(heads, ql, varlen, batch, quant):
     compare_outputs(w, out, range(batch) if batch <= 3 else _spread(batch, 9))
 
 
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5"])
+def test_baseline_configs_with_metadata(name):
+    """The benchmark configurations (16 / 64-token pages) through the small-block
+    path with get_pa_metadata's schedule, which runs the worklist kernel."""
+    from flydsl_amd import get_pa_metadata
+
+    cfg = CONFIGS[name]
+    print(f"[worklist] {name} with metadata: {cfg.description}", flush=True)
+    w = build_workload(cfg, "cuda")
+    md = get_pa_metadata(w["query"], w["key_cache"], w["context_lengths"], w["kv_indptr"], cfg.num_q_heads,
+                         cfg.num_kv_heads)
+    out, tag, _ = launch(w, metadata=md)
+    assert tag == "ps_small_block"
+    compare_outputs(w, out, _spread(cfg.batch, 6))
+
+
 WORKLIST_CASES = {
+    "bs16_tok_g4": dict(base="c3", batch=6, ctx_kind="uniform", ctx_a=1, ctx_b=3000),
+    "bs16_pt_mtp2_g8": dict(base="c2", batch=4, num_q_heads=16, num_kv_heads=2, query_length=2, ctx_kind="uniform",
+                            ctx_a=2, ctx_b=2500),
+    "bs64_tok_mtp4_g16": dict(base="c5", batch=3, ctx_kind="uniform", ctx_a=4, ctx_b=1500),
     "bs1024_tok": dict(base="c3", batch=3, block_size=1024, ctx_kind="uniform", ctx_a=1, ctx_b=2100),
     "bs32_ql2_g8": dict(base="c2", batch=3, num_q_heads=16, num_kv_heads=2, block_size=32, query_length=2,
                         ctx_kind="uniform", ctx_a=2, ctx_b=1200),
@@ -83,7 +103,7 @@ def test_worklist_partials_and_outputs(case, bins_per_head):
         md["partial_output"].fill_(float("nan"))
         md["partial_lse"].fill_(float("nan"))
     out, tag, _ = launch(w, metadata=md)
-    assert tag == "ps_split_reduce"
+    assert tag == ("ps_small_block" if cfg.block_size in (16, 64) else "ps_split_reduce")
     compare_outputs(w, out, range(cfg.batch))
     n = check_worklist_partials(w, md)
     if bins_per_head == 1:

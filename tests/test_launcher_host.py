@@ -247,3 +247,17 @@ def test_metadata_info_matches_oracle():
     ref = op.get_pa_metadata_info_v1(128, 8, 768)
     assert [s for s, _ in ours] == [s for s, _ in ref]
     assert [str(d).split(".")[-1] for _, d in ours] == [d for _, d in ref]
+
+
+@pytest.mark.parametrize("bs", [16, 64])
+def test_small_block_with_metadata_runs_the_worklist(bs):
+    t = make_paged(bs=bs, ctx=(1027, 300, 2000), num_cu=3)
+    p = plan(t, max_parts=4)
+    assert p.tag == "ps_small_block" and p.wargs is not None and p.dargs is None
+    assert p.wargs.block_size == bs and p.wargs.num_cu == 3
+    # without the flat page list, or with a window, the partition kernel runs
+    assert plan(t, max_parts=4, kv_indptr=None).dargs is not None
+    assert plan(t, sliding_window=300, max_parts=4).dargs is not None
+    # the reference's graph-capture rule for this path still holds
+    with pytest.raises(ValueError, match="small-block PS path"):
+        plan(t, capturing=True)
