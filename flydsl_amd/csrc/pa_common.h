@@ -21,6 +21,7 @@ constexpr int kGroup = 16;              // tokens per MFMA token group
 constexpr int kStep = 64;               // tokens per wave step (4 groups)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kSlack = 8.0f;          // log2 headroom before the online-softmax reference max is raised
 
 // Four fp8 e4m3fn bytes -> four bf16 (exact: every e4m3fn value is a bf16 value).
 __device__ __forceinline__ bf16x4 fp8x4_to_bf16x4(uint32_t w) {

@@ -142,16 +142,226 @@ __device__ __forceinline__ bf16x8 pack_bf16x8(f32x4 a, f32x4 b) {
     return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// Waves per SIMD the decode kernels are compiled for: one 16-row group per wave
+// fits two waves (<= 256 registers each); more row groups per wave hold their
+// accumulators in AGPRs and run one wave per SIMD.
+template <int MTPW>
+constexpr int kWavesPerSimd = MTPW == 1 ? 2 : 1;
+
+// Query rows of one wave: MTPW groups of 16 rows (r = qi*g + gi), the QK B
+// operands and the keys each row may see.  Lane (qrow l16, kg) holds dims
+// 32kg..32kg+31 of its row; keys visible to a row are [lo_n, hi_n) (causal bound
+// ctx+1-ql+qi, window start ctx-ql-sw+qi); lo_max / hi_min bound them over the
+// wave's live rows (wave-uniform).
+template <int MTPW>
+struct RowSet {
+    bf16x8 qop[MTPW][4];
+    int lo_n[MTPW], hi_n[MTPW];
+    int lo_max, hi_min;
+};
+
+template <int MTPW>
+__device__ __forceinline__ void setup_rows(RowSet<MTPW> &rw, const DecodeParams &p, int b, int h, int ctx, int tok_lo,
+                                           int tok_hi, int row_group0, int l16, int kg) {
+    rw.lo_max = tok_lo;
+    rw.hi_min = tok_hi;
+#pragma unroll
+    for (int mg = 0; mg < MTPW; ++mg) {
+        const int n = (row_group0 + mg) * 16 + l16;
+        if (n < p.eqgs) {
+            const int qi = n / p.g;
+            const int gi = n - qi * p.g;
+            const uint16_t *qrow =
+                p.query + (int64_t)(b * p.ql + qi) * p.s_q_seq + (int64_t)(h * p.g + gi) * p.s_q_head + 32 * kg;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) rw.qop[mg][s] = load_q8(qrow + 8 * s, p.q_f16 != 0);
+            rw.hi_n[mg] = min(tok_hi, ctx + 1 - p.ql + qi);
+            rw.lo_n[mg] = p.sw > 0 ? max(tok_lo, ctx - p.ql - p.sw + qi) : tok_lo;
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) rw.qop[mg][s] = bf16x8{};
+            rw.hi_n[mg] = tok_hi;  // padded rows: any finite value, never stored
+            rw.lo_n[mg] = tok_lo;
+        }
+        rw.lo_max = max(rw.lo_max, rw.lo_n[mg]);
+        rw.hi_min = min(rw.hi_min, rw.hi_n[mg]);
+    }
+    // the min / max over the 16 rows of a group: rows differ only through qi
+    for (int sh = 1; sh < 16; sh <<= 1) {
+        rw.lo_max = max(rw.lo_max, __shfl_xor(rw.lo_max, sh, 64));
+        rw.hi_min = min(rw.hi_min, __shfl_xor(rw.hi_min, sh, 64));
+    }
+    rw.lo_max = __builtin_amdgcn_readfirstlane(rw.lo_max);
+    rw.hi_min = __builtin_amdgcn_readfirstlane(rw.hi_min);
+}
+
+// Per-lane online-softmax state.  m_run is the reference max (log2 units) the
+// exponentials, l_run and o are taken against; it is raised only when a step's
+// max exceeds it by more than kSlack, so exp2(logit - m_run) <= 2^kSlack and o is
+// rescaled on few steps.  m_top is the true running max, used for the stats.
+template <int MTPW>
+struct SmState {
+    float m_run[MTPW], l_run[MTPW], m_top[MTPW];
+    f32x4 o[MTPW][8];
+
+    __device__ __forceinline__ void init() {
+#pragma unroll
+        for (int mg = 0; mg < MTPW; ++mg) {
+            m_run[mg] = -INFINITY;
+            m_top[mg] = -INFINITY;
+            l_run[mg] = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 8; ++m) o[mg][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+};
+
+// QK and softmax of one 64-token step: kr holds the step's K ([tile][chunk], 16 fp8
+// each: lane (l16, kg) of tile jt holds token 16*(l16>>2) + 4*jt + (l16&3), dims of
+// chunks 2kg and 2kg+1).  QK tile jt, row 4*kg+i of the MFMA output is token
+// trow + 4*jt + i with trow = t0 + 16*kg, so lane (qrow, kg) ends up owning the 16
+// tokens of group kg -- exactly the tokens of its PV operand row.  Writes the
+// bf16 probabilities of every row group to pop.  After the QK products, after_qk()
+// runs (the K registers are free again).
+template <int MTPW, bool PER_TOKEN, class AfterQk>
+__device__ __forceinline__ void step_qk_softmax(SmState<MTPW> &st, const RowSet<MTPW> &rw, const uint4 (&kr)[4][2],
+                                                const f32x4 (&ksr)[4], const f32x4 (&vsr)[4], float k_fac, int t0,
+                                                int kg, bf16x8 (&pop)[MTPW][2], AfterQk &&after_qk) {
+    const int trow = t0 + 16 * kg;  // token of (tile jt, i) = trow + 4jt + i
+    const bool interior = t0 >= rw.lo_max && t0 + kStep <= rw.hi_min;
+
+    // QK: S[token][qrow] for 4 tiles of 16 tokens
+    f32x4 sc[MTPW][4];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+        const bf16x8 a0 = fp8x8_to_bf16x8(kr[jt][0].x, kr[jt][0].y);
+        const bf16x8 a1 = fp8x8_to_bf16x8(kr[jt][0].z, kr[jt][0].w);
+        const bf16x8 a2 = fp8x8_to_bf16x8(kr[jt][1].x, kr[jt][1].y);
+        const bf16x8 a3 = fp8x8_to_bf16x8(kr[jt][1].z, kr[jt][1].w);
+#pragma unroll
+        for (int mg = 0; mg < MTPW; ++mg) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            acc = mfma_bf16(a0, rw.qop[mg][0], acc);
+            acc = mfma_bf16(a1, rw.qop[mg][1], acc);
+            acc = mfma_bf16(a2, rw.qop[mg][2], acc);
+            acc = mfma_bf16(a3, rw.qop[mg][3], acc);
+            sc[mg][jt] = acc;
+        }
+    }
+    after_qk();
+
+    f32x4 kf[4];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr[jt] * k_fac : f32x4{k_fac, k_fac, k_fac, k_fac};
+
+#pragma unroll
+    for (int mg = 0; mg < MTPW; ++mg) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            sc[mg][jt] *= kf[jt];
+            if (!interior) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = trow + 4 * jt + i;
+                    sc[mg][jt][i] = (t >= rw.lo_n[mg] && t < rw.hi_n[mg]) ? sc[mg][jt][i] : -INFINITY;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[mg][jt][i]);
+        }
+        mx = fmaxf(mx, shfl_xor_f(mx, 16));
+        mx = fmaxf(mx, shfl_xor_f(mx, 32));
+        st.m_top[mg] = fmaxf(st.m_top[mg], mx);
+        const bool raise = mx > st.m_run[mg] + kSlack;  // false while the row has seen no key
+        if (__any(raise)) {                              // wave-uniform
+            const float alpha = raise ? fast_exp2(st.m_run[mg] - mx) : 1.0f;  // 0 on a row's first keys
+            st.m_run[mg] = raise ? mx : st.m_run[mg];
+            st.l_run[mg] *= alpha;
+#pragma unroll
+            for (int m = 0; m < 8; ++m) st.o[mg][m] *= alpha;
+        }
+        const float m_use = st.m_run[mg] == -INFINITY ? 0.0f : st.m_run[mg];
+        float psum = 0.0f;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float pv = fast_exp2(sc[mg][jt][i] - m_use);
+                psum += pv;
+                sc[mg][jt][i] = pv;
+            }
+            if constexpr (PER_TOKEN) sc[mg][jt] *= vsr[jt];
+        }
+        st.l_run[mg] += psum;
+        pop[mg][0] = pack_bf16x8(sc[mg][0], sc[mg][1]);
+        pop[mg][1] = pack_bf16x8(sc[mg][2], sc[mg][3]);
+    }
+}
+
+// PV of one step: O[dim][qrow] += V^T P^T over its 64 tokens; vr[m] holds the 16
+// tokens of group kg of head dim 16m + l16.
+template <int MTPW>
+__device__ __forceinline__ void step_pv(SmState<MTPW> &st, const uint4 (&vr)[8], const bf16x8 (&pop)[MTPW][2]) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const bf16x8 v0 = fp8x8_to_bf16x8(vr[m].x, vr[m].y);
+        const bf16x8 v1 = fp8x8_to_bf16x8(vr[m].z, vr[m].w);
+#pragma unroll
+        for (int mg = 0; mg < MTPW; ++mg) {
+            st.o[mg][m] = mfma_bf16(v0, pop[mg][0], st.o[mg][m]);
+            st.o[mg][m] = mfma_bf16(v1, pop[mg][1], st.o[mg][m]);
+        }
+    }
+}
+
+// Rows of a wave that ran every step of the range itself: sum the four kg-lane
+// partial exp sums of each row, normalise and emit.
+template <int MTPW, class Sink>
+__device__ __forceinline__ void finish_rows(SmState<MTPW> &st, const DecodeParams &p, int row_group0, int l16, int kg,
+                                            float v_fac, const Sink &sink) {
+#pragma unroll
+    for (int mg = 0; mg < MTPW; ++mg) {
+        float lt = st.l_run[mg];
+        lt += shfl_xor_f(lt, 16);
+        lt += shfl_xor_f(lt, 32);
+        const int r = (row_group0 + mg) * 16 + l16;
+        if (r < p.eqgs) {
+            const float inv = lt > 0.f ? v_fac / lt : 0.f;
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const f32x4 v = st.o[mg][m] * inv;
+                const float v4[4] = {v[0], v[1], v[2], v[3]};
+                sink.row(r, 16 * m + 4 * kg, v4);
+            }
+            if (kg == 0) sink.stats(r, lt > 0.f ? lt * fast_exp2(st.m_run[mg] - st.m_top[mg]) : 0.f, st.m_top[mg]);
+        }
+    }
+}
+
+template <class Sink>
+__device__ __forceinline__ void emit_empty(const DecodeParams &p, int nthreads, const Sink &sink) {
+    // empty range (kernels/pa_decode_fp8.py:2591-2598)
+    const int tid = threadIdx.x;
+    for (int r = tid; r < p.eqgs; r += nthreads) sink.stats(r, 0.0f, -INFINITY);
+    const float zero8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int i = tid; i < p.eqgs * (kHeadDim / 8); i += nthreads)
+        sink.row(i / (kHeadDim / 8), (i % (kHeadDim / 8)) * 8, zero8);
+}
+
 // Attention of the query rows of (sequence b, kv head h) over the keys
-// [tok_lo, tok_hi) of the sequence; the result of each row r = qi*g + gi goes to
-// sink.row (normalised output) and sink.stats (exp sum and log2-domain max).
-// ctx is already clamped to the page row's capacity; bt_row is the sequence's
-// page row (block-table row or kv_page_indices window).  Every thread of the
-// workgroup calls this with the same arguments (it synchronises internally).
+// [tok_lo, tok_hi) of the sequence, streaming K / V through registers; the result
+// of each row r = qi*g + gi goes to sink.row (normalised output) and sink.stats
+// (exp sum and log2-domain max).  ctx is already clamped to the page row's
+// capacity; bt_row is the sequence's page row (block-table row or kv_page_indices
+// window).  Every thread of the workgroup calls this with the same arguments (it
+// synchronises internally).
 // The workgroup has NW = RS * NS waves.  Wave w owns query-row groups
 // [rs*MTPW, (rs+1)*MTPW) (rs = w % RS, 16 rows per group) and the steps
-// ns, ns+NS, ... of the range (ns = w / RS).  Waves of the same rs merge their
-// online-softmax states through LDS at the end.
+// ns, ns+NS, ... of the range (ns = w / RS).  Each wave loads its own steps: the
+// next step's K goes into the K registers right after the QK products, its V
+// right after the PV products.  Waves of the same rs merge their online-softmax
+// states through LDS at the end.
 template <int MTPW, int RS, int NS, bool PER_TOKEN, class Sink>
 __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b, const int h, const int ctx,
                                              const int tok_lo, const int tok_hi, const int32_t *bt_row,
@@ -167,60 +377,16 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
     const int kg = lane >> 4;
     const int bs = 1 << p.bs_log2;
 
-    if (tok_lo >= tok_hi) {  // empty range (kernels/pa_decode_fp8.py:2591-2598)
-        for (int r = tid; r < p.eqgs; r += NW * 64) sink.stats(r, 0.0f, -INFINITY);
-        const float zero8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int i = tid; i < p.eqgs * (D / 8); i += NW * 64) sink.row(i / (D / 8), (i % (D / 8)) * 8, zero8);
+    if (tok_lo >= tok_hi) {
+        emit_empty(p, NW * 64, sink);
         return;
     }
-
-    // ---- query operands (B of the QK MFMA): lane (qrow l16, kg) holds dims 32kg..32kg+31.
-    // Keys visible to a row: [lo_n, hi_n) (causal bound ctx+1-ql+qi, window start ctx-ql-sw+qi).
-    bf16x8 qop[MTPW][4];
-    int lo_n[MTPW], hi_n[MTPW];
-    int lo_max = tok_lo, hi_min = tok_hi;  // wave-uniform bounds over the wave's live rows
-#pragma unroll
-    for (int mg = 0; mg < MTPW; ++mg) {
-        const int n = (rs * MTPW + mg) * 16 + l16;
-        if (n < p.eqgs) {
-            const int qi = n / p.g;
-            const int gi = n - qi * p.g;
-            const uint16_t *qrow =
-                p.query + (int64_t)(b * p.ql + qi) * p.s_q_seq + (int64_t)(h * p.g + gi) * p.s_q_head + 32 * kg;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) qop[mg][s] = load_q8(qrow + 8 * s, p.q_f16 != 0);
-            hi_n[mg] = min(tok_hi, ctx + 1 - p.ql + qi);
-            lo_n[mg] = p.sw > 0 ? max(tok_lo, ctx - p.ql - p.sw + qi) : tok_lo;
-        } else {
-#pragma unroll
-            for (int s = 0; s < 4; ++s) qop[mg][s] = bf16x8{};
-            hi_n[mg] = tok_hi;  // padded rows: any finite value, never stored
-            lo_n[mg] = tok_lo;
-        }
-        lo_max = max(lo_max, lo_n[mg]);
-        hi_min = min(hi_min, hi_n[mg]);
-    }
-    // the min / max over the 16 rows of a group: rows differ only through qi
-    for (int sh = 1; sh < 16; sh <<= 1) {
-        lo_max = max(lo_max, __shfl_xor(lo_max, sh, 64));
-        hi_min = min(hi_min, __shfl_xor(hi_min, sh, 64));
-    }
-    lo_max = __builtin_amdgcn_readfirstlane(lo_max);
-    hi_min = __builtin_amdgcn_readfirstlane(hi_min);
-
+    RowSet<MTPW> rw;
+    setup_rows<MTPW>(rw, p, b, h, ctx, tok_lo, tok_hi, rs * MTPW, l16, kg);
     const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
     const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
-
-    // ---- per-lane running state
-    float m_run[MTPW], l_run[MTPW];
-    f32x4 o[MTPW][8];
-#pragma unroll
-    for (int mg = 0; mg < MTPW; ++mg) {
-        m_run[mg] = -INFINITY;
-        l_run[mg] = 0.0f;
-#pragma unroll
-        for (int m = 0; m < 8; ++m) o[mg][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    SmState<MTPW> st;
+    st.init();
 
     const int ngroups = (tok_hi - tok_lo + kGroup - 1) / kGroup;
     const int nsteps = (ngroups + 3) / 4;
@@ -286,126 +452,42 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
             nkb = k_ptr(nxt);
             v_loc(nxt, nvofs, nsofs);
         }
-        const int t0 = tok_lo + step * kStep;
-        const int trow = t0 + 16 * kg;  // token of (tile jt, i) = trow + 4jt + i
-        const bool interior = t0 >= lo_max && t0 + kStep <= hi_min;
-
-        // QK: S[token][qrow] for 4 tiles of 16 tokens
-        f32x4 sc[MTPW][4];
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-            const bf16x8 a0 = fp8x8_to_bf16x8(kr[jt][0].x, kr[jt][0].y);
-            const bf16x8 a1 = fp8x8_to_bf16x8(kr[jt][0].z, kr[jt][0].w);
-            const bf16x8 a2 = fp8x8_to_bf16x8(kr[jt][1].x, kr[jt][1].y);
-            const bf16x8 a3 = fp8x8_to_bf16x8(kr[jt][1].z, kr[jt][1].w);
-#pragma unroll
-            for (int mg = 0; mg < MTPW; ++mg) {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                acc = mfma_bf16(a0, qop[mg][0], acc);
-                acc = mfma_bf16(a1, qop[mg][1], acc);
-                acc = mfma_bf16(a2, qop[mg][2], acc);
-                acc = mfma_bf16(a3, qop[mg][3], acc);
-                sc[mg][jt] = acc;
-            }
-        }
-        if (has_nxt) load_k(nkb);  // K registers are free again
-
-        f32x4 kf[4];
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr[jt] * k_fac : f32x4{k_fac, k_fac, k_fac, k_fac};
-        f32x4 vsc[4];
+        f32x4 ksc[4], vsc[4];
         if constexpr (PER_TOKEN) {
 #pragma unroll
-            for (int jt = 0; jt < 4; ++jt) vsc[jt] = vsr[jt];
-            if (has_nxt) load_scales(nsofs);
+            for (int jt = 0; jt < 4; ++jt) {
+                ksc[jt] = ksr[jt];
+                vsc[jt] = vsr[jt];
+            }
         }
-
         bf16x8 pop[MTPW][2];
-#pragma unroll
-        for (int mg = 0; mg < MTPW; ++mg) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int jt = 0; jt < 4; ++jt) {
-                sc[mg][jt] *= kf[jt];
-                if (!interior) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int t = trow + 4 * jt + i;
-                        sc[mg][jt][i] = (t >= lo_n[mg] && t < hi_n[mg]) ? sc[mg][jt][i] : -INFINITY;
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[mg][jt][i]);
+        step_qk_softmax<MTPW, PER_TOKEN>(st, rw, kr, ksc, vsc, k_fac, tok_lo + step * kStep, kg, pop, [&] {
+            if (has_nxt) {
+                load_k(nkb);  // K registers are free again
+                if constexpr (PER_TOKEN) load_scales(nsofs);
             }
-            mx = fmaxf(mx, shfl_xor_f(mx, 16));
-            mx = fmaxf(mx, shfl_xor_f(mx, 32));
-            const float m_new = fmaxf(m_run[mg], mx);
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = fast_exp2(m_run[mg] - m_use);
-            m_run[mg] = m_new;
-            float psum = 0.0f;
-#pragma unroll
-            for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float pv = fast_exp2(sc[mg][jt][i] - m_use);
-                    psum += pv;
-                    sc[mg][jt][i] = pv;
-                }
-                if constexpr (PER_TOKEN) sc[mg][jt] *= vsc[jt];
-            }
-            l_run[mg] = l_run[mg] * alpha + psum;
-#pragma unroll
-            for (int m = 0; m < 8; ++m) o[mg][m] *= alpha;
-            pop[mg][0] = pack_bf16x8(sc[mg][0], sc[mg][1]);
-            pop[mg][1] = pack_bf16x8(sc[mg][2], sc[mg][3]);
-        }
-
-        // PV: O[dim][qrow] += V^T P^T over the step's 64 tokens
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            const bf16x8 v0 = fp8x8_to_bf16x8(vr[m].x, vr[m].y);
-            const bf16x8 v1 = fp8x8_to_bf16x8(vr[m].z, vr[m].w);
-#pragma unroll
-            for (int mg = 0; mg < MTPW; ++mg) {
-                o[mg][m] = mfma_bf16(v0, pop[mg][0], o[mg][m]);
-                o[mg][m] = mfma_bf16(v1, pop[mg][1], o[mg][m]);
-            }
-        }
+        });
+        step_pv<MTPW>(st, vr, pop);
         if (has_nxt) load_v(nvofs);  // V registers are free again
         step = nxt;
     }
 
-    // ---- finish: sum the four kg-lane partial exp sums of each query row
-#pragma unroll
-    for (int mg = 0; mg < MTPW; ++mg) {
-        float lt = l_run[mg];
-        lt += shfl_xor_f(lt, 16);
-        lt += shfl_xor_f(lt, 32);
-        l_run[mg] = lt;
-    }
-
     if constexpr (NS == 1) {
+        finish_rows<MTPW>(st, p, rs * MTPW, l16, kg, v_fac, sink);
+    } else {
+        // sum the four kg-lane partial exp sums of each query row
 #pragma unroll
         for (int mg = 0; mg < MTPW; ++mg) {
-            const int r = (rs * MTPW + mg) * 16 + l16;
-            if (r < p.eqgs) {
-                const float L = l_run[mg];
-                const float inv = L > 0.f ? v_fac / L : 0.f;
-#pragma unroll
-                for (int m = 0; m < 8; ++m) {
-                    const f32x4 v = o[mg][m] * inv;
-                    const float v4[4] = {v[0], v[1], v[2], v[3]};
-                    sink.row(r, 16 * m + 4 * kg, v4);
-                }
-                if (kg == 0) sink.stats(r, L, m_run[mg]);
-            }
+            float lt = st.l_run[mg];
+            lt += shfl_xor_f(lt, 16);
+            lt += shfl_xor_f(lt, 32);
+            st.l_run[mg] = lt;
         }
-    } else {
         constexpr int DP = D + 4;
         __shared__ float s_o[NW][16][DP];
         __shared__ float s_m[NW][16];
         __shared__ float s_l[NW][16];
+        __shared__ float s_t[NW][16];
         // merge: RS*16 rows x D outputs per pass, E per thread
         constexpr int E = RS * 16 * D / (NW * 64);
         const int flat = tid * E;
@@ -415,15 +497,19 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
 #pragma unroll
         for (int mg = 0; mg < MTPW; ++mg) {
 #pragma unroll
-            for (int m = 0; m < 8; ++m) *reinterpret_cast<f32x4 *>(&s_o[wave][l16][16 * m + 4 * kg]) = o[mg][m];
+            for (int m = 0; m < 8; ++m) *reinterpret_cast<f32x4 *>(&s_o[wave][l16][16 * m + 4 * kg]) = st.o[mg][m];
             if (kg == 0) {
-                s_m[wave][l16] = m_run[mg];
-                s_l[wave][l16] = l_run[mg];
+                s_m[wave][l16] = st.m_run[mg];
+                s_l[wave][l16] = st.l_run[mg];
+                s_t[wave][l16] = st.m_top[mg];
             }
             __syncthreads();
-            float M = -INFINITY;
+            float M = -INFINITY, Mt = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < NS; ++j) M = fmaxf(M, s_m[j * RS + mrs][n]);
+            for (int j = 0; j < NS; ++j) {
+                M = fmaxf(M, s_m[j * RS + mrs][n]);
+                Mt = fmaxf(Mt, s_t[j * RS + mrs][n]);
+            }
             const float Ms = M == -INFINITY ? 0.0f : M;
             float f[NS];
             float L = 0.f;
@@ -447,16 +533,209 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
                     }
                     sink.row(r, d0 + e0, v8);
                 }
-                if (d0 == 0) sink.stats(r, L, M);
+                if (d0 == 0) sink.stats(r, L > 0.f ? L * fast_exp2(M - Mt) : 0.f, Mt);
             }
             __syncthreads();
         }
     }
 }
 
+// ------------------------------------------------------- LDS-staged K / V stream
+// For layouts where every wave of the workgroup consumes every step (NS == 1),
+// the workgroup streams the steps' K / V through an LDS ring: each step's 16 KB
+// (plus its per-token scales) is loaded once per workgroup with direct
+// global -> LDS loads (global_load_lds_dwordx4, 16 bytes per lane, lane i landing
+// at M0 + 16 i), kStages - 1 steps ahead of the step being computed.  The loads
+// are issued from inline assembly, so the compiler does not order LDS reads
+// behind them; each wave waits for its own loads of a step with an explicit
+// s_waitcnt vmcnt(n) (loads complete in issue order, and n counts only loads this
+// wave issued later, so the wait is never short) and a barrier then publishes the
+// step to every wave.  Page indices for the load addresses come from an LDS window
+// of the page row, so no vector memory load of the compiler's own sits between
+// the asynchronous ones.
+//
+// Stage layout (bytes): K [4 groups][8 chunks][16 tokens][16] with the group
+// stride padded to 2112 (the QK operand reads of lanes 0-3 and 4-7 then hit
+// different banks), V [4 groups][128 dims][16 tokens], then the per-token K and V
+// scales [4 groups][16] f32 each.
+constexpr int kStages = 4;
+constexpr int kKGroupStride = 2048 + 64;
+constexpr int kStageV = 4 * kKGroupStride;
+constexpr int kStageS = kStageV + 4 * 2048;
+constexpr int kStageBytes = kStageS + 512;
+constexpr int kPageWin = 1024;  // page-row entries held in LDS at a time
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const lds_void_t *)p;
+}
+
+// 16 bytes from gptr to LDS byte address lds_base + 16 * lane.
+__device__ __forceinline__ void dma16(const void *gptr, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory", "m0");
+}
+
+// Wait until at most N of this wave's vector memory loads are outstanding and
+// its LDS operations are done, then meet the other waves.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+template <int MTPW, int RS, bool PER_TOKEN, class Sink>
+__device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const int b, const int h, const int ctx,
+                                                    const int tok_lo, const int tok_hi, const int32_t *bt_row,
+                                                    const int row_len, const Sink &sink) {
+    constexpr int NW = RS;
+    constexpr int KROWS = 8 / NW;             // K rows (1 KB each) a wave loads per step
+    constexpr int VROWS = 8 / NW;             // V rows
+    constexpr int SLANES = 32 / NW;           // lanes of a wave loading 16 bytes of scales
+    constexpr int R = KROWS + VROWS + (PER_TOKEN ? 1 : 0);  // loads a wave issues per step
+    static_assert(NW == 1 || NW == 2 || NW == 4, "1, 2 or 4 waves");
+    __shared__ __attribute__((aligned(16))) uint8_t s_ring[kStages * kStageBytes];
+    __shared__ int32_t s_pages[kPageWin];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15;
+    const int kg = lane >> 4;
+    const int bs = 1 << p.bs_log2;
+
+    // every wave is done with the ring and the page window of an earlier range
+    wait_vm_barrier<0>();
+    if (tok_lo >= tok_hi) {
+        emit_empty(p, NW * 64, sink);
+        return;
+    }
+    RowSet<MTPW> rw;
+    setup_rows<MTPW>(rw, p, b, h, ctx, tok_lo, tok_hi, wave * MTPW, l16, kg);
+    const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
+    const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
+    SmState<MTPW> st;
+    st.init();
+
+    const int ngroups = (tok_hi - tok_lo + kGroup - 1) / kGroup;
+    const int nsteps = (ngroups + 3) / 4;
+    const int last_group = tok_lo + (ngroups - 1) * kGroup;
+    const int last_page = last_group >> p.bs_log2;
+    const uint8_t *kc_h = p.kc + (int64_t)h * p.s_k_head;
+    const uint8_t *vc_h = p.vc + (int64_t)h * p.s_v_head;
+    const int64_t kchunk = (int64_t)bs * 16;
+    const uint32_t ring = lds_addr(s_ring);
+
+    int wbase = tok_lo >> p.bs_log2;
+    auto load_window = [&](int base) {  // every wave is past its last use of the window
+        wbase = base;
+        const int n = min(kPageWin, last_page - base + 1);
+        for (int i = tid; i < n; i += NW * 64) s_pages[i] = base + i < row_len ? bt_row[base + i] : 0;
+        __syncthreads();
+    };
+    load_window(wbase);
+
+    // physical block and 16-token sub-row of group g of step q
+    auto group_loc = [&](int q, int g, int &phys, int &sub) {
+        const int gs = min(tok_lo + q * kStep + 16 * g, last_group);
+        const int e = s_pages[(gs >> p.bs_log2) - wbase];
+        phys = min(max(e, 0), p.num_blocks - 1);
+        sub = (gs & (bs - 1)) >> 4;
+    };
+    auto issue = [&](int q) {
+        const int lastg_page = min(tok_lo + q * kStep + 48, last_group) >> p.bs_log2;
+        if (lastg_page - wbase >= kPageWin) load_window((tok_lo + q * kStep) >> p.bs_log2);
+        const uint32_t sb = ring + (uint32_t)((q % kStages) * kStageBytes);
+#pragma unroll
+        for (int j = 0; j < KROWS; ++j) {  // K rows: (group g, chunks 4*half .. 4*half+3)
+            const int r = wave + NW * j;
+            const int g = r >> 1, half = r & 1;
+            int phys, sub;
+            group_loc(q, g, phys, sub);
+            const uint8_t *src = kc_h + (int64_t)phys * p.s_k_block + (4 * half + (lane >> 4)) * kchunk + sub * 256 +
+                                 (lane & 15) * 16;
+            dma16(src, __builtin_amdgcn_readfirstlane(sb + g * kKGroupStride + half * 1024));
+        }
+#pragma unroll
+        for (int j = 0; j < VROWS; ++j) {  // V rows: (group g, dims 64*half .. 64*half+63)
+            const int r = wave + NW * j;
+            const int g = r >> 1, half = r & 1;
+            int phys, sub;
+            group_loc(q, g, phys, sub);
+            const uint8_t *src = vc_h + (int64_t)phys * p.s_v_block + sub * (kHeadDim * 16) + (64 * half + lane) * 16;
+            dma16(src, __builtin_amdgcn_readfirstlane(sb + kStageV + g * 2048 + half * 1024));
+        }
+        if constexpr (PER_TOKEN) {  // 32 pieces of 16 bytes: K scales of groups 0-3, then V scales
+            if (lane < SLANES) {
+                const int piece = wave * SLANES + lane;
+                const int g = (piece & 15) >> 2;
+                int phys, sub;
+                group_loc(q, g, phys, sub);
+                const float *src = (piece < 16 ? p.ks : p.vs) + (int64_t)phys * p.s_ks_block +
+                                   (int64_t)h * p.s_ks_head + sub * 16 + 4 * (piece & 3);
+                dma16(src, __builtin_amdgcn_readfirstlane(sb + kStageS + wave * SLANES * 16));
+            }
+        }
+    };
+
+#pragma unroll
+    for (int q = 0; q < kStages - 1; ++q)
+        if (q < nsteps) issue(q);
+
+    for (int n = 0; n < nsteps; ++n) {
+        // this wave's loads of step n are done once at most (later steps issued) * R remain
+        const int later = min(kStages - 2, nsteps - 1 - n);
+        if (later >= 2) wait_vm_barrier<2 * R>();
+        else if (later == 1) wait_vm_barrier<R>();
+        else wait_vm_barrier<0>();
+        // every wave has finished step n-1, so its stage takes step n + kStages - 1
+        if (n + kStages - 1 < nsteps) issue(n + kStages - 1);
+
+        const uint8_t *sk = s_ring + (n % kStages) * kStageBytes;
+        uint4 kr[4][2];
+        uint4 vr[8];
+        f32x4 ksr[4], vsr[4];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            const uint8_t *kp = sk + (l16 >> 2) * kKGroupStride + (2 * kg) * 256 + (4 * jt + (l16 & 3)) * 16;
+            kr[jt][0] = *reinterpret_cast<const uint4 *>(kp);
+            kr[jt][1] = *reinterpret_cast<const uint4 *>(kp + 256);
+        }
+        if constexpr (PER_TOKEN) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                ksr[q4] = *reinterpret_cast<const f32x4 *>(sk + kStageS + kg * 64 + 16 * q4);
+                vsr[q4] = *reinterpret_cast<const f32x4 *>(sk + kStageS + 256 + kg * 64 + 16 * q4);
+            }
+        }
+        bf16x8 pop[MTPW][2];
+        step_qk_softmax<MTPW, PER_TOKEN>(st, rw, kr, ksr, vsr, k_fac, tok_lo + n * kStep, kg, pop, [] {});
+#pragma unroll
+        for (int m = 0; m < 8; ++m)
+            vr[m] = *reinterpret_cast<const uint4 *>(sk + kStageV + kg * 2048 + (16 * m + l16) * 16);
+        step_pv<MTPW>(st, vr, pop);
+    }
+    finish_rows<MTPW>(st, p, wave * MTPW, l16, kg, v_fac, sink);
+}
+
 // Split-context decode: one workgroup per (sequence, kv head, partition slot).
+// Layout <MTPW, RS, NS>: NS >= 1 streams K / V through registers (attend_range);
+// NS == 0 stages them through LDS for RS waves that all take every step
+// (attend_range_staged).
+template <int RS, int NS>
+constexpr int kThreads = RS * (NS > 0 ? NS : 1) * 64;
+
+template <int MTPW, int RS, int NS, bool PER_TOKEN, class Sink>
+__device__ __forceinline__ void attend(const DecodeParams &p, int b, int h, int ctx, int tok_lo, int tok_hi,
+                                       const int32_t *bt_row, int row_len, const Sink &sink) {
+    if constexpr (NS == 0)
+        attend_range_staged<MTPW, RS, PER_TOKEN>(p, b, h, ctx, tok_lo, tok_hi, bt_row, row_len, sink);
+    else
+        attend_range<MTPW, RS, NS, PER_TOKEN>(p, b, h, ctx, tok_lo, tok_hi, bt_row, sink);
+}
+
 template <int MTPW, int RS, int NS, bool PER_TOKEN>
-__global__ __launch_bounds__(RS * NS * 64) void pa_decode_partition_kernel(const DecodeParams p) {
+__global__ __launch_bounds__((kThreads<RS, NS>), kWavesPerSimd<MTPW>) void pa_decode_partition_kernel(const DecodeParams p) {
     const int b = blockIdx.x;
     const int h = blockIdx.y;
     const int z = blockIdx.z;
@@ -484,7 +763,7 @@ __global__ __launch_bounds__(RS * NS * 64) void pa_decode_partition_kernel(const
                         p.max_logits + b * p.s_es_seq + h * p.s_es_head + z * p.s_es_part,
                         b,
                         h};
-    attend_range<MTPW, RS, NS, PER_TOKEN>(p, b, h, ctx, tok_lo, tok_hi, p.bt + (int64_t)b * p.s_bt_seq, sink);
+    attend<MTPW, RS, NS, PER_TOKEN>(p, b, h, ctx, tok_lo, tok_hi, p.bt + (int64_t)b * p.s_bt_seq, p.max_blocks, sink);
 }
 
 // ---------------------------------------------------------------- worklist path
@@ -536,7 +815,7 @@ struct WorkSink {
 // range-checked, so a malformed or overflowed worklist skips work instead of
 // touching memory outside the tensors.
 template <int MTPW, int RS, int NS, bool PER_TOKEN>
-__global__ __launch_bounds__(RS * NS * 64, 2) void pa_decode_worklist_kernel(const WorklistParams w) {
+__global__ __launch_bounds__((kThreads<RS, NS>), kWavesPerSimd<MTPW>) void pa_decode_worklist_kernel(const WorklistParams w) {
     const DecodeParams &p = w.kv;
     const int c = blockIdx.x;
     const int wbeg = max(__builtin_amdgcn_readfirstlane(w.work_indptr[c]), 0);
@@ -567,7 +846,7 @@ __global__ __launch_bounds__(RS * NS * 64, 2) void pa_decode_worklist_kernel(con
         const int tok_lo = (int)min(lp0 * kPartition, (int64_t)ctx);
         const int tok_hi = (int)max(min(lp1 * kPartition, (int64_t)ctx), (int64_t)tok_lo);
         const WorkSink sink{w, h, qo_start, pidx};
-        attend_range<MTPW, RS, NS, PER_TOKEN>(p, b, h, ctx, tok_lo, tok_hi, w.kv_page_indices + page0, sink);
+        attend<MTPW, RS, NS, PER_TOKEN>(p, b, h, ctx, tok_lo, tok_hi, w.kv_page_indices + page0, page1 - page0, sink);
     }
 }
 
@@ -688,19 +967,29 @@ __global__ __launch_bounds__(64) void pa_lse_reduce_kernel(const ReduceParams p)
 
 template <int MTPW, int RS, int NS, bool PT>
 hipError_t launch_decode(const DecodeParams &p, dim3 grid, hipStream_t s) {
-    hipLaunchKernelGGL((pa_decode_partition_kernel<MTPW, RS, NS, PT>), grid, dim3(RS * NS * 64), 0, s, p);
+    hipLaunchKernelGGL((pa_decode_partition_kernel<MTPW, RS, NS, PT>), grid, dim3((kThreads<RS, NS>)), 0, s, p);
     return hipGetLastError();
 }
 
 // Wave layout per number of 16-row query groups (ql * group_size / 16, rounded up):
-// one group -> 4 waves split the steps; more groups -> one wave per group (the
-// waves of a workgroup stream the same K/V, which the L2 serves after the first).
-// Tuning knob: PA_FP8_NS overrides the waves per workgroup of the one-group layout.
+//   one group    -> <1,1,4>: four waves split the steps;
+//   two groups   -> <2,1,4>: every wave holds both groups, four waves split the steps;
+//   3 / 4 groups -> <2,2,2>: each wave holds two groups (one fp8 -> bf16 conversion of
+//                   K / V feeds both), two wave pairs split the rows, the pairs split
+//                   the steps.
+// Tuning knobs (environment, read once): PA_FP8_NS overrides the waves of the
+// one-group layout (1/2/4/8); PA_FP8_WIDE picks the 3 / 4-group layout
+// (1: <1,4,1> one wave per group, 2: <2,2,2>, 4: <4,1,4>).
+int env_int(const char *name) {
+    const char *e = getenv(name);
+    return e ? atoi(e) : 0;
+}
 int env_ns() {
-    static const int v = [] {
-        const char *e = getenv("PA_FP8_NS");
-        return e ? atoi(e) : 0;
-    }();
+    static const int v = env_int("PA_FP8_NS");
+    return v;
+}
+int env_wide() {
+    static const int v = env_int("PA_FP8_WIDE");
     return v;
 }
 
@@ -714,15 +1003,20 @@ hipError_t dispatch_decode(const DecodeParams &p, int mtp, dim3 grid, hipStream_
         case 8: return launch_decode<1, 1, 8, PT>(p, grid, s);
         default: return launch_decode<1, 1, 4, PT>(p, grid, s);
         }
-    case 2: return launch_decode<1, 2, 2, PT>(p, grid, s);
-    case 3: return launch_decode<1, 3, 1, PT>(p, grid, s);
-    default: return launch_decode<1, 4, 1, PT>(p, grid, s);
+    case 2: return launch_decode<2, 1, 4, PT>(p, grid, s);
+    default:
+        switch (env_wide()) {
+        case 1: return launch_decode<1, 4, 1, PT>(p, grid, s);
+        case 2: return launch_decode<2, 2, 2, PT>(p, grid, s);
+        case 5: return launch_decode<2, 2, 0, PT>(p, grid, s);
+        default: return launch_decode<1, 4, 0, PT>(p, grid, s);
+        }
     }
 }
 
 template <int MTPW, int RS, int NS, bool PT>
 hipError_t launch_worklist(const WorklistParams &w, dim3 grid, hipStream_t s) {
-    hipLaunchKernelGGL((pa_decode_worklist_kernel<MTPW, RS, NS, PT>), grid, dim3(RS * NS * 64), 0, s, w);
+    hipLaunchKernelGGL((pa_decode_worklist_kernel<MTPW, RS, NS, PT>), grid, dim3((kThreads<RS, NS>)), 0, s, w);
     return hipGetLastError();
 }
 
@@ -730,9 +1024,14 @@ template <bool PT>
 hipError_t dispatch_worklist(const WorklistParams &w, int mtp, dim3 grid, hipStream_t s) {
     switch (mtp) {
     case 1: return launch_worklist<1, 1, 4, PT>(w, grid, s);
-    case 2: return launch_worklist<1, 2, 2, PT>(w, grid, s);
-    case 3: return launch_worklist<1, 3, 1, PT>(w, grid, s);
-    default: return launch_worklist<1, 4, 1, PT>(w, grid, s);
+    case 2: return launch_worklist<2, 1, 4, PT>(w, grid, s);
+    default:
+        switch (env_wide()) {
+        case 1: return launch_worklist<1, 4, 1, PT>(w, grid, s);
+        case 2: return launch_worklist<2, 2, 2, PT>(w, grid, s);
+        case 5: return launch_worklist<2, 2, 0, PT>(w, grid, s);
+        default: return launch_worklist<1, 4, 0, PT>(w, grid, s);
+        }
     }
 }
 

@@ -54,6 +54,9 @@ SMALL_CASES = {
                      ctx_a=4, ctx_b=1500),
     "mtp3_tok": dict(base="c5", batch=3, query_length=3, ctx_kind="uniform", ctx_a=3, ctx_b=1500),
     "mtp4_pt": dict(base="c5", batch=3, per_token=False, ctx_kind="uniform", ctx_a=4, ctx_b=1500),
+    # 16-token pages and contexts past 16K tokens: a slot's pages outgrow the
+    # 1024-entry page window of the LDS-staged layout, which is then refilled
+    "mtp4_g16_bs16_long": dict(base="c5", batch=2, block_size=16, ctx_kind="uniform", ctx_a=17000, ctx_b=40000),
 }
 
 

@@ -78,6 +78,7 @@ WORKLIST_CASES = {
     "bs256_tok_mtp4_g16": dict(base="c5", batch=4, block_size=256, ctx_kind="uniform", ctx_a=4, ctx_b=3000),
     "bs512_mtp3_g4": dict(base="c2", batch=5, block_size=512, query_length=3, ctx_kind="uniform", ctx_a=3,
                           ctx_b=4000),
+    "bs16_long_mtp4_g16": dict(base="c5", batch=2, block_size=16, ctx_kind="uniform", ctx_a=17000, ctx_b=40000),
     "bs1024_long": dict(base="c2", batch=2, num_q_heads=16, num_kv_heads=2, block_size=1024, ctx_kind="uniform",
                         ctx_a=9000, ctx_b=20000),
 }
