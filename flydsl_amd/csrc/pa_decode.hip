@@ -558,12 +558,21 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
 // stride padded to 2112 (the QK operand reads of lanes 0-3 and 4-7 then hit
 // different banks), V [4 groups][128 dims][16 tokens], then the per-token K and V
 // scales [4 groups][16] f32 each.
-constexpr int kStages = 4;
-constexpr int kKGroupStride = 2048 + 64;
+#ifndef PA_FP8_STAGES
+#define PA_FP8_STAGES 4  // ring depth (steps in flight + 1)
+#endif
+#ifndef PA_FP8_KPAD
+#define PA_FP8_KPAD 64  // bytes of padding after each K group
+#endif
+#ifndef PA_FP8_PAGE_WINDOW
+#define PA_FP8_PAGE_WINDOW 1024  // page-row entries held in LDS at a time
+#endif
+constexpr int kStages = PA_FP8_STAGES;
+constexpr int kKGroupStride = 2048 + PA_FP8_KPAD;
 constexpr int kStageV = 4 * kKGroupStride;
 constexpr int kStageS = kStageV + 4 * 2048;
 constexpr int kStageBytes = kStageS + 512;
-constexpr int kPageWin = 1024;  // page-row entries held in LDS at a time
+constexpr int kPageWin = PA_FP8_PAGE_WINDOW;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -584,76 +593,53 @@ __device__ __forceinline__ void wait_vm_barrier() {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-template <int MTPW, int RS, bool PER_TOKEN, class Sink>
-__device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const int b, const int h, const int ctx,
-                                                    const int tok_lo, const int tok_hi, const int32_t *bt_row,
-                                                    const int row_len, const Sink &sink) {
-    constexpr int NW = RS;
-    constexpr int KROWS = 8 / NW;             // K rows (1 KB each) a wave loads per step
-    constexpr int VROWS = 8 / NW;             // V rows
-    constexpr int SLANES = 32 / NW;           // lanes of a wave loading 16 bytes of scales
-    constexpr int R = KROWS + VROWS + (PER_TOKEN ? 1 : 0);  // loads a wave issues per step
+// Loads steps of one (sequence, kv head) token range into an LDS ring for NW waves:
+// K rows, V rows and (per-token) the scale piece of step q go to stage q % STAGES;
+// each wave issues R loads per step.  issue(q) needs every wave past its last use
+// of stage q % STAGES (the caller's barrier guarantees it).
+template <int NW, int STAGES, bool PER_TOKEN>
+struct KvStager {
+    static constexpr int KROWS = 8 / NW;    // K rows (1 KB each) a wave loads per step
+    static constexpr int VROWS = 8 / NW;    // V rows
+    static constexpr int SLANES = 32 / NW;  // lanes of a wave loading 16 bytes of scales
+    static constexpr int R = KROWS + VROWS + (PER_TOKEN ? 1 : 0);
     static_assert(NW == 1 || NW == 2 || NW == 4, "1, 2 or 4 waves");
-    __shared__ __attribute__((aligned(16))) uint8_t s_ring[kStages * kStageBytes];
-    __shared__ int32_t s_pages[kPageWin];
+    static_assert((STAGES - 2) * R <= 63, "vmcnt range");
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int l16 = lane & 15;
-    const int kg = lane >> 4;
-    const int bs = 1 << p.bs_log2;
+    const DecodeParams &p;
+    uint8_t *ring;
+    int32_t *pages;
+    const int32_t *bt_row;
+    const uint8_t *kc_h, *vc_h;
+    int64_t kchunk;
+    uint32_t ring_addr;
+    int h, row_len, tok_lo, last_group, last_page, nsteps, wbase, bs, tid, lane, wave;
 
-    // every wave is done with the ring and the page window of an earlier range
-    wait_vm_barrier<0>();
-    if (tok_lo >= tok_hi) {
-        emit_empty(p, NW * 64, sink);
-        return;
-    }
-    RowSet<MTPW> rw;
-    setup_rows<MTPW>(rw, p, b, h, ctx, tok_lo, tok_hi, wave * MTPW, l16, kg);
-    const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
-    const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
-    SmState<MTPW> st;
-    st.init();
-
-    const int ngroups = (tok_hi - tok_lo + kGroup - 1) / kGroup;
-    const int nsteps = (ngroups + 3) / 4;
-    const int last_group = tok_lo + (ngroups - 1) * kGroup;
-    const int last_page = last_group >> p.bs_log2;
-    const uint8_t *kc_h = p.kc + (int64_t)h * p.s_k_head;
-    const uint8_t *vc_h = p.vc + (int64_t)h * p.s_v_head;
-    const int64_t kchunk = (int64_t)bs * 16;
-    const uint32_t ring = lds_addr(s_ring);
-
-    int wbase = tok_lo >> p.bs_log2;
-    auto load_window = [&](int base) {  // every wave is past its last use of the window
+    __device__ __forceinline__ void load_window(int base) {  // every wave is past its last use of the window
         wbase = base;
         const int n = min(kPageWin, last_page - base + 1);
-        for (int i = tid; i < n; i += NW * 64) s_pages[i] = base + i < row_len ? bt_row[base + i] : 0;
+        for (int i = tid; i < n; i += NW * 64) pages[i] = base + i < row_len ? bt_row[base + i] : 0;
         __syncthreads();
-    };
-    load_window(wbase);
-
+    }
     // physical block and 16-token sub-row of group g of step q
-    auto group_loc = [&](int q, int g, int &phys, int &sub) {
+    __device__ __forceinline__ void group_loc(int q, int g, int &phys, int &sub) const {
         const int gs = min(tok_lo + q * kStep + 16 * g, last_group);
-        const int e = s_pages[(gs >> p.bs_log2) - wbase];
+        const int e = pages[(gs >> p.bs_log2) - wbase];
         phys = min(max(e, 0), p.num_blocks - 1);
         sub = (gs & (bs - 1)) >> 4;
-    };
-    auto issue = [&](int q) {
+    }
+    __device__ __forceinline__ void issue(int q) {
         const int lastg_page = min(tok_lo + q * kStep + 48, last_group) >> p.bs_log2;
         if (lastg_page - wbase >= kPageWin) load_window((tok_lo + q * kStep) >> p.bs_log2);
-        const uint32_t sb = ring + (uint32_t)((q % kStages) * kStageBytes);
+        const uint32_t sb = ring_addr + (uint32_t)((q % STAGES) * kStageBytes);
 #pragma unroll
         for (int j = 0; j < KROWS; ++j) {  // K rows: (group g, chunks 4*half .. 4*half+3)
             const int r = wave + NW * j;
             const int g = r >> 1, half = r & 1;
             int phys, sub;
             group_loc(q, g, phys, sub);
-            const uint8_t *src = kc_h + (int64_t)phys * p.s_k_block + (4 * half + (lane >> 4)) * kchunk + sub * 256 +
-                                 (lane & 15) * 16;
+            const uint8_t *src =
+                kc_h + (int64_t)phys * p.s_k_block + (4 * half + (lane >> 4)) * kchunk + sub * 256 + (lane & 15) * 16;
             dma16(src, __builtin_amdgcn_readfirstlane(sb + g * kKGroupStride + half * 1024));
         }
 #pragma unroll
@@ -676,22 +662,89 @@ __device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const
                 dma16(src, __builtin_amdgcn_readfirstlane(sb + kStageS + wave * SLANES * 16));
             }
         }
-    };
-
+    }
+    __device__ __forceinline__ void prologue() {
 #pragma unroll
-    for (int q = 0; q < kStages - 1; ++q)
-        if (q < nsteps) issue(q);
+        for (int q = 0; q < STAGES - 1; ++q)
+            if (q < nsteps) issue(q);
+    }
+    template <int L>
+    __device__ __forceinline__ void wait_later(int later) {
+        if constexpr (L > 0) {
+            if (later >= L) {
+                wait_vm_barrier<L * R>();
+                return;
+            }
+            wait_later<L - 1>(later);
+        } else {
+            wait_vm_barrier<0>();
+        }
+    }
+    // Step n is in LDS for every wave, and every wave is done with step n-1, after
+    // this wave's loads of step n landed (at most (later steps issued) * R of its
+    // loads remain outstanding) and the barrier.
+    __device__ __forceinline__ void wait_step(int n) { wait_later<STAGES - 2>(min(STAGES - 2, nsteps - 1 - n)); }
+    __device__ __forceinline__ const uint8_t *stage(int n) const { return ring + (n % STAGES) * kStageBytes; }
+};
 
-    for (int n = 0; n < nsteps; ++n) {
-        // this wave's loads of step n are done once at most (later steps issued) * R remain
-        const int later = min(kStages - 2, nsteps - 1 - n);
-        if (later >= 2) wait_vm_barrier<2 * R>();
-        else if (later == 1) wait_vm_barrier<R>();
-        else wait_vm_barrier<0>();
-        // every wave has finished step n-1, so its stage takes step n + kStages - 1
-        if (n + kStages - 1 < nsteps) issue(n + kStages - 1);
+template <int NW, int STAGES, bool PER_TOKEN>
+__device__ __forceinline__ void init_stager(KvStager<NW, STAGES, PER_TOKEN> &sg, uint8_t *ring, int32_t *pages,
+                                            const DecodeParams &p, int h, int tok_lo, int tok_hi,
+                                            const int32_t *bt_row, int row_len) {
+    sg.ring = ring;
+    sg.pages = pages;
+    sg.ring_addr = lds_addr(ring);
+    sg.bt_row = bt_row;
+    sg.row_len = row_len;
+    sg.h = h;
+    sg.kc_h = p.kc + (int64_t)h * p.s_k_head;
+    sg.vc_h = p.vc + (int64_t)h * p.s_v_head;
+    sg.bs = 1 << p.bs_log2;
+    sg.kchunk = (int64_t)sg.bs * 16;
+    sg.tok_lo = tok_lo;
+    const int ngroups = (tok_hi - tok_lo + kGroup - 1) / kGroup;
+    sg.nsteps = (ngroups + 3) / 4;
+    sg.last_group = tok_lo + (ngroups - 1) * kGroup;
+    sg.last_page = sg.last_group >> p.bs_log2;
+    sg.tid = threadIdx.x;
+    sg.lane = threadIdx.x & 63;
+    sg.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    sg.load_window(tok_lo >> p.bs_log2);
+}
 
-        const uint8_t *sk = s_ring + (n % kStages) * kStageBytes;
+// Row-split LDS-staged layout: RS waves each own MTPW row groups and all take
+// every 64-token step from the ring.
+template <int MTPW, int RS, bool PER_TOKEN, class Sink>
+__device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const int b, const int h, const int ctx,
+                                                    const int tok_lo, const int tok_hi, const int32_t *bt_row,
+                                                    const int row_len, const Sink &sink) {
+    constexpr int NW = RS;
+    __shared__ __attribute__((aligned(16))) uint8_t s_ring[kStages * kStageBytes];
+    __shared__ int32_t s_pages[kPageWin];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15;
+    const int kg = lane >> 4;
+
+    // every wave is done with the ring and the page window of an earlier range
+    wait_vm_barrier<0>();
+    if (tok_lo >= tok_hi) {
+        emit_empty(p, NW * 64, sink);
+        return;
+    }
+    RowSet<MTPW> rw;
+    setup_rows<MTPW>(rw, p, b, h, ctx, tok_lo, tok_hi, wave * MTPW, l16, kg);
+    const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
+    const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
+    SmState<MTPW> st;
+    st.init();
+    KvStager<NW, kStages, PER_TOKEN> sg{p};
+    init_stager(sg, s_ring, s_pages, p, h, tok_lo, tok_hi, bt_row, row_len);
+    sg.prologue();
+    for (int n = 0; n < sg.nsteps; ++n) {
+        sg.wait_step(n);
+        if (n + kStages - 1 < sg.nsteps) sg.issue(n + kStages - 1);
+        const uint8_t *sk = sg.stage(n);
         uint4 kr[4][2];
         uint4 vr[8];
         f32x4 ksr[4], vsr[4];
@@ -718,7 +771,6 @@ __device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const
     finish_rows<MTPW>(st, p, wave * MTPW, l16, kg, v_fac, sink);
 }
 
-// Split-context decode: one workgroup per (sequence, kv head, partition slot).
 // Layout <MTPW, RS, NS>: NS >= 1 streams K / V through registers (attend_range);
 // NS == 0 stages them through LDS for RS waves that all take every step
 // (attend_range_staged).
@@ -862,45 +914,72 @@ struct ReduceV1Params {
     int32_t num_groups, num_heads, max_qlen, partial_rows, output_rows, partial_map_len, out_dtype;
 };
 
-// Merge of the partials of one (reduce group, query row, head): one wave, lane owns
-// head dims 2*lane and 2*lane+1.  Weights exp(lse_j - LSE) with LSE the
-// log-sum-exp of the partials' log-sum-exps.
-__global__ __launch_bounds__(64) void pa_reduce_v1_kernel(const ReduceV1Params p) {
-    const int lane = threadIdx.x;
-    const int grp = blockIdx.x, hd = blockIdx.y, qi = blockIdx.z;
+// Merge of the partials of one (reduce group, query row, head) per wave, four
+// waves per workgroup; lane owns head dims 2*lane and 2*lane+1.  Lane j first
+// loads the log-sum-exp of partial j (all partials in parallel), the wave forms
+// LSE = log sum_j exp(lse_j) and the weights exp(lse_j - LSE), and the partial
+// rows are then summed four at a time with the weights and row indices broadcast
+// from the lanes that hold them.
+__global__ __launch_bounds__(256) void pa_reduce_v1_kernel(const ReduceV1Params p) {
+    const int lane = threadIdx.x & 63;
+    const int grp = blockIdx.x;
+    const int row = blockIdx.y * 4 + (threadIdx.x >> 6);  // (qi, head) = (row / heads, row % heads)
+    const int qi = row / p.num_heads, hd = row - qi * p.num_heads;
     const int j0 = max(p.reduce_indptr[grp], 0);
     const int j1 = min(p.reduce_indptr[grp + 1], p.partial_map_len);
-    if (j0 >= j1) return;
+    if (j0 >= j1 || qi >= p.max_qlen) return;
     const int qo_start = p.final_map[2 * grp];
     const int qo_end = p.final_map[2 * grp + 1];
     if (qi >= qo_end - qo_start || qo_start < 0 || qo_start + qi >= p.output_rows) return;
+    const int np = j1 - j0;
 
+    // pass 1: max and exp-sum of the partials' log-sum-exps (64 per lane round)
     float mloc = -INFINITY;
-    for (int j = j0 + lane; j < j1; j += 64) {
-        const int row = p.partial_map[j] + qi;
-        if (row >= 0 && row < p.partial_rows) mloc = fmaxf(mloc, p.pl[row * p.s_pl_row + hd * p.s_pl_head]);
+    for (int j = lane; j < np; j += 64) {
+        const int r = p.partial_map[j0 + j] + qi;
+        if (r >= 0 && r < p.partial_rows) mloc = fmaxf(mloc, p.pl[r * p.s_pl_row + hd * p.s_pl_head]);
     }
 #pragma unroll
     for (int sh = 32; sh >= 1; sh >>= 1) mloc = fmaxf(mloc, shfl_xor_f(mloc, sh));
     const float Ms = mloc == -INFINITY ? 0.0f : mloc;
     float wl = 0.f;
-    for (int j = j0 + lane; j < j1; j += 64) {
-        const int row = p.partial_map[j] + qi;
-        if (row >= 0 && row < p.partial_rows) wl += fast_exp2((p.pl[row * p.s_pl_row + hd * p.s_pl_head] - Ms) * kLog2e);
+    for (int j = lane; j < np; j += 64) {
+        const int r = p.partial_map[j0 + j] + qi;
+        if (r >= 0 && r < p.partial_rows) wl += fast_exp2((p.pl[r * p.s_pl_row + hd * p.s_pl_head] - Ms) * kLog2e);
     }
 #pragma unroll
     for (int sh = 32; sh >= 1; sh >>= 1) wl += shfl_xor_f(wl, sh);
     const float inv = wl > 0.f ? 1.0f / wl : 0.0f;
 
+    // pass 2: weighted sum of the partial rows, 64 partials per round
     float a0 = 0.f, a1 = 0.f;
-    for (int j = j0; j < j1; ++j) {
-        const int row = p.partial_map[j] + qi;
-        if (row < 0 || row >= p.partial_rows) continue;
-        const float wgt = fast_exp2((p.pl[row * p.s_pl_row + hd * p.s_pl_head] - Ms) * kLog2e) * inv;
-        if (wgt != 0.f) {
-            const float2 two = *reinterpret_cast<const float2 *>(p.po + row * p.s_po_row + hd * p.s_po_head + 2 * lane);
-            a0 += wgt * two.x;
-            a1 += wgt * two.y;
+    for (int c0 = 0; c0 < np; c0 += 64) {
+        const int j = c0 + lane;
+        int r = -1;
+        float w = 0.f;
+        if (j < np) {
+            r = p.partial_map[j0 + j] + qi;
+            if (r >= 0 && r < p.partial_rows) w = fast_exp2((p.pl[r * p.s_pl_row + hd * p.s_pl_head] - Ms) * kLog2e) * inv;
+            else r = -1;
+        }
+        const int n = min(64, np - c0);
+        for (int k = 0; k < n; k += 4) {
+            float2 v[4];
+            float wk[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int src = min(k + u, n - 1);
+                wk[u] = k + u < n ? __shfl(w, src, 64) : 0.f;
+                const int rk = __shfl(r, src, 64);
+                v[u] = (wk[u] != 0.f && rk >= 0)
+                           ? *reinterpret_cast<const float2 *>(p.po + rk * p.s_po_row + hd * p.s_po_head + 2 * lane)
+                           : make_float2(0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                a0 += wk[u] * v[u].x;
+                a1 += wk[u] * v[u].y;
+            }
         }
     }
     const int64_t orow = qo_start + qi;
@@ -1335,7 +1414,9 @@ int pa_fp8_reduce_v1(const pa_fp8_reduce_v1_args *a, void *stream) {
     p.output_rows = a->output_rows;
     p.partial_map_len = a->partial_map_len;
     p.out_dtype = a->out_dtype;
-    hipLaunchKernelGGL(pa_reduce_v1_kernel, dim3(a->num_groups, a->num_heads, a->max_qlen), dim3(64), 0,
+    const int64_t rows = (int64_t)a->num_heads * a->max_qlen;  // (qi, head) rows of a group, four per workgroup
+    if ((rows + 3) / 4 > 65535) return PA_FP8_ERR_SHAPE;
+    hipLaunchKernelGGL(pa_reduce_v1_kernel, dim3(a->num_groups, (rows + 3) / 4), dim3(256), 0,
                        reinterpret_cast<hipStream_t>(stream), p);
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;

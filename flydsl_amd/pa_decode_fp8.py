@@ -525,9 +525,10 @@ def pa_decode_ps_launch(
     * ``sliding_window > 0``: sliding-window split-context path (partition
       kernel + log-sum-exp reduce; every block size), reading ``block_tables``;
     * block sizes 16 / 64: small-block path.  Given ``metadata`` (from
-      ``get_pa_metadata``) and ``kv_page_indices`` / ``kv_indptr`` it runs the
-      worklist kernel over that schedule, which balances ragged batches;
-      otherwise the split-context partition kernel reading ``block_tables``;
+      ``get_pa_metadata``) of a ragged batch and ``kv_page_indices`` /
+      ``kv_indptr`` it runs the worklist kernel over that schedule, which
+      balances the batch; otherwise the split-context partition kernel reading
+      ``block_tables``;
     * other block sizes: the persistent path -- the worklist kernel over
       ``metadata`` (computed with ``get_pa_metadata`` when absent, which
       synchronises once) reading pages through ``kv_page_indices`` /
@@ -636,12 +637,15 @@ def _build_plan(
     small = block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES
     # Block sizes other than 16 / 64 take the persistent path, as in the reference.
     # The small-block path also runs the worklist kernel when the caller hands
-    # in get_pa_metadata's schedule with the flat page list: the schedule balances
-    # ragged batches across CUs, which fixed partition slots cannot.  The tag
-    # stays "ps_small_block" and exp_sums / max_logits / temporary_output are
+    # in get_pa_metadata's schedule with the flat page list and the batch is
+    # ragged: the schedule balances ragged batches across CUs, which fixed
+    # partition slots cannot (equal-length batches keep the partition kernel,
+    # whose slots are balanced already and which skips the worklist reads).  The
+    # tag stays "ps_small_block" and exp_sums / max_logits / temporary_output are
     # not touched (they are scratch of the split-context kernels).
-    if sliding_window <= 0 and (not small or (metadata is not None and kv_page_indices is not None
-                                              and kv_indptr is not None)):
+    balanced_worklist = (metadata is not None and kv_page_indices is not None and kv_indptr is not None
+                         and not metadata.get("uniform_context", False))
+    if sliding_window <= 0 and (not small or balanced_worklist):
         if small:
             if is_graph_capturing and (exp_sums is None or max_logits is None or temporary_output is None):
                 raise ValueError(  # the reference's small-block rule (kernels/pa_decode_fp8.py:3030-3034)
@@ -731,7 +735,11 @@ def get_pa_metadata(
         num_cu=num_sm,
     )
     work_info_flat = work_info.reshape(-1).contiguous()
-    num_partials = int(reduce_indptr[-1].item())
+    # one host read (the reference reads reduce_indptr[-1] here too): the partial
+    # count, and whether every sequence has the same context length
+    ctx_i32 = context_lengths.to(torch.int32)
+    host = torch.stack([reduce_indptr[-1], (ctx_i32.max() == ctx_i32.min()).to(torch.int32)]).cpu()
+    num_partials, uniform = int(host[0]), bool(host[1])
     partial_output = torch.empty(
         ((num_partials + 1) * query_length, 1, num_query_heads, head_size), dtype=torch.float32, device=dev
     )
@@ -751,6 +759,9 @@ def get_pa_metadata(
         "stride_po_ql": num_query_heads * head_size,
         "stride_pl_ql": num_query_heads,
         "query_length": query_length,
+        # equal context lengths: fixed partition slots are already balanced, so the
+        # small-block path keeps its partition kernel instead of the worklist
+        "uniform_context": uniform,
     }
 
 

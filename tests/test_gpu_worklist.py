@@ -60,6 +60,8 @@ def test_baseline_configs_with_metadata(name):
     w = build_workload(cfg, "cuda")
     md = get_pa_metadata(w["query"], w["key_cache"], w["context_lengths"], w["kv_indptr"], cfg.num_q_heads,
                          cfg.num_kv_heads)
+    assert md["uniform_context"] == (len(set(w["context_list"])) == 1)
+    md["uniform_context"] = False  # run the worklist kernel on every config, c2 included
     out, tag, _ = launch(w, metadata=md)
     assert tag == "ps_small_block"
     compare_outputs(w, out, _spread(cfg.batch, 6))
