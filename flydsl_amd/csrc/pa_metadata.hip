@@ -1,7 +1,7 @@
 // get_pa_metadata_v1 worklist scheduler on the device (kernels/pa_metadata.py:145-420).
 //
 // The schedule is a serial state machine over (CU bin, batch) pairs, so one
-// thread runs it; it is tiny (O(num_cu + batch) steps per kv head) and keeps
+// thread runs it (O(num_cu + batch) steps per kv head, reading LDS); it keeps
 // the caller free of a device->host copy of context_lens.  Buffers are written
 // exactly where the reference writes them, including its overwrite-safe
 // unconditional stores; only the valid prefixes are defined.  Every store is
@@ -25,60 +25,121 @@ struct MetaParams {
 
 __device__ __forceinline__ int cdiv_u(int a, int b) { return (int)(((unsigned)a + (unsigned)b - 1u) / (unsigned)b); }
 
+constexpr int kStagedBatches = 4096;   // batches whose qo offsets and partition counts are staged in LDS
+constexpr int kRingRows = 1024;        // work_info rows buffered in LDS before a coalesced copy-out
+constexpr int kStagedIndptr = 4097;    // work_indptr entries kept in LDS (num_cu + 1)
+constexpr int kStagedReduce = 2048;    // batches whose reduce maps are kept in LDS
+constexpr int kStagedSplits = 4096;    // reduce_partial_map entries kept in LDS
+
+// Every lane runs the same serial state machine on the same (uniform) values.
+// Its outputs go to LDS -- a ring of work_info rows, work_indptr and the reduce
+// maps -- and the 64 lanes copy them to global memory with coalesced stores, so
+// the loop is not throttled by single-lane global stores.  Per-batch partition
+// counts and qo offsets are staged in LDS first (and the counts summed by all
+// lanes).  Buffers larger than the LDS copies are written to global memory
+// directly by lane 0.
 __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaParams p) {
-    if (threadIdx.x != 0) return;
+    __shared__ int32_t s_np[kStagedBatches];
+    __shared__ int32_t s_sq[kStagedBatches + 1];
+    __shared__ __attribute__((aligned(16))) int32_t s_ring[kRingRows * 8];
+    __shared__ int32_t s_wi[kStagedIndptr];
+    __shared__ int32_t s_ri[kStagedReduce + 1];
+    __shared__ int32_t s_rfm[2 * kStagedReduce];
+    __shared__ int32_t s_rpm[kStagedSplits];
+    const int lane = threadIdx.x;
+    const bool lead = lane == 0;
+    const int staged = min(p.nb, kStagedBatches);
+    const bool wi_lds = p.num_cu + 1 <= kStagedIndptr;
+    const bool red_lds = p.nb <= kStagedReduce;
+    const bool rpm_lds = p.max_split_tiles <= kStagedSplits;
+    long long part = 0;
+    for (int b = lane; b < p.nb; b += 64) {
+        const int n = cdiv_u(p.ctx[b], p.kv_gran);
+        part += n;
+        if (b < staged) s_np[b] = n;
+    }
+    for (int b = lane; b <= staged; b += 64) s_sq[b] = p.sq[b];
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) part += __shfl_xor(part, sh, 64);
+    __syncthreads();
     const int nspk = p.num_cu / p.nhk;
-    long long sum_blocks = 0;
-    for (int b = 0; b < p.nb; ++b) sum_blocks += cdiv_u(p.ctx[b], p.kv_gran);
+    const long long sum_blocks = part;
     const int average = (int)(sum_blocks / nspk);
     const int reminder = (int)(sum_blocks % nspk);
     auto quota = [&](int c) { return average + ((c % nspk) < reminder ? 1 : 0); };
-    auto npart = [&](int b) { return cdiv_u(p.ctx[b], p.kv_gran); };
+    auto npart = [&](int b) { return b < staged ? s_np[b] : cdiv_u(p.ctx[b], p.kv_gran); };
+    auto sq = [&](int b) { return b <= staged ? s_sq[b] : p.sq[b]; };
+    auto put_wi = [&](int i, int v) {
+        if (wi_lds) { if (lead) s_wi[i] = v; }
+        else if (lead) p.work_indptr[i] = v;
+    };
+    auto put_ri = [&](int i, int v) {
+        if (red_lds) { if (lead) s_ri[i] = v; }
+        else if (lead) p.reduce_indptr[i] = v;
+    };
+    auto put_rfm = [&](int g, int a, int b) {
+        if (red_lds) { if (lead) { s_rfm[2 * g] = a; s_rfm[2 * g + 1] = b; } }
+        else if (lead) { p.reduce_final_map[2 * g] = a; p.reduce_final_map[2 * g + 1] = b; }
+    };
+    auto put_rpm = [&](int i, int v) {
+        if (rpm_lds) { if (lead) s_rpm[i] = v; }
+        else if (lead) p.reduce_partial_map[i] = v;
+    };
+    // rows [flushed, upto) of the ring go to work_info (rows past max_work are dropped)
+    int flushed = 0;
+    auto flush = [&](int upto) {
+        __syncthreads();
+        for (int i = flushed * 2 + lane; i < upto * 2; i += 64) {  // half rows of 16 bytes
+            const int row = i >> 1;
+            if (row < p.max_work)
+                reinterpret_cast<int4 *>(p.work_info)[i] =
+                    reinterpret_cast<const int4 *>(s_ring)[((row % kRingRows) << 1) | (i & 1)];
+        }
+        __syncthreads();
+        flushed = upto;
+    };
     bool overflow = false;
 
-    p.work_indptr[0] = 0;
-    p.reduce_indptr[0] = 0;
+    put_wi(0, 0);
+    put_ri(0, 0);
     int cid = 0, num_works = 0, lri = 0, grt = 0;
-    for (int kh = 0; kh < p.nhk; ++kh) {
+    // one kv head of the state machine (kernels/pa_metadata.py:212-387), from the current cid
+    auto run_head = [&](int kh) {
         const int32_t qhr =
             (int32_t)((((unsigned)(kh + 1) * (unsigned)p.gqa) << 16) | (((unsigned)kh * (unsigned)p.gqa) & 0xFFFFu));
         int batch = 0, kvblk = 0, nsplit = 0, pidx = 0, kvbeg = 0;
         int kvend = p.nb > 0 ? npart(0) : 0;
-        int remain = quota(cid);
+        int cpos = cid % nspk;  // cid % nspk, kept incrementally
+        int remain = average + (cpos < reminder ? 1 : 0);
         lri = 0;
         grt = 0;
         while (cid < p.num_cu && batch < p.nb) {
             const int remain_kv = (kvend - kvbeg) - kvblk;
             const bool do_finish = remain >= remain_kv;
-            const int qo_start = p.sq[batch];
-            const int qo_end = p.sq[batch + 1];
+            const int qo_start = sq(batch);
+            const int qo_end = sq(batch + 1);
             const int kv_start = kvbeg + kvblk;
             const int w_ploc = do_finish ? (nsplit > 0 ? pidx : -1) : pidx;
             const int w_kv_end = do_finish ? kvend : min(kv_start + remain, kvend);
+            // the work slot at num_works is written every iteration (overwritten when not emitted)
+            if (num_works >= flushed + kRingRows) flush(num_works);
             if (num_works < p.max_work) {
-                int32_t *w = p.work_info + (long long)num_works * 8;
-                w[0] = batch;
-                w[1] = w_ploc;
-                w[2] = qo_start;
-                w[3] = qo_end;
-                w[4] = kv_start;
-                w[5] = w_kv_end;
-                w[6] = 0;
-                w[7] = qhr;
+                if (lead) {
+                    int4 *w = reinterpret_cast<int4 *>(s_ring) + ((num_works % kRingRows) << 1);
+                    w[0] = make_int4(batch, w_ploc, qo_start, qo_end);
+                    w[1] = make_int4(kv_start, w_kv_end, 0, qhr);
+                }
             } else {
                 overflow = true;
             }
             const bool do_reduce = do_finish && nsplit > 0;
             const int num_splits = nsplit + 1;
-            if (grt + 1 <= p.nb) p.reduce_indptr[grt + 1] = lri + num_splits;
-            if (grt < p.nb) {
-                p.reduce_final_map[2 * grt] = qo_start;
-                p.reduce_final_map[2 * grt + 1] = qo_end;
-            }
+            if (grt + 1 <= p.nb) put_ri(grt + 1, lri + num_splits);
+            if (grt < p.nb) put_rfm(grt, qo_start, qo_end);
             if (do_reduce) {
-                for (int s = 0; s < num_splits; ++s) {
-                    if (lri + s < p.max_split_tiles)
-                        p.reduce_partial_map[lri + s] = pidx - (nsplit - s) * p.ql;
+                for (int s2 = 0; s2 < num_splits; ++s2) {
+                    if (lri + s2 < p.max_split_tiles)
+                        put_rpm(lri + s2, pidx - (nsplit - s2) * p.ql);
                     else
                         overflow = true;
                 }
@@ -95,26 +156,76 @@ __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaParams p) 
                 nsplit = 0;
                 kvbeg = kvend;
                 kvend = kvend + (batch < p.nb ? npart(batch) : 0);
-                p.work_indptr[cid + 1] = n_nworks;
+                put_wi(cid + 1, n_nworks);
             } else {
                 const bool emit = remain > 0;
                 n_nworks = emit ? num_works + 1 : num_works;
                 pidx = emit ? pidx + p.ql : pidx;
                 kvblk = emit ? kvblk + remain : kvblk;
                 nsplit = emit ? nsplit + 1 : nsplit;
-                p.work_indptr[cid + 1] = n_nworks;
+                put_wi(cid + 1, n_nworks);
                 cid = cid + 1;
-                remain = quota(cid);
+                cpos = cpos + 1 == nspk ? 0 : cpos + 1;
+                remain = average + (cpos < reminder ? 1 : 0);
             }
             num_works = n_nworks;
             lri = n_lri;
             grt = n_grt;
         }
         if (cid < p.num_cu) cid += 1;
+    };
+
+    run_head(0);
+    // Head 0 filled exactly bins [0, nspk): every later head then repeats its
+    // schedule on bins [k*nspk, (k+1)*nspk) (quotas depend on cid % nspk only and
+    // the per-head state restarts), shifted by k*W works and with its own head
+    // range, and leaves the same reduce maps.  Replicate it in parallel; otherwise
+    // run the remaining heads through the state machine.
+    const int W = num_works;
+    const bool replicated = p.nhk > 1 && cid == nspk && W <= kRingRows && flushed == 0;
+    if (replicated) {
+        __syncthreads();
+        for (int i = lane; i < (p.nhk - 1) * W; i += 64) {
+            const int k = 1 + i / W, j = i - (k - 1) * W;
+            const int row = k * W + j;
+            if (row >= p.max_work) continue;
+            const int32_t qhr = (int32_t)((((unsigned)(k + 1) * (unsigned)p.gqa) << 16) |
+                                          (((unsigned)k * (unsigned)p.gqa) & 0xFFFFu));
+            const int4 *src = reinterpret_cast<const int4 *>(s_ring) + (j << 1);
+            int4 hi = src[1];
+            hi.w = qhr;
+            reinterpret_cast<int4 *>(p.work_info)[row * 2] = src[0];
+            reinterpret_cast<int4 *>(p.work_info)[row * 2 + 1] = hi;
+        }
+        if (p.nhk * W > p.max_work) overflow = true;
+        for (int i = lane; i < (p.nhk - 1) * nspk; i += 64) {  // work_indptr[k*nspk + j] for j in 1..nspk
+            const int k = 1 + i / nspk, j = 1 + (i - (k - 1) * nspk);
+            const int v = (wi_lds ? s_wi[j] : p.work_indptr[j]) + k * W;
+            if (wi_lds) s_wi[k * nspk + j] = v;
+            else p.work_indptr[k * nspk + j] = v;
+        }
+        __syncthreads();
+        cid = p.nhk * nspk;
+        num_works = p.nhk * W;
+    } else {
+        for (int kh = 1; kh < p.nhk; ++kh) run_head(kh);
     }
-    for (int i = cid; i <= p.num_cu; ++i) p.work_indptr[i] = num_works;
-    for (int i = grt; i <= p.nb; ++i) p.reduce_indptr[i] = lri;
-    if (overflow) p.work_indptr[0] = -1;
+    for (int i = cid; i <= p.num_cu; ++i) put_wi(i, num_works);
+    for (int i = grt; i <= p.nb; ++i) put_ri(i, lri);
+    // The ring still holds rows [flushed, num_works]; the last slot written (num_works) is
+    // copied too, as the reference leaves it in the buffer.  After a replication the ring
+    // holds head 0's W rows only (its slot W would overwrite head 1's first row).
+    flush(replicated ? W : min(num_works + 1, flushed + kRingRows));
+    if (wi_lds)
+        for (int i = lane; i <= p.num_cu; i += 64) p.work_indptr[i] = s_wi[i];
+    if (red_lds) {
+        for (int i = lane; i <= p.nb; i += 64) p.reduce_indptr[i] = s_ri[i];
+        for (int i = lane; i < 2 * min(grt + 1, p.nb); i += 64) p.reduce_final_map[i] = s_rfm[i];
+    }
+    if (rpm_lds)
+        for (int i = lane; i < min(lri + 1, p.max_split_tiles); i += 64) p.reduce_partial_map[i] = s_rpm[i];
+    __syncthreads();
+    if (lead && overflow) p.work_indptr[0] = -1;
 }
 
 }  // namespace

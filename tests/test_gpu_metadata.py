@@ -71,3 +71,24 @@ def test_get_pa_metadata_c3_shape():
     np.testing.assert_array_equal(md["partition_indptr"].cpu().numpy(), np.concatenate([[0], np.cumsum(parts)]))
     npart = int(v["reduce_indptr"][-1])
     assert md["partial_output"].shape == ((npart + 1) * 1, 1, 32, 128)
+
+
+def test_device_scheduler_past_the_lds_staging_capacity():
+    """More batches than the scheduler stages in LDS (8192): the rest are read
+    from global memory, with the same result."""
+    rng = np.random.default_rng(99)
+    ctx = [int(x) for x in rng.integers(1, 600, size=9000)]
+    got, ref = run_device(ctx, 2, 4, 2, 64, 256)
+    for key, val in op.metadata_valid_prefixes(ref).items():
+        np.testing.assert_array_equal(op.metadata_valid_prefixes(got)[key], val, err_msg=key)
+
+
+@pytest.mark.parametrize("b,nhk,num_cu", [(3000, 1, 512), (200, 8, 4104)])
+def test_device_scheduler_ring_wrap_and_large_bin_counts(b, nhk, num_cu):
+    """More works than the scheduler's 1024-row LDS ring (copied out as it fills),
+    and more bins than its LDS copy of work_indptr holds."""
+    rng = np.random.default_rng(b)
+    ctx = [int(x) for x in rng.integers(1, 3000, size=b)]
+    got, ref = run_device(ctx, 1, 4, nhk, num_cu, 256)
+    for key, val in op.metadata_valid_prefixes(ref).items():
+        np.testing.assert_array_equal(op.metadata_valid_prefixes(got)[key], val, err_msg=key)
