@@ -13,7 +13,7 @@ from pathlib import Path
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("PA_FP8_LIB", str(_HERE / "libpa_fp8.so")))
 
-PA_FP8_ABI_VERSION = 2
+PA_FP8_ABI_VERSION = 3
 PA_FP8_BF16, PA_FP8_F16, PA_FP8_F32 = 0, 1, 2
 
 _vp = ctypes.c_void_p
@@ -70,6 +70,8 @@ class DecodeArgs(ctypes.Structure):
         ("stride_o_len", _i64),
         ("stride_o_head", _i64),
         ("stride_o_group", _i64),
+        ("waves_per_slot", _i32),
+        ("reserved", _i32),
     ]
 
 

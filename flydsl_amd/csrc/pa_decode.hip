@@ -490,6 +490,7 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
         __shared__ float s_t[NW][16];
         // merge: RS*16 rows x D outputs per pass, E per thread
         constexpr int E = RS * 16 * D / (NW * 64);
+        static_assert(E >= 4 && E % 4 == 0 && E * NW * 64 == RS * 16 * D, "merge covers each row pass exactly");
         const int flat = tid * E;
         const int mrs = flat / (16 * D);  // row split this thread merges
         const int n = (flat / D) % 16;
@@ -521,11 +522,12 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
             const float inv = L > 0.f ? v_fac / L : 0.f;
             const int r = (mrs * MTPW + mg) * 16 + n;
             if (r < p.eqgs) {
+                constexpr int EW = E < 8 ? E : 8;  // outputs per store (E is 4 with 8 waves)
 #pragma unroll
-                for (int e0 = 0; e0 < E; e0 += 8) {
-                    float v8[8];
+                for (int e0 = 0; e0 < E; e0 += EW) {
+                    float v8[EW];
 #pragma unroll
-                    for (int j2 = 0; j2 < 8; ++j2) {
+                    for (int j2 = 0; j2 < EW; ++j2) {
                         float a = 0.f;
 #pragma unroll
                         for (int j = 0; j < NS; ++j) a += s_o[j * RS + mrs][n][d0 + e0 + j2] * f[j];
@@ -1056,16 +1058,12 @@ hipError_t launch_decode(const DecodeParams &p, dim3 grid, hipStream_t s) {
 //   3 / 4 groups -> <2,2,2>: each wave holds two groups (one fp8 -> bf16 conversion of
 //                   K / V feeds both), two wave pairs split the rows, the pairs split
 //                   the steps.
-// Tuning knobs (environment, read once): PA_FP8_NS overrides the waves of the
-// one-group layout (1/2/4/8); PA_FP8_WIDE picks the 3 / 4-group layout
+// The waves of the one-group layout come with the launch (waves_per_slot).
+// Tuning knob (environment, read once): PA_FP8_WIDE picks the 3 / 4-group layout
 // (1: <1,4,1> one wave per group, 2: <2,2,2>, 4: <4,1,4>).
 int env_int(const char *name) {
     const char *e = getenv(name);
     return e ? atoi(e) : 0;
-}
-int env_ns() {
-    static const int v = env_int("PA_FP8_NS");
-    return v;
 }
 int env_wide() {
     static const int v = env_int("PA_FP8_WIDE");
@@ -1073,10 +1071,10 @@ int env_wide() {
 }
 
 template <bool PT>
-hipError_t dispatch_decode(const DecodeParams &p, int mtp, dim3 grid, hipStream_t s) {
+hipError_t dispatch_decode(const DecodeParams &p, int mtp, int waves, dim3 grid, hipStream_t s) {
     switch (mtp) {
     case 1:
-        switch (env_ns()) {
+        switch (waves) {
         case 1: return launch_decode<1, 1, 1, PT>(p, grid, s);
         case 2: return launch_decode<1, 1, 2, PT>(p, grid, s);
         case 8: return launch_decode<1, 1, 8, PT>(p, grid, s);
@@ -1158,6 +1156,9 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
     if (a->max_context_partition_num < 1 || a->max_context_partition_num > 65535) return PA_FP8_ERR_PARTITIONS;
     if (a->query_dtype != PA_FP8_BF16 && a->query_dtype != PA_FP8_F16) return PA_FP8_ERR_DTYPE;
     if (a->num_kv_heads > 65535 || a->sliding_window < 0) return PA_FP8_ERR_SHAPE;
+    if (a->waves_per_slot != 0 && a->waves_per_slot != 1 && a->waves_per_slot != 2 && a->waves_per_slot != 4 &&
+        a->waves_per_slot != 8)
+        return PA_FP8_ERR_SHAPE;
     if (a->direct_output) {
         if (a->max_context_partition_num != 1) return PA_FP8_ERR_PARTITIONS;
         if (a->out_dtype != PA_FP8_BF16 && a->out_dtype != PA_FP8_F16 && a->out_dtype != PA_FP8_F32)
@@ -1237,7 +1238,9 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
     const dim3 grid(a->batch_size, a->num_kv_heads, a->max_context_partition_num);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int mtp = (eqgs + 15) / 16;
-    const hipError_t err = a->per_token_kv ? dispatch_decode<true>(p, mtp, grid, s) : dispatch_decode<false>(p, mtp, grid, s);
+    const int waves = a->waves_per_slot;
+    const hipError_t err =
+        a->per_token_kv ? dispatch_decode<true>(p, mtp, waves, grid, s) : dispatch_decode<false>(p, mtp, waves, grid, s);
     return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
 }
 

@@ -265,21 +265,39 @@ class _Plan:
         return self.tag
 
 
-# Default partition count when the caller passes max_context_partition_num=0:
-# enough workgroups to fill the GPU at two waves per SIMD (4 waves each), and
-# slots no longer than _MAX_SLOT_TOKENS of the longest possible sequence, so
-# ragged batches stay balanced.  (get_recommended_splits keeps the reference
-# formula for callers that ask for it.)
+# Default partition count when the caller passes max_context_partition_num=0,
+# together with the waves per workgroup of the one-row-group layout.  Eight waves
+# resident per CU (two per SIMD) keep enough K/V loads in flight: either two
+# 4-wave workgroups per CU, or -- when the (sequence, kv head) pairs are at most
+# one per CU -- one 8-wave workgroup per slot, which needs fewer slots (no
+# partials, no reduce at one slot).  Slots hold at most _MAX_SLOT_TOKENS of the
+# longest possible sequence, so ragged batches stay balanced.
+# (get_recommended_splits keeps the reference formula for callers that ask for it.)
 _TARGET_WORKGROUPS_PER_CU = 2
 _MAX_SLOT_TOKENS = 8192
 
 
 def _auto_partitions(dev, batch_size, num_kv_heads, max_tokens, sliding_window, query_length):
+    return _auto_layout(dev, batch_size, num_kv_heads, max_tokens, sliding_window, query_length)[0]
+
+
+def _auto_layout(dev, batch_size, num_kv_heads, max_tokens, sliding_window, query_length):
+    """(partition slots, waves per slot) for the launcher's default."""
     cus = _device_cu_count(dev)
-    fill = _cdiv(cus * _TARGET_WORKGROUPS_PER_CU, max(1, batch_size * num_kv_heads))
+    pairs = max(1, batch_size * num_kv_heads)
     span = min(max_tokens, sliding_window + query_length) if sliding_window > 0 else max_tokens
     tiles = max(1, _cdiv(span, KV_COMPUTE_BLOCK) + (1 if sliding_window > 0 else 0))
-    return max(1, min(max(fill, _cdiv(span, _MAX_SLOT_TOKENS)), tiles))
+    least = _cdiv(span, _MAX_SLOT_TOKENS)
+    p8 = max(1, min(max(_cdiv(cus, pairs), least), tiles))
+    if pairs * p8 <= cus:
+        return p8, 8
+    fill = _cdiv(cus * _TARGET_WORKGROUPS_PER_CU, pairs)
+    return max(1, min(max(fill, least), tiles)), 4
+
+
+def _waves_per_slot(dev, batch_size, num_kv_heads, max_parts):
+    """Eight waves per slot when the grid fits one workgroup per CU, else four."""
+    return 8 if batch_size * num_kv_heads * max_parts <= _device_cu_count(dev) else 4
 
 
 _PLAN_CACHE: "OrderedDict[tuple, _Plan]" = OrderedDict()
@@ -361,6 +379,7 @@ def _partitioned_plan(
         softmax_scale=softmax_scale,
     )
     out_dtype = _get_output_dtype_str(output)
+    dargs.waves_per_slot = _waves_per_slot(dev, batch_size, num_kv_heads, max_parts)
     if direct:
         dargs.direct_output = 1
         dargs.out_dtype = {"bf16": _lib.PA_FP8_BF16, "f16": _lib.PA_FP8_F16, "f32": _lib.PA_FP8_F32}[out_dtype]

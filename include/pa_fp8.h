@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define PA_FP8_ABI_VERSION 2
+#define PA_FP8_ABI_VERSION 3
 
 enum pa_fp8_status {
     PA_FP8_OK = 0,
@@ -101,6 +101,10 @@ typedef struct pa_fp8_decode_args {
     int32_t out_dtype;
     void *output;
     int64_t stride_o_seq, stride_o_len, stride_o_head, stride_o_group;
+    /* waves per workgroup when ql * query_group_size <= 16 (the waves split a slot's
+     * steps): 0 = 4, or 1, 2, 4, 8.  Eight suits grids of at most one workgroup per CU. */
+    int32_t waves_per_slot;
+    int32_t reserved;
 } pa_fp8_decode_args;
 
 int pa_fp8_decode_partitions(const pa_fp8_decode_args *args, void *hip_stream);

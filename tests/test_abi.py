@@ -110,6 +110,7 @@ def _decode_args(lib, **over):
         ({"query_dtype": 2}, 6),
         ({"num_kv_heads": 0}, 5),
         ({"direct_output": 1}, 7),
+        ({"waves_per_slot": 3}, 5),
         ({"batch_size": 3}, 1),  # null pointers
     ],
 )

@@ -13,6 +13,12 @@ from flydsl_amd.pa_decode_swa import get_sw_max_context_partition_num
 from flydsl_amd.pa_metadata import get_pa_metadata_info_v1
 
 
+@pytest.fixture(autouse=True)
+def _mi355x_cus(monkeypatch):
+    """Plans are built on CPU tensors here; the launcher sizes grids for 256 CUs."""
+    monkeypatch.setattr(pdf, "_device_cu_count", lambda dev: 256)
+
+
 def make(batch=3, hq=8, hkv=2, bs=16, ql=1, nb=20, per_token=False, max_blocks=8):
     d = 128
     t = dict(
@@ -225,10 +231,17 @@ def test_auto_partition_policy(monkeypatch):
     assert pdf._auto_partitions(None, 64, 8, 4096, 0, 1) == 1
     # c3: sequences up to 32768 tokens -> slots of at most 8192 tokens
     assert pdf._auto_partitions(None, 128, 8, 32768, 0, 1) == 4
-    # c4: 32 x 8 pairs -> 2 slots to fill the GPU; never more slots than window tiles
-    assert pdf._auto_partitions(None, 32, 8, 32768, 4096, 1) == 2
+    assert pdf._auto_layout(None, 64, 8, 4096, 0, 1) == (1, 4)
+    # c4: 32 x 8 pairs = one per CU -> one 8-wave slot per pair, direct output
+    assert pdf._auto_layout(None, 32, 8, 32768, 4096, 1) == (1, 8)
+    # between one and two pairs per CU: two 4-wave slots
+    assert pdf._auto_layout(None, 48, 8, 4096, 0, 1) == (2, 4)
+    # few pairs: 8-wave slots up to one workgroup per CU, never more slots than tiles
+    assert pdf._auto_layout(None, 4, 8, 32768, 0, 1) == (8, 8)
     assert pdf._auto_partitions(None, 1, 1, 300, 0, 1) == 2
     assert pdf._auto_partitions(None, 1, 1, 100, 0, 1) == 1
+    # explicit slot counts: eight waves only while the grid fits one workgroup per CU
+    assert pdf._waves_per_slot(None, 32, 8, 1) == 8 and pdf._waves_per_slot(None, 32, 8, 2) == 4
 
 
 def test_recommended_splits_reference_formula(monkeypatch):
