@@ -13,8 +13,10 @@ from pathlib import Path
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("PA_FP8_LIB", str(_HERE / "libpa_fp8.so")))
 
-PA_FP8_ABI_VERSION = 3
+PA_FP8_ABI_VERSION = 4
 PA_FP8_BF16, PA_FP8_F16, PA_FP8_F32 = 0, 1, 2
+PA_FP8_CACHE_ELEM, PA_FP8_CACHE_FP8_TENSOR, PA_FP8_CACHE_FP8_TOKEN = 0, 1, 2
+PA_FP8_KV_FLASH, PA_FP8_KV_X_PACKED, PA_FP8_KV_X_TRANS = 0, 1, 2
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -198,12 +200,65 @@ class MetadataArgs(ctypes.Structure):
     ]
 
 
+class RopeCacheArgs(ctypes.Structure):
+    _fields_ = [
+        ("query", _vp),
+        ("key", _vp),
+        ("value", _vp),
+        ("positions", _vp),
+        ("cos_cache", _vp),
+        ("sin_cache", _vp),
+        ("slot_mapping", _vp),
+        ("key_cache", _vp),
+        ("value_cache", _vp),
+        ("query_out", _vp),
+        ("key_out", _vp),
+        ("key_scale", _vp),
+        ("value_scale", _vp),
+        ("stride_q_token", _i64),
+        ("stride_q_head", _i64),
+        ("stride_k_token", _i64),
+        ("stride_k_head", _i64),
+        ("stride_v_token", _i64),
+        ("stride_v_head", _i64),
+        ("stride_qo_token", _i64),
+        ("stride_qo_head", _i64),
+        ("stride_ko_token", _i64),
+        ("stride_ko_head", _i64),
+        ("stride_cos_pos", _i64),
+        ("stride_sin_pos", _i64),
+        ("stride_kc_block", _i64),
+        ("stride_kc_head", _i64),
+        ("stride_kc_token", _i64),
+        ("stride_vc_block", _i64),
+        ("stride_vc_head", _i64),
+        ("stride_vc_token", _i64),
+        ("stride_ks_block", _i64),
+        ("stride_ks_head", _i64),
+        ("num_tokens", _i32),
+        ("num_q_heads", _i32),
+        ("num_kv_heads", _i32),
+        ("head_dim", _i32),
+        ("block_size", _i32),
+        ("num_blocks", _i32),
+        ("max_pos", _i32),
+        ("elem_dtype", _i32),
+        ("cache_format", _i32),
+        ("kv_layout", _i32),
+        ("reuse_freqs_front_part", _i32),
+        ("positions_i64", _i32),
+        ("slots_i64", _i32),
+        ("reserved", _i32),
+    ]
+
+
 EXPORTED_SYMBOLS = (
     "pa_fp8_decode_partitions",
     "pa_fp8_lse_reduce",
     "pa_fp8_decode_worklist",
     "pa_fp8_reduce_v1",
     "pa_fp8_metadata_v1",
+    "pa_fp8_rope_cache",
     "pa_fp8_status_string",
     "pa_fp8_abi_version",
 )
@@ -239,6 +294,8 @@ def _load() -> ctypes.CDLL:
     lib.pa_fp8_reduce_v1.restype = ctypes.c_int
     lib.pa_fp8_metadata_v1.argtypes = [ctypes.POINTER(MetadataArgs), _vp]
     lib.pa_fp8_metadata_v1.restype = ctypes.c_int
+    lib.pa_fp8_rope_cache.argtypes = [ctypes.POINTER(RopeCacheArgs), _vp]
+    lib.pa_fp8_rope_cache.restype = ctypes.c_int
     lib.pa_fp8_status_string.argtypes = [ctypes.c_int]
     lib.pa_fp8_status_string.restype = ctypes.c_char_p
     return lib
@@ -270,3 +327,7 @@ def reduce_v1(args: ReduceV1Args, stream: int) -> None:
 
 def metadata_v1(args: MetadataArgs, stream: int) -> None:
     check("pa_fp8_metadata_v1", LIB.pa_fp8_metadata_v1(ctypes.byref(args), _vp(stream)))
+
+
+def rope_cache(args: RopeCacheArgs, stream: int) -> None:
+    check("pa_fp8_rope_cache", LIB.pa_fp8_rope_cache(ctypes.byref(args), _vp(stream)))

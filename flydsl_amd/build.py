@@ -16,7 +16,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 REPO = HERE.parent
 LIB_PATH = HERE / "libpa_fp8.so"
-SOURCES = [HERE / "csrc" / "pa_decode.hip", HERE / "csrc" / "pa_metadata.hip"]
+SOURCES = [HERE / "csrc" / "pa_decode.hip", HERE / "csrc" / "pa_metadata.hip", HERE / "csrc" / "rope_cache.hip"]
 HEADERS = [HERE / "csrc" / "pa_common.h", REPO / "include" / "pa_fp8.h"]
 OFFLOAD_ARCH = "gfx950"
 

@@ -1131,13 +1131,14 @@ const char *pa_fp8_status_string(int status) {
     switch (status) {
     case PA_FP8_OK: return "ok";
     case PA_FP8_ERR_NULL_POINTER: return "a required pointer is NULL";
-    case PA_FP8_ERR_HEAD_DIM: return "unsupported head_dim (only 128 is built)";
+    case PA_FP8_ERR_HEAD_DIM: return "unsupported head_dim (decode: 128; KV-cache writer: a multiple of 16 up to 1024)";
     case PA_FP8_ERR_BLOCK_SIZE: return "block_size must be a power of two >= 16";
     case PA_FP8_ERR_GROUP: return "query_length * query_group_size must be in 1..64";
     case PA_FP8_ERR_SHAPE: return "a size, stride or alignment is out of range";
     case PA_FP8_ERR_DTYPE: return "unsupported dtype";
     case PA_FP8_ERR_PARTITIONS: return "max_context_partition_num must be in 1..65535";
     case PA_FP8_ERR_WORKLIST: return "worklist buffers too small for the schedule";
+    case PA_FP8_ERR_LAYOUT: return "KV-cache layout or format not valid for these sizes";
     default: break;
     }
     if (status >= PA_FP8_ERR_HIP) return hipGetErrorString((hipError_t)(status - PA_FP8_ERR_HIP));

@@ -1,0 +1,437 @@
+// gfx950 fused NeoX rotary embedding + paged KV-cache writer (C ABI: pa_fp8_rope_cache).
+//
+// Work unit: one ROW = one (token, head) vector of Q or K.  A row is handled by
+// a power-of-two group of lanes (lanes_per_row = next_pow2(D/16)); lane c owns
+// head dims [8c, 8c+8) AND their rotation partners [D/2 + 8c, D/2 + 8c + 8), so
+// the NeoX pair (d, d + D/2) sits in one lane and no cross-lane exchange is
+// needed for the rotation (the reference gives each lane a contiguous slice and
+// fetches the partner with ds_bpermute, kernels/fused_rope_cache_kernel.py:150-177).
+// Every load and store of Q/K/V/outputs/cos/sin is one 16-byte vector access.
+// Rows of token t are laid out [Q heads..., K heads...] in the flat row index,
+// so consecutive lanes stream consecutive bytes of Q then K.  A K row also
+// reads V and writes the two cache entries of its token.
+//
+// Numerics follow the reference kernel (kernels/fused_rope_cache_kernel.py:214-247),
+// which computes in the element dtype: every product and the final sum are
+// rounded to bf16 / f16 (computed in f32 -- exact products of two 16-bit values --
+// then rounded to nearest even).  fp8 cache codes come from v_cvt_pk_fp8_f32
+// (round to nearest even; |x| > 464 -> NaN, as torch's float8_e4m3fn cast).
+// Per-tensor scales are applied as x * (1/scale) with the reciprocal computed
+// once per lane by IEEE division (the reference uses the approximate v_rcp_f32,
+// :282-283, which equals it at scales such as 0.1 and powers of two).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pa_common.h"
+#include "pa_fp8.h"
+
+namespace pa {
+namespace {
+
+constexpr int kRopeThreads = 256;
+
+struct RopeParams {
+    const uint16_t *q, *k, *v, *cos, *sin;
+    const int32_t *pos, *slot;
+    uint16_t *qo, *ko;
+    uint8_t *kc, *vc;
+    float *ks, *vs;
+    int64_t sq_t, sq_h, sk_t, sk_h, sv_t, sv_h, sqo_t, sqo_h, sko_t, sko_h, scos, ssin;
+    int64_t skc_b, skc_h, skc_t, svc_b, svc_h, svc_t, sks_b, sks_h;
+    int64_t rows;  // num_tokens * (num_q_heads + num_kv_heads)
+    int32_t QH, KH, D, bs, nb, max_pos;
+    int32_t pos_shift, slot_shift;  // 1: int64 index tensor, low word at element 2t
+    int32_t reuse, lpr_log2, chunks;
+};
+
+template <int ELEM>
+__device__ __forceinline__ float to_f(uint32_t bits16) {
+    if constexpr (ELEM == PA_FP8_BF16) return __uint_as_float(bits16 << 16);
+    else return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// float -> 16-bit pattern, round to nearest even (v_cvt_pk_bf16_f32 / v_cvt_f16_f32)
+template <int ELEM>
+__device__ __forceinline__ uint32_t from_f(float f) {
+    if constexpr (ELEM == PA_FP8_BF16) return __builtin_bit_cast(uint16_t, (__bf16)f);
+    else return f32_to_f16_bits(f);
+}
+
+template <int ELEM>
+__device__ __forceinline__ float rnd(float f) { return to_f<ELEM>(from_f<ELEM>(f)); }
+
+template <int ELEM>
+__device__ __forceinline__ void unpack8(uint4 w, float (&x)[8]) {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        x[2 * i] = to_f<ELEM>(u[i] & 0xffffu);
+        x[2 * i + 1] = to_f<ELEM>(u[i] >> 16);
+    }
+}
+
+template <int ELEM>
+__device__ __forceinline__ uint4 pack8(const float (&x)[8]) {
+    uint32_t u[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = from_f<ELEM>(x[2 * i]) | (from_f<ELEM>(x[2 * i + 1]) << 16);
+    return make_uint4(u[0], u[1], u[2], u[3]);
+}
+
+__device__ __forceinline__ uint4 ld16v(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+__device__ __forceinline__ void st16v(uint16_t *p, uint4 w) { *reinterpret_cast<uint4 *>(p) = w; }
+
+// Eight floats -> eight e4m3fn bytes (two dwords, element i in byte i).
+__device__ __forceinline__ uint2 fp8x8(const float (&x)[8]) {
+    int w0 = __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
+    w0 = __builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], w0, true);
+    int w1 = __builtin_amdgcn_cvt_pk_fp8_f32(x[4], x[5], 0, false);
+    w1 = __builtin_amdgcn_cvt_pk_fp8_f32(x[6], x[7], w1, true);
+    return make_uint2((uint32_t)w0, (uint32_t)w1);
+}
+
+// nan -> 0, +-inf -> +-448 (pertoken_quant's nan_to_num, tests/utils.py:29-73)
+__device__ __forceinline__ float clean448(float x) {
+    if (x != x) return 0.0f;
+    if (__builtin_isinf(x)) return x > 0.0f ? 448.0f : -448.0f;
+    return x;
+}
+
+// NeoX rotation of one lane's 8 (first-half) + 8 (second-half) elements, rounded
+// after each product and after the sum exactly as the element-dtype arithmetic.
+// Contraction is off so that no product is fused with the add that follows it
+// (v_fma_f16 / v_fma_mix would skip the product's rounding).  f16 computes in
+// native IEEE f16 ops; bf16 in f32 with an explicit round after each step.
+template <int ELEM>
+__device__ __forceinline__ void rotate(float (&x1)[8], float (&x2)[8], const float (&c1)[8], const float (&s1)[8],
+                                       const float (&c2)[8], const float (&s2)[8]) {
+#pragma clang fp contract(off)
+    if constexpr (ELEM == PA_FP8_F16) {
+        // native IEEE f16 products and sums (v_mul_f16 / v_sub_f16 / v_add_f16)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const _Float16 a = (_Float16)x1[i], b = (_Float16)x2[i];
+            const _Float16 p1 = a * (_Float16)c1[i], p2 = b * (_Float16)s1[i];
+            const _Float16 p3 = b * (_Float16)c2[i], p4 = a * (_Float16)s2[i];
+            x1[i] = (float)(_Float16)(p1 - p2);
+            x2[i] = (float)(_Float16)(p3 + p4);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float a = x1[i], b = x2[i];
+            x1[i] = rnd<ELEM>(rnd<ELEM>(a * c1[i]) - rnd<ELEM>(b * s1[i]));
+            x2[i] = rnd<ELEM>(rnd<ELEM>(b * c2[i]) + rnd<ELEM>(a * s2[i]));
+        }
+    }
+}
+
+// Writes one lane's 8 + 8 values of one token into a K (IS_V = false) or V cache.
+// Element offsets inside the (block, head) tile:
+//   flash      pos*stride_token + d
+//   x-packed K (d/16)*(bs*16) + pos*16 + d%16
+//   V 4-D      d*bs + pos
+//   V trans    (pos/16)*(D*16) + d*16 + pos%16
+template <int FMT, int LAYOUT, bool IS_V, int ELEM>
+__device__ __forceinline__ void write_cache(uint8_t *tile, int64_t stride_token, int pos, int bs, int D, int d1,
+                                            int d2, const float (&x1)[8], const float (&x2)[8]) {
+    constexpr int esz = FMT == PA_FP8_CACHE_ELEM ? 2 : 1;
+    const bool contiguous8 = LAYOUT == PA_FP8_KV_FLASH || !IS_V;
+    if (contiguous8) {
+        int64_t o1, o2;
+        if (LAYOUT == PA_FP8_KV_FLASH) {
+            o1 = int64_t(pos) * stride_token + d1;
+            o2 = int64_t(pos) * stride_token + d2;
+        } else {
+            o1 = int64_t(d1 >> 4) * (bs * 16) + pos * 16 + (d1 & 15);
+            o2 = int64_t(d2 >> 4) * (bs * 16) + pos * 16 + (d2 & 15);
+        }
+        if constexpr (FMT == PA_FP8_CACHE_ELEM) {
+            st16v(reinterpret_cast<uint16_t *>(tile + o1 * esz), pack8<ELEM>(x1));
+            st16v(reinterpret_cast<uint16_t *>(tile + o2 * esz), pack8<ELEM>(x2));
+        } else {
+            *reinterpret_cast<uint2 *>(tile + o1) = fp8x8(x1);
+            *reinterpret_cast<uint2 *>(tile + o2) = fp8x8(x2);
+        }
+        return;
+    }
+    // V, dim-major layouts: one element per head dim, strided
+    int64_t base, step;
+    if (LAYOUT == PA_FP8_KV_X_PACKED) {
+        base = pos;
+        step = bs;
+    } else {
+        base = int64_t(pos >> 4) * (int64_t(D) * 16) + (pos & 15);
+        step = 16;
+    }
+    if constexpr (FMT == PA_FP8_CACHE_ELEM) {
+        uint16_t *t16 = reinterpret_cast<uint16_t *>(tile);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            t16[base + int64_t(d1 + i) * step] = (uint16_t)from_f<ELEM>(x1[i]);
+            t16[base + int64_t(d2 + i) * step] = (uint16_t)from_f<ELEM>(x2[i]);
+        }
+    } else {
+        const uint2 b1 = fp8x8(x1), b2 = fp8x8(x2);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t w1 = i < 4 ? b1.x : b1.y, w2 = i < 4 ? b2.x : b2.y;
+            tile[base + int64_t(d1 + i) * step] = (uint8_t)(w1 >> (8 * (i & 3)));
+            tile[base + int64_t(d2 + i) * step] = (uint8_t)(w2 >> (8 * (i & 3)));
+        }
+    }
+}
+
+template <int ELEM, int FMT, int LAYOUT>
+__global__ __launch_bounds__(kRopeThreads) void rope_cache_kernel(RopeParams p) {
+    const int64_t gid = int64_t(blockIdx.x) * kRopeThreads + threadIdx.x;
+    const int64_t row = gid >> p.lpr_log2;
+    const int c = int(gid & ((1 << p.lpr_log2) - 1));
+    const int heads = p.QH + p.KH;
+    const bool live = row < p.rows && c < p.chunks;
+    const int half = p.D >> 1;
+    const int d1 = 8 * c, d2 = half + 8 * c;
+
+    int t = 0, h = 0;
+    bool is_k = false;
+    if (row < p.rows) {
+        t = int(row / heads);
+        const int hh = int(row - int64_t(t) * heads);
+        is_k = hh >= p.QH;
+        h = is_k ? hh - p.QH : hh;
+    }
+
+    float x1[8], x2[8], v1[8], v2[8];
+    int slot = -1;
+    if (live) {
+        const int pos = min(max(p.pos[int64_t(t) << p.pos_shift], 0), p.max_pos - 1);
+        const uint16_t *crow = p.cos + int64_t(pos) * p.scos;
+        const uint16_t *srow = p.sin + int64_t(pos) * p.ssin;
+        const uint16_t *x = is_k ? p.k + int64_t(t) * p.sk_t + int64_t(h) * p.sk_h
+                                 : p.q + int64_t(t) * p.sq_t + int64_t(h) * p.sq_h;
+        const uint4 wx1 = ld16v(x + d1), wx2 = ld16v(x + d2);
+        const uint4 wc1 = ld16v(crow + d1), ws1 = ld16v(srow + d1);
+        float c1[8], s1[8], c2[8], s2[8];
+        unpack8<ELEM>(wc1, c1);
+        unpack8<ELEM>(ws1, s1);
+        if (p.reuse) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                c2[i] = c1[i];
+                s2[i] = s1[i];
+            }
+        } else {
+            unpack8<ELEM>(ld16v(crow + d2), c2);
+            unpack8<ELEM>(ld16v(srow + d2), s2);
+        }
+        unpack8<ELEM>(wx1, x1);
+        unpack8<ELEM>(wx2, x2);
+        rotate<ELEM>(x1, x2, c1, s1, c2, s2);
+        uint16_t *out = is_k ? p.ko + int64_t(t) * p.sko_t + int64_t(h) * p.sko_h
+                             : p.qo + int64_t(t) * p.sqo_t + int64_t(h) * p.sqo_h;
+        st16v(out + d1, pack8<ELEM>(x1));
+        st16v(out + d2, pack8<ELEM>(x2));
+        if (is_k) {
+            slot = p.slot[int64_t(t) << p.slot_shift];
+            if (slot >= 0 && slot / p.bs < p.nb) {
+                const uint16_t *vr = p.v + int64_t(t) * p.sv_t + int64_t(h) * p.sv_h;
+                unpack8<ELEM>(ld16v(vr + d1), v1);
+                unpack8<ELEM>(ld16v(vr + d2), v2);
+            } else {
+                slot = -1;
+            }
+        }
+    }
+    const bool write = live && is_k && slot >= 0;
+    const int blk = write ? slot / p.bs : 0;
+    const int bpos = write ? slot - blk * p.bs : 0;
+
+    if constexpr (FMT == PA_FP8_CACHE_FP8_TENSOR) {
+        if (write) {
+            const float rk = 1.0f / p.ks[0];
+            const float rv = 1.0f / p.vs[0];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                x1[i] *= rk;
+                x2[i] *= rk;
+                v1[i] *= rv;
+                v2[i] *= rv;
+            }
+        }
+    } else if constexpr (FMT == PA_FP8_CACHE_FP8_TOKEN) {
+        // amax over the row: every lane of the wave takes part in the exchange
+        // (lanes without a cache write contribute 0); a row's lanes form an
+        // aligned power-of-two group, so the xor butterfly stays inside it.
+        float ak = 0.0f, av = 0.0f;
+        if (write) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                x1[i] = clean448(x1[i]);
+                x2[i] = clean448(x2[i]);
+                v1[i] = clean448(v1[i]);
+                v2[i] = clean448(v2[i]);
+                ak = fmaxf(ak, fmaxf(fabsf(x1[i]), fabsf(x2[i])));
+                av = fmaxf(av, fmaxf(fabsf(v1[i]), fabsf(v2[i])));
+            }
+        }
+        for (int m = (1 << p.lpr_log2) >> 1; m >= 1; m >>= 1) {
+            ak = fmaxf(ak, __shfl_xor(ak, m, 64));
+            av = fmaxf(av, __shfl_xor(av, m, 64));
+        }
+        if (write) {
+            float sk = ak / 448.0f, sv = av / 448.0f;
+            if (sk == 0.0f) sk = 1.0f;
+            if (sv == 0.0f) sv = 1.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                x1[i] = x1[i] / sk;
+                x2[i] = x2[i] / sk;
+                v1[i] = v1[i] / sv;
+                v2[i] = v2[i] / sv;
+            }
+            if (c == 0) {
+                const int64_t so = int64_t(blk) * p.sks_b + int64_t(h) * p.sks_h + bpos;
+                p.ks[so] = sk;
+                p.vs[so] = sv;
+            }
+        }
+    }
+    if (write) {
+        constexpr int esz = FMT == PA_FP8_CACHE_ELEM ? 2 : 1;
+        uint8_t *kt = p.kc + (int64_t(blk) * p.skc_b + int64_t(h) * p.skc_h) * esz;
+        uint8_t *vt = p.vc + (int64_t(blk) * p.svc_b + int64_t(h) * p.svc_h) * esz;
+        write_cache<FMT, LAYOUT, false, ELEM>(kt, p.skc_t, bpos, p.bs, p.D, d1, d2, x1, x2);
+        write_cache<FMT, LAYOUT, true, ELEM>(vt, p.svc_t, bpos, p.bs, p.D, d1, d2, v1, v2);
+    }
+}
+
+template <int ELEM, int FMT>
+hipError_t launch_layout(const RopeParams &p, int layout, dim3 grid, hipStream_t s) {
+    switch (layout) {
+    case PA_FP8_KV_FLASH:
+        hipLaunchKernelGGL((rope_cache_kernel<ELEM, FMT, PA_FP8_KV_FLASH>), grid, dim3(kRopeThreads), 0, s, p);
+        break;
+    case PA_FP8_KV_X_PACKED:
+        hipLaunchKernelGGL((rope_cache_kernel<ELEM, FMT, PA_FP8_KV_X_PACKED>), grid, dim3(kRopeThreads), 0, s, p);
+        break;
+    default:
+        hipLaunchKernelGGL((rope_cache_kernel<ELEM, FMT, PA_FP8_KV_X_TRANS>), grid, dim3(kRopeThreads), 0, s, p);
+        break;
+    }
+    return hipGetLastError();
+}
+
+template <int ELEM>
+hipError_t launch_format(const RopeParams &p, int fmt, int layout, dim3 grid, hipStream_t s) {
+    switch (fmt) {
+    case PA_FP8_CACHE_ELEM: return launch_layout<ELEM, PA_FP8_CACHE_ELEM>(p, layout, grid, s);
+    case PA_FP8_CACHE_FP8_TENSOR: return launch_layout<ELEM, PA_FP8_CACHE_FP8_TENSOR>(p, layout, grid, s);
+    default: return launch_layout<ELEM, PA_FP8_CACHE_FP8_TOKEN>(p, layout, grid, s);
+    }
+}
+
+inline bool aligned(const void *ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; }
+
+}  // namespace
+}  // namespace pa
+
+extern "C" int pa_fp8_rope_cache(const pa_fp8_rope_cache_args *a, void *hip_stream) {
+    using namespace pa;
+    if (!a) return PA_FP8_ERR_NULL_POINTER;
+    // per-token tensors may be empty (NULL) when there are no tokens
+    if (a->num_tokens != 0 && (!a->query || !a->key || !a->value || !a->positions || !a->slot_mapping ||
+                               !a->query_out || !a->key_out))
+        return PA_FP8_ERR_NULL_POINTER;
+    if (!a->cos_cache || !a->sin_cache || !a->key_cache || !a->value_cache) return PA_FP8_ERR_NULL_POINTER;
+    if (a->elem_dtype != PA_FP8_BF16 && a->elem_dtype != PA_FP8_F16) return PA_FP8_ERR_DTYPE;
+    if (a->cache_format < PA_FP8_CACHE_ELEM || a->cache_format > PA_FP8_CACHE_FP8_TOKEN) return PA_FP8_ERR_LAYOUT;
+    if (a->kv_layout < PA_FP8_KV_FLASH || a->kv_layout > PA_FP8_KV_X_TRANS) return PA_FP8_ERR_LAYOUT;
+    if (a->cache_format != PA_FP8_CACHE_ELEM && (!a->key_scale || !a->value_scale)) return PA_FP8_ERR_NULL_POINTER;
+    const int D = a->head_dim;
+    if (D < 16 || D > 1024 || D % 16 != 0) return PA_FP8_ERR_HEAD_DIM;
+    if (a->num_tokens < 0 || a->num_q_heads < 1 || a->num_kv_heads < 1 || a->block_size < 1 || a->num_blocks < 1 ||
+        a->max_pos < 1)
+        return PA_FP8_ERR_SHAPE;
+    if (int64_t(a->num_q_heads) + a->num_kv_heads > (1 << 20)) return PA_FP8_ERR_SHAPE;
+    if (a->kv_layout == PA_FP8_KV_X_TRANS && a->block_size % 16 != 0) return PA_FP8_ERR_LAYOUT;
+    // 16-byte vector rows for every 16-bit tensor
+    const void *p16[] = {a->query, a->key, a->value, a->cos_cache, a->sin_cache, a->query_out, a->key_out};
+    for (const void *ptr : p16)
+        if (!aligned(ptr, 16)) return PA_FP8_ERR_SHAPE;
+    const int64_t s16[] = {a->stride_q_token,  a->stride_q_head,  a->stride_k_token,  a->stride_k_head,
+                           a->stride_v_token,  a->stride_v_head,  a->stride_qo_token, a->stride_qo_head,
+                           a->stride_ko_token, a->stride_ko_head, a->stride_cos_pos,  a->stride_sin_pos};
+    for (int64_t s : s16)
+        if (s < 0 || s % 8 != 0) return PA_FP8_ERR_SHAPE;
+    // caches: 16-byte (16-bit cache) or 8-byte (fp8) runs of 8 head dims
+    const uintptr_t ca = a->cache_format == PA_FP8_CACHE_ELEM ? 16 : 8;
+    if (!aligned(a->key_cache, ca) || !aligned(a->value_cache, ca)) return PA_FP8_ERR_SHAPE;
+    const int64_t sc[] = {a->stride_kc_block, a->stride_kc_head, a->stride_vc_block, a->stride_vc_head};
+    for (int64_t s : sc)
+        if (s < 0 || s % 8 != 0) return PA_FP8_ERR_SHAPE;
+    if (a->kv_layout == PA_FP8_KV_FLASH && (a->stride_kc_token < 0 || a->stride_kc_token % 8 != 0 ||
+                                            a->stride_vc_token < 0 || a->stride_vc_token % 8 != 0))
+        return PA_FP8_ERR_SHAPE;
+    if (a->cache_format == PA_FP8_CACHE_FP8_TOKEN && (a->stride_ks_block < 0 || a->stride_ks_head < 0))
+        return PA_FP8_ERR_SHAPE;
+    if (a->num_tokens == 0) return PA_FP8_OK;
+
+    const int chunks = D / 16;
+    int lpr_log2 = 0;
+    while ((1 << lpr_log2) < chunks) ++lpr_log2;
+    RopeParams p;
+    p.q = static_cast<const uint16_t *>(a->query);
+    p.k = static_cast<const uint16_t *>(a->key);
+    p.v = static_cast<const uint16_t *>(a->value);
+    p.cos = static_cast<const uint16_t *>(a->cos_cache);
+    p.sin = static_cast<const uint16_t *>(a->sin_cache);
+    p.pos = static_cast<const int32_t *>(a->positions);
+    p.slot = static_cast<const int32_t *>(a->slot_mapping);
+    p.qo = static_cast<uint16_t *>(a->query_out);
+    p.ko = static_cast<uint16_t *>(a->key_out);
+    p.kc = static_cast<uint8_t *>(a->key_cache);
+    p.vc = static_cast<uint8_t *>(a->value_cache);
+    p.ks = a->key_scale;
+    p.vs = a->value_scale;
+    p.sq_t = a->stride_q_token;
+    p.sq_h = a->stride_q_head;
+    p.sk_t = a->stride_k_token;
+    p.sk_h = a->stride_k_head;
+    p.sv_t = a->stride_v_token;
+    p.sv_h = a->stride_v_head;
+    p.sqo_t = a->stride_qo_token;
+    p.sqo_h = a->stride_qo_head;
+    p.sko_t = a->stride_ko_token;
+    p.sko_h = a->stride_ko_head;
+    p.scos = a->stride_cos_pos;
+    p.ssin = a->stride_sin_pos;
+    p.skc_b = a->stride_kc_block;
+    p.skc_h = a->stride_kc_head;
+    p.skc_t = a->stride_kc_token;
+    p.svc_b = a->stride_vc_block;
+    p.svc_h = a->stride_vc_head;
+    p.svc_t = a->stride_vc_token;
+    p.sks_b = a->stride_ks_block;
+    p.sks_h = a->stride_ks_head;
+    p.rows = int64_t(a->num_tokens) * (a->num_q_heads + a->num_kv_heads);
+    p.QH = a->num_q_heads;
+    p.KH = a->num_kv_heads;
+    p.D = D;
+    p.bs = a->block_size;
+    p.nb = a->num_blocks;
+    p.max_pos = a->max_pos;
+    p.pos_shift = a->positions_i64 ? 1 : 0;
+    p.slot_shift = a->slots_i64 ? 1 : 0;
+    p.reuse = a->reuse_freqs_front_part ? 1 : 0;
+    p.lpr_log2 = lpr_log2;
+    p.chunks = chunks;
+    const int64_t threads = p.rows << lpr_log2;
+    const int64_t blocks = (threads + kRopeThreads - 1) / kRopeThreads;
+    if (blocks > 0x7fffffffLL) return PA_FP8_ERR_SHAPE;
+    const dim3 grid((unsigned)blocks);
+    hipStream_t s = static_cast<hipStream_t>(hip_stream);
+    const hipError_t e = a->elem_dtype == PA_FP8_BF16
+                             ? launch_format<PA_FP8_BF16>(p, a->cache_format, a->kv_layout, grid, s)
+                             : launch_format<PA_FP8_F16>(p, a->cache_format, a->kv_layout, grid, s);
+    return e == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + int(e);
+}

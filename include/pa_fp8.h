@@ -22,18 +22,19 @@
 extern "C" {
 #endif
 
-#define PA_FP8_ABI_VERSION 3
+#define PA_FP8_ABI_VERSION 4
 
 enum pa_fp8_status {
     PA_FP8_OK = 0,
     PA_FP8_ERR_NULL_POINTER = 1,     /* a required pointer is NULL            */
-    PA_FP8_ERR_HEAD_DIM = 2,         /* head_dim other than 128               */
+    PA_FP8_ERR_HEAD_DIM = 2,         /* head_dim unsupported by the entry     */
     PA_FP8_ERR_BLOCK_SIZE = 3,       /* block_size not a power of two >= 16   */
     PA_FP8_ERR_GROUP = 4,            /* query_length * group_size not in 1..64 */
     PA_FP8_ERR_SHAPE = 5,            /* a size or stride out of range         */
     PA_FP8_ERR_DTYPE = 6,            /* unsupported query / output dtype      */
     PA_FP8_ERR_PARTITIONS = 7,       /* max_context_partition_num out of range */
     PA_FP8_ERR_WORKLIST = 8,         /* metadata buffer too small             */
+    PA_FP8_ERR_LAYOUT = 9,           /* cache layout / format not valid here  */
     PA_FP8_ERR_HIP = 1000            /* 1000 + hipError_t of a failed launch  */
 };
 
@@ -269,6 +270,88 @@ typedef struct pa_fp8_metadata_args {
 } pa_fp8_metadata_args;
 
 int pa_fp8_metadata_v1(const pa_fp8_metadata_args *args, void *hip_stream);
+
+/* KV-cache formats written by pa_fp8_rope_cache */
+enum pa_fp8_cache_format {
+    PA_FP8_CACHE_ELEM = 0,       /* cache of the element dtype (bf16 / f16), written unscaled   */
+    PA_FP8_CACHE_FP8_TENSOR = 1, /* fp8 e4m3fn, code = e4m3(x * (1 / scale[0])), scale read     */
+    PA_FP8_CACHE_FP8_TOKEN = 2   /* fp8 e4m3fn, scale = amax/448 per (token, kv head) written,
+                                    code = e4m3(x / scale)                                     */
+};
+
+/* KV-cache layouts written by pa_fp8_rope_cache */
+enum pa_fp8_kv_layout {
+    PA_FP8_KV_FLASH = 0,    /* K, V [nb, bs, Hkv, D]                                */
+    PA_FP8_KV_X_PACKED = 1, /* K [nb, Hkv, D/16, bs, 16], V [nb, Hkv, D, bs]        */
+    PA_FP8_KV_X_TRANS = 2   /* K [nb, Hkv, D/16, bs, 16], V [nb, Hkv, bs/16, D, 16] */
+};
+
+/*
+ * Fused NeoX rotary embedding + paged KV-cache write, one launch:
+ *   query_out = rope(query), key_out = rope(key) for every token;
+ *   for tokens whose slot >= 0 (and slot / block_size < num_blocks): the cache
+ *   entry (slot / block_size, slot % block_size) of every kv head receives
+ *   rope(key) and value in cache_format / kv_layout.
+ * rope pairs head dim d with d + D/2 (NeoX, rotary_dim == D):
+ *   out[d]       = r(r(x[d] * c) - r(x[d + D/2] * s))
+ *   out[d + D/2] = r(r(x[d + D/2] * c') + r(x[d] * s'))
+ * with r = rounding to the element dtype, (c, s) = cos/sin[pos, d] and
+ * (c', s') = the same (reuse_freqs_front_part, cos/sin [max_pos, D/2]) or
+ * cos/sin[pos, d + D/2] (cos/sin [max_pos, D]).
+ * Positions and slots are int32, or int64 of which the low word is read;
+ * positions outside [0, max_pos) are clamped into it.
+ * query / key / value / outputs [T, H, D] with a free token and head stride
+ * (inner dim contiguous, 16-byte aligned rows); cos / sin [max_pos, cols]
+ * with a free row stride; caches contiguous inside a (block, head) tile with
+ * free block and head strides (and token stride for the flash layout).
+ * Per-token scales [nb, Hkv, bs, 1] f32: element blk*stride_ks_block +
+ * h*stride_ks_head + slot % block_size.
+ *
+ * Replaces the launcher of `build_fused_rope_cache_module`
+ * (kernels/fused_rope_cache_kernel.py:439-475, kernel :106-429).
+ * PA_FP8_KV_X_TRANS and PA_FP8_CACHE_FP8_TOKEN have no counterpart there:
+ * they write the V layout and the per-token scales pa_fp8_decode_* read.
+ */
+typedef struct pa_fp8_rope_cache_args {
+    const void *query;
+    const void *key;
+    const void *value;
+    const void *positions;
+    const void *cos_cache;
+    const void *sin_cache;
+    const void *slot_mapping;
+    void *key_cache;
+    void *value_cache;
+    void *query_out;
+    void *key_out;
+    float *key_scale;
+    float *value_scale;
+    int64_t stride_q_token, stride_q_head;
+    int64_t stride_k_token, stride_k_head;
+    int64_t stride_v_token, stride_v_head;
+    int64_t stride_qo_token, stride_qo_head;
+    int64_t stride_ko_token, stride_ko_head;
+    int64_t stride_cos_pos, stride_sin_pos;
+    int64_t stride_kc_block, stride_kc_head, stride_kc_token;
+    int64_t stride_vc_block, stride_vc_head, stride_vc_token;
+    int64_t stride_ks_block, stride_ks_head;
+    int32_t num_tokens;
+    int32_t num_q_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t block_size;
+    int32_t num_blocks;
+    int32_t max_pos;
+    int32_t elem_dtype;     /* PA_FP8_BF16 or PA_FP8_F16 (query, key, value, cos, sin, outputs) */
+    int32_t cache_format;   /* pa_fp8_cache_format */
+    int32_t kv_layout;      /* pa_fp8_kv_layout */
+    int32_t reuse_freqs_front_part;
+    int32_t positions_i64;
+    int32_t slots_i64;
+    int32_t reserved;
+} pa_fp8_rope_cache_args;
+
+int pa_fp8_rope_cache(const pa_fp8_rope_cache_args *args, void *hip_stream);
 
 /* Human-readable text of a status code (static storage). */
 const char *pa_fp8_status_string(int status);

@@ -38,7 +38,7 @@ def declared_functions():
 def test_header_declares_the_expected_api():
     assert declared_functions() == sorted(
         ["pa_fp8_decode_partitions", "pa_fp8_lse_reduce", "pa_fp8_decode_worklist", "pa_fp8_reduce_v1",
-         "pa_fp8_metadata_v1", "pa_fp8_status_string", "pa_fp8_abi_version"]
+         "pa_fp8_metadata_v1", "pa_fp8_rope_cache", "pa_fp8_status_string", "pa_fp8_abi_version"]
     )
 
 
@@ -62,6 +62,7 @@ STRUCTS = {
     "pa_fp8_worklist_args": "WorklistArgs",
     "pa_fp8_reduce_v1_args": "ReduceV1Args",
     "pa_fp8_metadata_args": "MetadataArgs",
+    "pa_fp8_rope_cache_args": "RopeCacheArgs",
 }
 
 
@@ -124,7 +125,8 @@ def test_null_args_and_status_strings(lib):
     assert lib.LIB.pa_fp8_metadata_v1(None, None) == 1
     assert lib.LIB.pa_fp8_decode_worklist(None, None) == 1
     assert lib.LIB.pa_fp8_reduce_v1(None, None) == 1
-    for code in range(0, 9):
+    assert lib.LIB.pa_fp8_rope_cache(None, None) == 1
+    for code in range(0, 10):
         assert lib.LIB.pa_fp8_status_string(code)
     with pytest.raises(lib.PaFp8Error, match="status 2"):
         lib.check("pa_fp8_decode_partitions", 2)
@@ -187,3 +189,47 @@ def test_reduce_v1_validation(lib):
     assert lib.LIB.pa_fp8_reduce_v1(ctypes.byref(r), None) == 1  # null buffers
     r.max_qlen = 0
     assert lib.LIB.pa_fp8_reduce_v1(ctypes.byref(r), None) == 5
+
+
+def _rope_args(lib, **over):
+    """Zero tokens and fake (never dereferenced) 16-byte aligned pointers: validation only."""
+    a = lib.RopeCacheArgs()
+    for i, name in enumerate(["query", "key", "value", "positions", "cos_cache", "sin_cache", "slot_mapping",
+                              "key_cache", "value_cache", "query_out", "key_out", "key_scale", "value_scale"]):
+        setattr(a, name, 0x10000 + 0x100 * i)
+    a.num_tokens, a.num_q_heads, a.num_kv_heads, a.head_dim = 0, 8, 1, 128
+    a.block_size, a.num_blocks, a.max_pos = 16, 4, 64
+    a.stride_q_token, a.stride_q_head = 8 * 128, 128
+    a.stride_kc_block, a.stride_kc_head, a.stride_vc_block, a.stride_vc_head = 2048, 2048, 2048, 2048
+    a.elem_dtype, a.cache_format, a.kv_layout = lib.PA_FP8_BF16, lib.PA_FP8_CACHE_FP8_TOKEN, lib.PA_FP8_KV_X_TRANS
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "over,status",
+    [
+        ({}, 0),  # no tokens: nothing to launch
+        ({"head_dim": 72}, 2),
+        ({"head_dim": 2048}, 2),
+        ({"elem_dtype": 2}, 6),
+        ({"cache_format": 3}, 9),
+        ({"kv_layout": 3}, 9),
+        ({"block_size": 8}, 9),  # trans_v V needs block_size % 16 == 0
+        ({"block_size": 8, "kv_layout": 1}, 0),  # 4-D V takes any block size
+        ({"num_tokens": -1}, 5),
+        ({"num_kv_heads": 0}, 5),
+        ({"max_pos": 0}, 5),
+        ({"query": 0x10008}, 5),  # 16-bit rows must be 16-byte aligned
+        ({"stride_q_head": 100}, 5),
+        ({"key_cache": 0x10004}, 5),  # fp8 runs of 8 head dims: 8-byte aligned
+        ({"key_scale": 0}, 1),
+        ({"key_scale": 0, "cache_format": 0, "key_cache": 0x10000, "value_cache": 0x10000}, 0),
+        ({"slot_mapping": 0}, 0),  # empty per-token tensors are fine without tokens
+        ({"slot_mapping": 0, "num_tokens": 1}, 1),
+        ({"cos_cache": 0}, 1),
+    ],
+)
+def test_rope_cache_validation_codes(lib, over, status):
+    assert lib.LIB.pa_fp8_rope_cache(ctypes.byref(_rope_args(lib, **over)), None) == status

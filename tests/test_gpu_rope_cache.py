@@ -1,0 +1,403 @@
+"""GPU parity of the fused RoPE + KV-cache writer (pa_fp8_rope_cache) against oracle/rope_cache.py.
+
+Cases mirror the reference test's categories (tests/kernels/test_fused_rope_cache.py:502-760:
+decode T=1, flash bf16 over the model shapes, non-flash, f16, i32/i64 positions,
+half/full cos-sin tables, negative slots, fp8 cache) plus this build's trans_v
+V layout, per-token fp8 scales, strided Q/K/V views, clamped positions,
+out-of-cache slots, large prefill batches and a write-then-decode round trip.
+
+The bar is bit-exact: Q_out, K_out, every cache byte and every written scale
+equal the oracle's (same rounding after each element-dtype product and sum,
+same fp8 encoding).  The reference test's own tolerances are checked too.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import quant as oq
+from oracle import rope_cache as orc
+from oracle.fp8 import e4m3_decode
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+MAX_POS = 8192
+TORCH_DT = {"bf16": torch.bfloat16, "f16": torch.float16}
+FP8 = torch.float8_e4m3fn
+
+MODELS = [
+    ("Llama8B-TP1", 32, 8, 128),
+    ("Llama8B-TP8", 4, 1, 128),
+    ("Llama70B-TP1", 64, 8, 128),
+    ("Llama70B-TP8", 8, 1, 128),
+    ("Llama405B-TP1", 128, 8, 128),
+    ("Llama405B-TP8", 16, 1, 128),
+    ("Qwen72B-TP1", 64, 4, 128),
+    ("GPTOSS-TP1", 64, 8, 64),
+    ("GPTOSS-TP8", 8, 1, 64),
+]
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.float().cpu().numpy()
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.uint8 if t.element_size() == 1 else torch.int16).cpu().numpy().view(
+        np.uint8 if t.element_size() == 1 else np.uint16
+    )
+
+
+def _cache_shapes(layout, nb, bs, KH, D):
+    if layout == "flash":
+        return (nb, bs, KH, D), (nb, bs, KH, D)
+    k = (nb, KH, D // 16, bs, 16)
+    return k, ((nb, KH, D, bs) if layout == "x4" else (nb, KH, bs // 16, D, 16))
+
+
+def run_case(
+    T, D, QH, KH, layout="flash", elem="bf16", fmt="elem", reuse=True, pos_dtype="i32", negative_slots=False,
+    bs=16, num_blocks=None, slots=None, positions=None, fused_qkv=False, scale=(0.1, 0.1), seed=42, max_pos=MAX_POS,
+    value_scale=1.0,
+):
+    """Launch the writer and compare every output with the oracle; returns the tensors."""
+    from flydsl_amd.fused_rope_cache import build_fused_rope_cache_module
+
+    dt = TORCH_DT[elem]
+    g = torch.Generator().manual_seed(seed)
+    nb = num_blocks or max(32, (T + bs - 1) // bs + 4)
+    cols = D // 2 if reuse else D
+    if fused_qkv:  # Q, K, V as strided views of one [T, (QH + 2KH) * D] projection output
+        qkv = torch.randn(T, (QH + 2 * KH) * D, generator=g).to(dt).to(DEV)
+        q = qkv[:, : QH * D].view(T, QH, D)
+        k = qkv[:, QH * D : (QH + KH) * D].view(T, KH, D)
+        v = qkv[:, (QH + KH) * D :].view(T, KH, D)
+    else:
+        q = torch.randn(T, QH, D, generator=g).to(dt).to(DEV)
+        k = torch.randn(T, KH, D, generator=g).to(dt).to(DEV)
+        v = (torch.randn(T, KH, D, generator=g) * value_scale).to(dt).to(DEV)
+    cos = torch.randn(max_pos, cols, generator=g).to(dt).to(DEV)
+    sin = torch.randn(max_pos, cols, generator=g).to(dt).to(DEV)
+    if positions is None:
+        positions = torch.randint(0, max_pos, (T,), generator=g, dtype=torch.int32)
+    positions = torch.as_tensor(positions, dtype=torch.int32)
+    if slots is None:
+        slots = torch.arange(T, dtype=torch.int32)
+        if negative_slots:
+            slots[1::2] = -1
+    slots = torch.as_tensor(slots, dtype=torch.int32)
+    idx_dt = torch.int64 if pos_dtype == "i64" else torch.int32
+    pos_t, slot_t = positions.to(idx_dt).to(DEV), slots.to(idx_dt).to(DEV)
+
+    kshape, vshape = _cache_shapes(layout, nb, bs, KH, D)
+    cache_dt = dt if fmt == "elem" else FP8
+    kc = torch.zeros(kshape, dtype=cache_dt, device=DEV)
+    vc = torch.zeros(vshape, dtype=cache_dt, device=DEV)
+    if fmt == "fp8_token":
+        ks = torch.zeros(nb, KH, bs, 1, dtype=torch.float32, device=DEV)
+        vs = torch.zeros(nb, KH, bs, 1, dtype=torch.float32, device=DEV)
+    else:
+        ks = torch.tensor([scale[0]], dtype=torch.float32, device=DEV)
+        vs = torch.tensor([scale[1]], dtype=torch.float32, device=DEV)
+    q_out = torch.empty(T, QH, D, dtype=dt, device=DEV)
+    k_out = torch.empty(T, KH, D, dtype=dt, device=DEV)
+
+    launch = build_fused_rope_cache_module(
+        head_dim=D, num_q_heads=QH, num_kv_heads=KH, block_size=bs, flash_layout=layout == "flash", dtype_str=elem,
+        apply_scale=fmt != "elem", reuse_freqs_front_part=reuse, pos_dtype=pos_dtype,
+    )
+    print(f"rope_cache case T={T} D={D} QH={QH} KH={KH} layout={layout} elem={elem} fmt={fmt} reuse={reuse} "
+          f"pos={pos_dtype} bs={bs} nb={nb}", flush=True)
+    launch(q, k, v, pos_t, cos, sin, slot_t, kc, vc, q_out, k_out, T, ks, vs, stream=torch.cuda.current_stream())
+    torch.cuda.synchronize()
+
+    # oracle on the same inputs
+    okc, ovc = orc.new_caches(nb, bs, KH, D, layout, fmt != "elem")
+    oks = ovs = None
+    if fmt == "fp8_tensor":
+        oks, ovs = np.float32(scale[0]), np.float32(scale[1])
+    elif fmt == "fp8_token":
+        oks, ovs = np.zeros((nb, KH, bs, 1), np.float32), np.zeros((nb, KH, bs, 1), np.float32)
+    pos_np = orc.low_word(pos_t.cpu().numpy())
+    slot_np = orc.low_word(slot_t.cpu().numpy())
+    oq_out, ok_out = orc.fused_rope_cache(
+        _np(q), _np(k), _np(v), pos_np, _np(cos), _np(sin), slot_np, okc, ovc, elem=elem, layout=layout,
+        block_size=bs, fmt=fmt, k_scale=oks, v_scale=ovs,
+    )
+    np.testing.assert_array_equal(_bits(q_out), orc.elem_bits(oq_out, elem), err_msg="Q_out")
+    np.testing.assert_array_equal(_bits(k_out), orc.elem_bits(ok_out, elem), err_msg="K_out")
+    np.testing.assert_array_equal(_bits(kc), okc, err_msg="key cache")
+    np.testing.assert_array_equal(_bits(vc), ovc, err_msg="value cache")
+    if fmt == "fp8_token":
+        np.testing.assert_array_equal(ks.cpu().numpy(), oks, err_msg="key scales")
+        np.testing.assert_array_equal(vs.cpu().numpy(), ovs, err_msg="value scales")
+    return dict(q=q, k=k, v=v, cos=cos, sin=sin, pos=positions, slots=slots, kc=kc, vc=vc, ks=ks, vs=vs,
+                q_out=q_out, k_out=k_out, nb=nb, bs=bs, layout=layout, fmt=fmt, elem=elem)
+
+
+def _reference_tolerances(r, atol):
+    """The reference test's acceptance check (tests/kernels/test_fused_rope_cache.py:354-391)."""
+    D = r["q"].shape[-1]
+    dt = r["q"].dtype
+    pos = r["pos"].long().to(DEV)
+    cos = r["cos"][pos].unsqueeze(1)
+    sin = r["sin"][pos].unsqueeze(1)
+    if cos.shape[-1] == D // 2:
+        cos, sin = torch.cat([cos, cos], -1), torch.cat([sin, sin], -1)
+
+    def rot(x):
+        x1, x2 = x[..., : D // 2], x[..., D // 2 :]
+        return torch.cat([x1 * cos[..., : D // 2] - x2 * sin[..., : D // 2],
+                          x2 * cos[..., D // 2 :] + x1 * sin[..., D // 2 :]], -1).to(dt)
+
+    assert (r["q_out"].float() - rot(r["q"]).float()).abs().max().item() < atol
+    assert (r["k_out"].float() - rot(r["k"]).float()).abs().max().item() < atol
+
+
+# ---- reference categories -------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("name,QH,KH,D", MODELS, ids=[m[0] for m in MODELS])
+def test_decode_flash(name, QH, KH, D):
+    r = run_case(1, D, QH, KH)
+    _reference_tolerances(r, 1e-2)
+
+
+@pytest.mark.parametrize("T", [32, 128])
+@pytest.mark.parametrize("name,QH,KH,D", MODELS, ids=[m[0] for m in MODELS])
+def test_flash_bf16(T, name, QH, KH, D):
+    run_case(T, D, QH, KH)
+
+
+@pytest.mark.parametrize("layout", ["x4", "x5"])
+@pytest.mark.parametrize("T", [1, 32, 128])
+@pytest.mark.parametrize("name,QH,KH,D", [MODELS[0], MODELS[1], MODELS[3], MODELS[8]],
+                         ids=["Llama8B-TP1", "Llama8B-TP8", "Llama70B-TP8", "GPTOSS-TP8"])
+def test_nonflash_bf16(layout, T, name, QH, KH, D):
+    run_case(T, D, QH, KH, layout=layout)
+
+
+@pytest.mark.parametrize("layout", ["flash", "x4", "x5"])
+@pytest.mark.parametrize("T", [1, 32])
+def test_f16(layout, T):
+    r = run_case(T, 128, 4, 1, layout=layout, elem="f16")
+    _reference_tolerances(r, 5e-3)
+
+
+@pytest.mark.parametrize("pos_dtype", ["i32", "i64"])
+@pytest.mark.parametrize("T", [1, 32, 128])
+def test_pos_dtype(pos_dtype, T):
+    run_case(T, 128, 8, 1, pos_dtype=pos_dtype)
+
+
+def test_i64_reads_the_low_word():
+    # int64 indices above 2**32 alias their low word, as the reference's stride-2 int32 view does
+    T = 8
+    pos = torch.arange(T, dtype=torch.int64) * 3 + (1 << 32)
+    slots = torch.arange(T, dtype=torch.int64) + (5 << 32)
+    from flydsl_amd.fused_rope_cache import build_fused_rope_cache_module
+
+    r = run_case(T, 128, 8, 1, pos_dtype="i64")  # values in range: same as int32
+    launch = build_fused_rope_cache_module(head_dim=128, num_q_heads=8, num_kv_heads=1, pos_dtype="i64")
+    kc = torch.zeros_like(r["kc"])
+    vc = torch.zeros_like(r["vc"])
+    qo = torch.empty_like(r["q_out"])
+    ko = torch.empty_like(r["k_out"])
+    launch(r["q"], r["k"], r["v"], pos.to(DEV), r["cos"], r["sin"], slots.to(DEV), kc, vc, qo, ko, T, r["ks"], r["vs"])
+    torch.cuda.synchronize()
+    okc, ovc = orc.new_caches(r["nb"], 16, 1, 128, "flash", False)
+    oqo, oko = orc.fused_rope_cache(_np(r["q"]), _np(r["k"]), _np(r["v"]), orc.low_word(pos.numpy()), _np(r["cos"]),
+                                    _np(r["sin"]), orc.low_word(slots.numpy()), okc, ovc, elem="bf16",
+                                    layout="flash", block_size=16)
+    np.testing.assert_array_equal(_bits(qo), orc.elem_bits(oqo, "bf16"))
+    np.testing.assert_array_equal(_bits(kc), okc)
+    np.testing.assert_array_equal(_bits(vc), ovc)
+
+
+@pytest.mark.parametrize("reuse", [True, False], ids=["half_dim", "full_dim"])
+@pytest.mark.parametrize("T", [1, 32])
+@pytest.mark.parametrize("layout", ["flash", "x4"])
+def test_reuse_freqs(reuse, T, layout):
+    run_case(T, 128, 8, 1, layout=layout, reuse=reuse)
+
+
+@pytest.mark.parametrize("T", [4, 32])
+@pytest.mark.parametrize("layout", ["flash", "x4", "x5"])
+def test_negative_slots(T, layout):
+    r = run_case(T, 128, 8, 1, layout=layout, negative_slots=True)
+    # skipped tokens leave their cache entries zero
+    assert r["kc"].float().abs().sum().item() > 0
+    assert int((r["slots"] >= 0).sum()) == (T + 1) // 2
+
+
+@pytest.mark.parametrize("T", [1, 32])
+@pytest.mark.parametrize("layout", ["flash", "x4", "x5"])
+@pytest.mark.parametrize("QH,KH,D", [(8, 1, 64), (8, 1, 128), (32, 8, 128)], ids=["GPTOSS-TP8", "Llama-TP8", "Llama8B-TP1"])
+def test_fp8_cache(T, layout, QH, KH, D):
+    r = run_case(T, D, QH, KH, layout=layout, fmt="fp8_tensor")
+    # the reference test's bound: dequantised error <= max|ref| / 8 (flash layout, tokens 0..T-1)
+    if layout == "flash":
+        kd = r["kc"].float() * r["ks"].float()
+        ref = torch.zeros_like(kd)
+        ref[: (T + 15) // 16].view(-1, KH, D)[:T] = r["k_out"].float()
+        assert (kd - ref).abs().max().item() <= max(1e-3, ref.abs().max().item() / 8)
+
+
+# ---- this build's additions --------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("scale", [(0.37, 1.3), (1.0, 1.0), (3.0e-3, 7.0)])
+def test_fp8_scales_where_the_approximate_reciprocal_differs(scale):
+    # v_rcp_f32 is off by one ulp at e.g. 3.0 and 0.37; the writer's reciprocal is correctly rounded
+    run_case(64, 128, 8, 2, layout="x5", fmt="fp8_tensor", scale=scale)
+
+
+@pytest.mark.parametrize("layout", ["flash", "x4", "x5"])
+@pytest.mark.parametrize("QH,KH,D", [(8, 1, 128), (32, 8, 128), (8, 1, 64), (16, 2, 256)])
+def test_fp8_per_token(layout, QH, KH, D):
+    run_case(48, D, QH, KH, layout=layout, fmt="fp8_token", slots=torch.randperm(32 * 16)[:48].int())
+
+
+@pytest.mark.parametrize("D", [16, 32, 80, 96, 192, 256, 512])
+@pytest.mark.parametrize("fmt", ["elem", "fp8_token"])
+def test_other_head_dims(D, fmt):
+    run_case(33, D, 6, 2, layout="x5", fmt=fmt)
+
+
+@pytest.mark.parametrize("layout", ["flash", "x4", "x5"])
+def test_fused_qkv_views(layout):
+    run_case(40, 128, 32, 8, layout=layout, fused_qkv=True, fmt="fp8_tensor")
+
+
+@pytest.mark.parametrize("bs", [1, 16, 64, 1024])
+def test_block_sizes_random_slots(bs):
+    layout = "x5" if bs % 16 == 0 else "x4"
+    nb = max(4, 3000 // bs)
+    slots = torch.randperm(nb * bs, generator=torch.Generator().manual_seed(bs))[:200].int()
+    run_case(200, 128, 8, 2, layout=layout, bs=bs, num_blocks=nb, slots=slots, fmt="fp8_token")
+
+
+def test_positions_clamped_and_slots_past_the_cache_skipped():
+    T = 16
+    pos = torch.tensor([0, 5, -3, 99, 100, 1 << 20, 7, 50, -1, 2, 3, 4, 98, 97, 1000, 1], dtype=torch.int32)
+    slots = torch.tensor([0, 1, 2, 3, 16 * 6 - 1, 16 * 6, 16 * 6 + 5, 1 << 30, 8, 9, -7, 11, 12, 13, 14, 15],
+                         dtype=torch.int32)
+    run_case(T, 128, 8, 2, layout="x5", positions=pos, slots=slots, num_blocks=6, max_pos=100, fmt="fp8_token")
+
+
+def test_large_prefill_batch():
+    T = 4096
+    slots = torch.randperm(5000, generator=torch.Generator().manual_seed(1))[:T].int()
+    run_case(T, 128, 32, 8, layout="x5", fmt="fp8_tensor", slots=slots, num_blocks=5000 // 16)
+
+
+def test_zero_tokens_is_a_no_op():
+    from flydsl_amd.fused_rope_cache import build_fused_rope_cache_module
+
+    launch = build_fused_rope_cache_module(head_dim=128, num_q_heads=8, num_kv_heads=1)
+    t = lambda *s: torch.zeros(*s, dtype=torch.bfloat16, device=DEV)  # noqa: E731
+    kc, vc = t(4, 16, 1, 128), t(4, 16, 1, 128)
+    launch(t(0, 8, 128), t(0, 1, 128), t(0, 1, 128), torch.zeros(0, dtype=torch.int32, device=DEV), t(16, 64),
+           t(16, 64), torch.zeros(0, dtype=torch.int32, device=DEV), kc, vc, t(0, 8, 128), t(0, 1, 128), 0,
+           torch.ones(1, device=DEV), torch.ones(1, device=DEV))
+    torch.cuda.synchronize()
+    assert kc.abs().sum().item() == 0
+
+
+def test_repeated_launches_reuse_argument_blocks():
+    # the launcher caches prepared argument blocks per tensor set; new slot values on the same
+    # tensors must still be honoured (the kernel reads them from device memory)
+    from flydsl_amd.fused_rope_cache import build_fused_rope_cache_module
+
+    r = run_case(8, 128, 8, 1, layout="x5", fmt="fp8_tensor")
+    launch = build_fused_rope_cache_module(head_dim=128, num_q_heads=8, num_kv_heads=1, flash_layout=False,
+                                           apply_scale=True)
+    slot_t = torch.zeros(8, dtype=torch.int32, device=DEV)
+    pos_t = r["pos"].to(DEV)
+    kc = torch.zeros_like(r["kc"])
+    vc = torch.zeros_like(r["vc"])
+    qo, ko = torch.empty_like(r["q_out"]), torch.empty_like(r["k_out"])
+    for step in range(3):
+        slot_t.copy_(torch.arange(8, dtype=torch.int32) + 8 * step)
+        launch(r["q"], r["k"], r["v"], pos_t, r["cos"], r["sin"], slot_t, kc, vc, qo, ko, 8, r["ks"], r["vs"])
+    torch.cuda.synchronize()
+    k_tok = oq.k_x_to_tok(_bits(kc))
+    for step in range(3):
+        for t in range(8):
+            blk, p = divmod(8 * step + t, 16)
+            np.testing.assert_array_equal(k_tok[blk, 0, p], _bits(r["kc"])[0, 0, :, t, :].reshape(-1))
+
+
+@pytest.mark.parametrize("per_token", [False, True], ids=["per_tensor", "per_token"])
+def test_write_then_decode(per_token):
+    """Write a batch's K/V with the writer (x-packed K, trans_v V, fp8) and decode over it."""
+    from flydsl_amd import pa_decode_ps_launch
+    from flydsl_amd.fused_rope_cache import build_fused_rope_cache_module
+
+    B, QH, KH, D, bs = 4, 16, 2, 128, 16
+    ctx = [37, 300, 129, 513]
+    g = torch.Generator().manual_seed(7)
+    blocks = [math.ceil(c / bs) for c in ctx]
+    nb = sum(blocks) + 3
+    perm = torch.randperm(nb, generator=g)
+    tables = torch.zeros(B, max(blocks), dtype=torch.int32)
+    start = 0
+    for b in range(B):
+        tables[b, : blocks[b]] = perm[start : start + blocks[b]]
+        start += blocks[b]
+    # every token of every sequence, prefill-style, in one launch
+    T = sum(ctx)
+    slots = torch.cat([tables[b, torch.arange(ctx[b]) // bs].long() * bs + torch.arange(ctx[b]) % bs
+                       for b in range(B)]).int()
+    positions = torch.cat([torch.arange(c) for c in ctx]).int()
+    k = torch.randn(T, KH, D, generator=g).bfloat16().to(DEV)
+    v = torch.randn(T, KH, D, generator=g).bfloat16().to(DEV)
+    q_tok = torch.randn(T, QH, D, generator=g).bfloat16().to(DEV)
+    th = torch.arange(MAX_POS)[:, None].float() * (10000.0 ** (-torch.arange(D // 2).float() / (D // 2)))
+    cos, sin = th.cos().bfloat16().to(DEV), th.sin().bfloat16().to(DEV)
+    kc = torch.zeros(nb, KH, D // 16, bs, 16, dtype=FP8, device=DEV)
+    vc = torch.zeros(nb, KH, bs // 16, D, 16, dtype=FP8, device=DEV)
+    if per_token:
+        ks = torch.zeros(nb, KH, bs, 1, device=DEV)
+        vs = torch.zeros(nb, KH, bs, 1, device=DEV)
+    else:
+        ks = torch.tensor([0.02], device=DEV)
+        vs = torch.tensor([0.015], device=DEV)
+    q_out = torch.empty_like(q_tok)
+    k_out = torch.empty_like(k)
+    launch = build_fused_rope_cache_module(head_dim=D, num_q_heads=QH, num_kv_heads=KH, block_size=bs,
+                                           flash_layout=False, apply_scale=True)
+    launch(q_tok, k, v, positions.to(DEV), cos, sin, slots.to(DEV), kc, vc, q_out, k_out, T, ks, vs)
+    # decode the last token of every sequence with its rotated query
+    last = torch.tensor(np.cumsum(ctx) - 1)
+    query = q_out[last.to(DEV)].contiguous()
+    out = torch.empty_like(query)
+    ctx_t = torch.tensor(ctx, dtype=torch.int32, device=DEV)
+    pa_decode_ps_launch(out, query, kc, vc, ctx_t, None, None, 1.0 / math.sqrt(D), ks, vs,
+                        block_tables=tables.to(DEV))
+    torch.cuda.synchronize()
+    # oracle: attention over the dequantised cache the writer produced (itself checked bit-exact above)
+    k_tok = oq.k_x_to_tok(_bits(kc))
+    v_tok = oq.v_4d_to_tok(oq.v_trans_to_4d(_bits(vc)))
+    ksn, vsn = ks.cpu().numpy(), vs.cpu().numpy()
+    for b in range(B):
+        rows = slots[int(np.sum(ctx[:b])) : int(np.sum(ctx[: b + 1]))].long().numpy()
+        blk, p = rows // bs, rows % bs
+        kk = e4m3_decode(k_tok[blk, :, p])  # [ctx, KH, D]
+        vv = e4m3_decode(v_tok[blk, :, p])
+        if per_token:
+            kk = kk * ksn[blk, :, p]
+            vv = vv * vsn[blk, :, p]
+        else:
+            kk, vv = kk * ksn[0], vv * vsn[0]
+        # the written keys are the rotated keys, to fp8 precision
+        kref = _np(k_out)[int(np.sum(ctx[:b])) : int(np.sum(ctx[: b + 1]))]
+        assert np.abs(kk - kref).max() <= np.abs(kref).max() / 8
+        want = oatt.reference_masked_attention(_np(query)[b : b + 1], kk, vv, 1.0 / math.sqrt(D), True, 0)
+        np.testing.assert_allclose(_np(out)[b : b + 1], want, atol=2e-2, rtol=2e-2)
