@@ -51,6 +51,9 @@ def _parse():
                     help="launch without get_pa_metadata's schedule (16 / 64-token pages then run the partition kernel)")
     ap.add_argument("--traffic-run", action="store_true",
                     help="for rocprofv3 --pmc passes: a 256 MiB copy (counter calibration) then --steps decode steps")
+    ap.add_argument("--path", default="decode", choices=["decode", "rope_cache"],
+                    help="decode: the headline paged decode; rope_cache: the fused RoPE + KV-cache writer")
+    ap.add_argument("--rope-tokens", type=int, default=16384, help="tokens per writer launch (--path rope_cache)")
     return ap.parse_args()
 
 
@@ -146,6 +149,193 @@ def cpu_baseline(w, seconds: float):
     }
 
 
+# ---------------------------------------------------------------- fused RoPE + KV-cache writer
+ROPE_METRIC = "KV-cache writer HBM GB/s (% of peak) + us/launch, fused NeoX RoPE + fp8 paged-cache write"
+ROPE_SHAPE = dict(num_q_heads=32, num_kv_heads=8, head_dim=128, block_size=16)  # Llama-3-8B, c2's cache format
+
+
+def rope_bytes_per_token(qh, kh, d, cache_bytes=1, reuse=True, index_bytes=4):
+    """Algorithmic HBM bytes of one token: read Q, K, V (bf16), its cos and sin rows and its
+    position and slot; write Q_out, K_out (bf16) and the K and V cache entries."""
+    cols = d // 2 if reuse else d
+    reads = (qh + 2 * kh) * d * 2 + 2 * cols * 2 + 2 * index_bytes
+    writes = (qh + kh) * d * 2 + 2 * kh * d * cache_bytes
+    return reads + writes
+
+
+def rope_workload(torch, dev, tokens, seed, num_blocks):
+    g = torch.Generator().manual_seed(seed)
+    qh, kh, d, bs = (ROPE_SHAPE[k] for k in ("num_q_heads", "num_kv_heads", "head_dim", "block_size"))
+    w = {
+        "q": torch.randn(tokens, qh, d, generator=g).bfloat16().to(dev),
+        "k": torch.randn(tokens, kh, d, generator=g).bfloat16().to(dev),
+        "v": torch.randn(tokens, kh, d, generator=g).bfloat16().to(dev),
+        # prefill chunk: consecutive positions and consecutive slots from a random page
+        "pos": (torch.arange(tokens, dtype=torch.int32) % 8192).to(dev),
+        "slot": (torch.randint(0, num_blocks - tokens // bs - 1, (1,), generator=g).item() * bs
+                 + torch.arange(tokens, dtype=torch.int32)).int().to(dev),
+        "q_out": torch.empty(tokens, qh, d, dtype=torch.bfloat16, device=dev),
+        "k_out": torch.empty(tokens, kh, d, dtype=torch.bfloat16, device=dev),
+    }
+    return w
+
+
+def rope_cpu_baseline(tokens: int, seconds: float):
+    """The numpy restatement of the writer on this host, one thread, on a bounded sample."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import rope_cache as orc
+
+    qh, kh, d, bs = (ROPE_SHAPE[k] for k in ("num_q_heads", "num_kv_heads", "head_dim", "block_size"))
+    rng = np.random.default_rng(0)
+    n = min(tokens, 256)
+    q = orc.round_elem(rng.standard_normal((n, qh, d)), "bf16")
+    k = orc.round_elem(rng.standard_normal((n, kh, d)), "bf16")
+    v = orc.round_elem(rng.standard_normal((n, kh, d)), "bf16")
+    cos = orc.round_elem(rng.standard_normal((8192, d // 2)), "bf16")
+    sin = orc.round_elem(rng.standard_normal((8192, d // 2)), "bf16")
+    nb = n // bs + 2
+    done = 0
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            kc, vc = orc.new_caches(nb, bs, kh, d, "x5", True)
+            orc.fused_rope_cache(q, k, v, np.arange(n), cos, sin, np.arange(n), kc, vc, elem="bf16", layout="x5",
+                                 block_size=bs, fmt="fp8_tensor", k_scale=np.float32(0.1), v_scale=np.float32(0.1))
+            done += n
+        dt = time.perf_counter() - t0
+    bpt = rope_bytes_per_token(qh, kh, d)
+    return {
+        "value": round(done * bpt / dt / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{done} tokens ({n} per pass) of the writer's numpy restatement, {dt:.1f} s, "
+        f"{dt / done * 1e6:.1f} us per token; host {platform.processor() or platform.machine()}",
+    }
+
+
+def rope_main(args):
+    import torch
+
+    from flydsl_amd.fused_rope_cache import build_fused_rope_cache_module
+
+    dev = torch.device("cuda:0")
+    qh, kh, d, bs = (ROPE_SHAPE[k] for k in ("num_q_heads", "num_kv_heads", "head_dim", "block_size"))
+    T = args.rope_tokens
+    nb = 4 * (T // bs) + 64
+    print(f"[bench] rope_cache: {T} tokens/launch, 2 input copies, cache {nb} pages", file=sys.stderr, flush=True)
+    works = [rope_workload(torch, dev, T, 7 + i, nb) for i in range(2)]
+    g = torch.Generator().manual_seed(3)
+    cos = torch.randn(8192, d // 2, generator=g).bfloat16().to(dev)
+    sin = torch.randn(8192, d // 2, generator=g).bfloat16().to(dev)
+    kc = torch.zeros(nb, kh, d // 16, bs, 16, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros(nb, kh, bs // 16, d, 16, dtype=torch.float8_e4m3fn, device=dev)
+    ks = torch.tensor([0.1], device=dev)
+    vs = torch.tensor([0.1], device=dev)
+    launch = build_fused_rope_cache_module(head_dim=d, num_q_heads=qh, num_kv_heads=kh, block_size=bs,
+                                           flash_layout=False, apply_scale=True)
+
+    def step(i, n=T):
+        w = works[i % 2]
+        launch(w["q"], w["k"], w["v"], w["pos"], cos, sin, w["slot"], kc, vc, w["q_out"], w["k_out"], n, ks, vs)
+
+    if args.traffic_run:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            step(i)
+        torch.cuda.synchronize()
+        print(json.dumps({"traffic_run": "rope_cache", "copy_bytes": src.numel(), "steps": args.steps}))
+        return
+
+    def per_launch(n):
+        # HIP events bracketing each launch on the launch stream (torch's current stream).
+        # A GPU-side sleep holds the stream until every launch is queued, so a kernel
+        # shorter than the host's launch overhead is timed without host gaps.
+        for i in range(args.warmup):
+            step(i, n)
+        evs = _events(torch, 2 * args.steps)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(int(2.5e6 + 2e4 * args.steps))  # cycles: several ms of queue head start
+        for i in range(args.steps):
+            evs[2 * i].record()
+            step(i, n)
+            evs[2 * i + 1].record()
+        torch.cuda.synchronize()
+        ms = sorted(evs[2 * i].elapsed_time(evs[2 * i + 1]) for i in range(args.steps))
+        return sum(ms) / len(ms), ms[len(ms) // 2]
+
+    for i in range(args.warmup):
+        step(i)
+    e0, e1 = _events(torch, 2)
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(args.steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+    k_mean, k_med = per_launch(T)
+    dec_mean, dec_med = per_launch(64)  # a decode step of c2's batch: one token per sequence
+
+    bpt = rope_bytes_per_token(qh, kh, d)
+    kbytes = bpt * T
+    gbs = kbytes / (ms_per_step * 1e-3) / 1e9
+    achieved = kbytes / (k_mean * 1e-3) / 1e9
+    traffic = None
+    tfile = ROOT / "profiles" / "rope_cache_kernel_prefill16k_traffic.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
+        except Exception:
+            traffic = None
+    cpu = rope_cpu_baseline(T, args.cpu_seconds) if args.cpu_baseline == "on" else None
+    line = {
+        "metric": ROPE_METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_step": round(ms_per_step * 1e3, 2),
+        "pct_of_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"rope_cache prefill chunk: {T} tokens, Hq {qh} / Hkv {kh}, D {d}, bs {bs}, "
+            "bf16 in, fp8 e4m3fn per-tensor cache, x-packed K + trans_v V, half-width cos/sin",
+            "tokens": T,
+            "bytes_per_token": bpt,
+            "input_copies_rotated": 2,
+        },
+        "decode_step_64_tokens_us": {"mean": round(dec_mean * 1e3, 2), "median": round(dec_med * 1e3, 2),
+                                     "bytes": bpt * 64},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "rope_cache_kernel",
+            "algorithmic_bytes_per_launch": kbytes,
+            "kernel_us_mean": round(k_mean * 1e3, 2),
+            "kernel_us_median": round(k_med * 1e3, 2),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = _parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -156,6 +346,8 @@ def main():
             file=sys.stderr,
         )
         sys.exit(2)
+    if args.path == "rope_cache":
+        return rope_main(args)
 
     import torch
 

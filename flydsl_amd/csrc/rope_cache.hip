@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+
 #include "pa_common.h"
 #include "pa_fp8.h"
 
@@ -38,7 +39,10 @@ struct RopeParams {
     float *ks, *vs;
     int64_t sq_t, sq_h, sk_t, sk_h, sv_t, sv_h, sqo_t, sqo_h, sko_t, sko_h, scos, ssin;
     int64_t skc_b, skc_h, skc_t, svc_b, svc_h, svc_t, sks_b, sks_h;
-    int64_t rows;  // num_tokens * (num_q_heads + num_kv_heads)
+    int64_t q_rows;   // num_tokens * num_q_heads
+    int64_t q_tiles;  // workgroups of Q rows (the K/V workgroups follow)
+    int32_t T;
+    int32_t gather;   // V of the dim-major layouts may be staged through LDS
     int32_t QH, KH, D, bs, nb, max_pos;
     int32_t pos_shift, slot_shift;  // 1: int64 index tensor, low word at element 2t
     int32_t reuse, lpr_log2, chunks;
@@ -182,74 +186,102 @@ __device__ __forceinline__ void write_cache(uint8_t *tile, int64_t stride_token,
     }
 }
 
-template <int ELEM, int FMT, int LAYOUT>
-__global__ __launch_bounds__(kRopeThreads) void rope_cache_kernel(RopeParams p) {
-    const int64_t gid = int64_t(blockIdx.x) * kRopeThreads + threadIdx.x;
-    const int64_t row = gid >> p.lpr_log2;
-    const int c = int(gid & ((1 << p.lpr_log2) - 1));
-    const int heads = p.QH + p.KH;
-    const bool live = row < p.rows && c < p.chunks;
-    const int half = p.D >> 1;
-    const int d1 = 8 * c, d2 = half + 8 * c;
+// One row's inputs as loaded (raw 16-byte vectors) and its indices.
+struct RowIn {
+    uint4 x1, x2, v1, v2, c1, s1, c2, s2;
+    int t, h, slot, praw;
+    bool live, is_k;
+};
 
-    int t = 0, h = 0;
-    bool is_k = false;
-    if (row < p.rows) {
-        t = int(row / heads);
-        const int hh = int(row - int64_t(t) * heads);
-        is_k = hh >= p.QH;
-        h = is_k ? hh - p.QH : hh;
+// Loads of one row that depend on nothing but the row (t, h, is_k, live set by the
+// caller): position, the Q or K vector, and for K rows the slot and the V vector.
+__device__ __forceinline__ void load_row(const RopeParams &p, int d1, int d2, RowIn &r) {
+    r.slot = -1;
+    if (!r.live) return;
+    r.praw = p.pos[int64_t(r.t) << p.pos_shift];
+    const uint16_t *x = r.is_k ? p.k + int64_t(r.t) * p.sk_t + int64_t(r.h) * p.sk_h
+                               : p.q + int64_t(r.t) * p.sq_t + int64_t(r.h) * p.sq_h;
+    r.x1 = ld16v(x + d1);
+    r.x2 = ld16v(x + d2);
+    if (r.is_k) {
+        r.slot = p.slot[int64_t(r.t) << p.slot_shift];
+        const uint16_t *vr = p.v + int64_t(r.t) * p.sv_t + int64_t(r.h) * p.sv_h;
+        r.v1 = ld16v(vr + d1);
+        r.v2 = ld16v(vr + d2);
     }
+}
 
-    float x1[8], x2[8], v1[8], v2[8];
-    int slot = -1;
-    if (live) {
-        const int pos = min(max(p.pos[int64_t(t) << p.pos_shift], 0), p.max_pos - 1);
-        const uint16_t *crow = p.cos + int64_t(pos) * p.scos;
-        const uint16_t *srow = p.sin + int64_t(pos) * p.ssin;
-        const uint16_t *x = is_k ? p.k + int64_t(t) * p.sk_t + int64_t(h) * p.sk_h
-                                 : p.q + int64_t(t) * p.sq_t + int64_t(h) * p.sq_h;
-        const uint4 wx1 = ld16v(x + d1), wx2 = ld16v(x + d2);
-        const uint4 wc1 = ld16v(crow + d1), ws1 = ld16v(srow + d1);
-        float c1[8], s1[8], c2[8], s2[8];
-        unpack8<ELEM>(wc1, c1);
-        unpack8<ELEM>(ws1, s1);
-        if (p.reuse) {
+// The cos / sin rows of the row's position (the only loads that wait for another).
+__device__ __forceinline__ void load_freqs(const RopeParams &p, int d1, int d2, RowIn &r) {
+    if (!r.live) return;
+    const int pos = min(max(r.praw, 0), p.max_pos - 1);
+    const uint16_t *crow = p.cos + int64_t(pos) * p.scos;
+    const uint16_t *srow = p.sin + int64_t(pos) * p.ssin;
+    r.c1 = ld16v(crow + d1);
+    r.s1 = ld16v(srow + d1);
+    if (!p.reuse) {
+        r.c2 = ld16v(crow + d2);
+        r.s2 = ld16v(srow + d2);
+    }
+}
+
+// Rotation and output store of one row; returns the rotated values in x1 / x2.
+template <int ELEM>
+__device__ __forceinline__ void rotate_row(const RopeParams &p, const RowIn &r, int d1, int d2, float (&x1)[8],
+                                           float (&x2)[8]) {
+    float c1[8], s1[8], c2[8], s2[8];
+    unpack8<ELEM>(r.c1, c1);
+    unpack8<ELEM>(r.s1, s1);
+    if (p.reuse) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                c2[i] = c1[i];
-                s2[i] = s1[i];
-            }
-        } else {
-            unpack8<ELEM>(ld16v(crow + d2), c2);
-            unpack8<ELEM>(ld16v(srow + d2), s2);
+        for (int i = 0; i < 8; ++i) {
+            c2[i] = c1[i];
+            s2[i] = s1[i];
         }
-        unpack8<ELEM>(wx1, x1);
-        unpack8<ELEM>(wx2, x2);
-        rotate<ELEM>(x1, x2, c1, s1, c2, s2);
-        uint16_t *out = is_k ? p.ko + int64_t(t) * p.sko_t + int64_t(h) * p.sko_h
-                             : p.qo + int64_t(t) * p.sqo_t + int64_t(h) * p.sqo_h;
-        st16v(out + d1, pack8<ELEM>(x1));
-        st16v(out + d2, pack8<ELEM>(x2));
-        if (is_k) {
-            slot = p.slot[int64_t(t) << p.slot_shift];
-            if (slot >= 0 && slot / p.bs < p.nb) {
-                const uint16_t *vr = p.v + int64_t(t) * p.sv_t + int64_t(h) * p.sv_h;
-                unpack8<ELEM>(ld16v(vr + d1), v1);
-                unpack8<ELEM>(ld16v(vr + d2), v2);
-            } else {
-                slot = -1;
-            }
+    } else {
+        unpack8<ELEM>(r.c2, c2);
+        unpack8<ELEM>(r.s2, s2);
+    }
+    unpack8<ELEM>(r.x1, x1);
+    unpack8<ELEM>(r.x2, x2);
+    rotate<ELEM>(x1, x2, c1, s1, c2, s2);
+    uint16_t *out = r.is_k ? p.ko + int64_t(r.t) * p.sko_t + int64_t(r.h) * p.sko_h
+                           : p.qo + int64_t(r.t) * p.sqo_t + int64_t(r.h) * p.sqo_h;
+    st16v(out + d1, pack8<ELEM>(x1));
+    st16v(out + d2, pack8<ELEM>(x2));
+}
+
+// Cache element pattern of one value (16-bit element or fp8 code).
+template <int FMT, int ELEM>
+__device__ __forceinline__ uint32_t cache_bits(float x) {
+    if constexpr (FMT == PA_FP8_CACHE_ELEM) return from_f<ELEM>(x);
+    else return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x, 0.0f, 0, false) & 0xffu;
+}
+
+// K / V rows (K rows of the KV tiles): rotation, output store, cache values and
+// writes.  Every thread of the wave calls this (the per-token scale exchange
+// needs the whole wave).  With `vstage` the V entry goes to the workgroup's
+// staging buffer (row i of the 16-token group, all head dims) instead of memory.
+template <int ELEM, int FMT, int LAYOUT>
+__device__ __forceinline__ void finish_kv_row(const RopeParams &p, const RowIn &r, int c, int d1, int d2,
+                                              float kscale, float vscale, uint16_t *vstage) {
+    float x1[8], x2[8], v1[8], v2[8];
+    bool write = false;
+    if (r.live) {
+        rotate_row<ELEM>(p, r, d1, d2, x1, x2);
+        write = r.slot >= 0 && r.slot / p.bs < p.nb;
+        if (write) {
+            unpack8<ELEM>(r.v1, v1);
+            unpack8<ELEM>(r.v2, v2);
         }
     }
-    const bool write = live && is_k && slot >= 0;
-    const int blk = write ? slot / p.bs : 0;
-    const int bpos = write ? slot - blk * p.bs : 0;
+    const int blk = write ? r.slot / p.bs : 0;
+    const int bpos = write ? r.slot - blk * p.bs : 0;
 
     if constexpr (FMT == PA_FP8_CACHE_FP8_TENSOR) {
         if (write) {
-            const float rk = 1.0f / p.ks[0];
-            const float rv = 1.0f / p.vs[0];
+            const float rk = 1.0f / kscale;
+            const float rv = 1.0f / vscale;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 x1[i] *= rk;
@@ -290,7 +322,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_cache_kernel(RopeParams p) 
                 v2[i] = v2[i] / sv;
             }
             if (c == 0) {
-                const int64_t so = int64_t(blk) * p.sks_b + int64_t(h) * p.sks_h + bpos;
+                const int64_t so = int64_t(blk) * p.sks_b + int64_t(r.h) * p.sks_h + bpos;
                 p.ks[so] = sk;
                 p.vs[so] = sv;
             }
@@ -298,10 +330,119 @@ __global__ __launch_bounds__(kRopeThreads) void rope_cache_kernel(RopeParams p) 
     }
     if (write) {
         constexpr int esz = FMT == PA_FP8_CACHE_ELEM ? 2 : 1;
-        uint8_t *kt = p.kc + (int64_t(blk) * p.skc_b + int64_t(h) * p.skc_h) * esz;
-        uint8_t *vt = p.vc + (int64_t(blk) * p.svc_b + int64_t(h) * p.svc_h) * esz;
+        uint8_t *kt = p.kc + (int64_t(blk) * p.skc_b + int64_t(r.h) * p.skc_h) * esz;
         write_cache<FMT, LAYOUT, false, ELEM>(kt, p.skc_t, bpos, p.bs, p.D, d1, d2, x1, x2);
-        write_cache<FMT, LAYOUT, true, ELEM>(vt, p.svc_t, bpos, p.bs, p.D, d1, d2, v1, v2);
+        if (vstage) {
+            // staging buffer [group][D][16 tokens] of cache elements
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                vstage[(d1 + i) * 16] = (uint16_t)cache_bits<FMT, ELEM>(v1[i]);
+                vstage[(d2 + i) * 16] = (uint16_t)cache_bits<FMT, ELEM>(v2[i]);
+            }
+        } else {
+            uint8_t *vt = p.vc + (int64_t(blk) * p.svc_b + int64_t(r.h) * p.svc_h) * esz;
+            write_cache<FMT, LAYOUT, true, ELEM>(vt, p.svc_t, bpos, p.bs, p.D, d1, d2, v1, v2);
+        }
+    }
+}
+
+// Grid: Q tiles first, then K/V tiles; a tile is 256 threads = 256 / lanes_per_row
+// rows, thread tid handling chunk tid % lanes_per_row of row tid / lanes_per_row.
+// Q rows are numbered t * QH + h.  K/V rows are numbered in groups of 16 tokens,
+// head-major inside a group: ((t / 16) * KH + h) * 16 + t % 16, so a K/V tile holds
+// whole (kv head, 16 consecutive tokens) groups.  When every group of a K/V tile
+// goes to one 16-aligned run of slots (a prefill chunk), the V entries of the
+// dim-major layouts are staged in LDS and each (head, dim) segment of 16 tokens is
+// written with one 16-byte store (two for 16-bit caches); otherwise (decode: one
+// token per sequence) each lane writes its own elements.
+// Workgroups are dealt round-robin to the 8 XCDs (workgroup w runs on XCD w % 8);
+// the remapped index gives XCD x one contiguous range of tiles, so that cache
+// entries of neighbouring tokens written element-wise merge in one L2.
+template <int ELEM, int FMT, int LAYOUT>
+__global__ __launch_bounds__(kRopeThreads) void rope_cache_kernel(RopeParams p) {
+    __shared__ __align__(16) uint16_t vstage[kRopeThreads * 16];
+    __shared__ int group_slot0[16];
+    const uint32_t nwg = gridDim.x, w = blockIdx.x;
+    const uint32_t xcd = w & 7u, per = nwg >> 3, rem = nwg & 7u;
+    const int64_t tile = int64_t(xcd * per + min(xcd, rem) + (w >> 3));
+    const int lpr_log2 = p.lpr_log2;
+    const int c = int(threadIdx.x & ((1u << lpr_log2) - 1));
+    const int rpp = kRopeThreads >> lpr_log2;  // rows per tile
+    const int lrow = int(threadIdx.x >> lpr_log2);
+    const bool lane_live = c < p.chunks;
+    const int d1 = 8 * c, d2 = (p.D >> 1) + 8 * c;
+    RowIn r;
+
+    if (tile < p.q_tiles) {
+        const int64_t row = tile * rpp + lrow;
+        r.live = lane_live && row < p.q_rows;
+        r.is_k = false;
+        r.t = r.live ? int(row / p.QH) : 0;
+        r.h = r.live ? int(row - int64_t(r.t) * p.QH) : 0;
+        load_row(p, d1, d2, r);
+        load_freqs(p, d1, d2, r);
+        if (r.live) {
+            float x1[8], x2[8];
+            rotate_row<ELEM>(p, r, d1, d2, x1, x2);
+        }
+        return;
+    }
+
+    float kscale = 1.0f, vscale = 1.0f;
+    if constexpr (FMT == PA_FP8_CACHE_FP8_TENSOR) {
+        kscale = p.ks[0];
+        vscale = p.vs[0];
+    }
+    const int64_t krow = (tile - p.q_tiles) * rpp + lrow;
+    const int64_t grp = krow >> 4;  // (token group, head) pair
+    const int gi = int(krow & 15);  // token inside the group
+    const int64_t tg = grp / p.KH;
+    r.h = int(grp - tg * p.KH);
+    r.t = int(tg * 16 + gi);
+    r.is_k = true;
+    r.live = lane_live && r.t < p.T;
+    load_row(p, d1, d2, r);
+    load_freqs(p, d1, d2, r);
+
+    bool stage = false;
+    if (LAYOUT != PA_FP8_KV_FLASH && p.gather) {
+        // stage V through LDS when every row of every group in this tile sits at
+        // slot0 + i of an aligned run (slot0 = the group's first slot)
+        const int slot0 = tg * 16 < p.T ? p.slot[int64_t(tg * 16) << p.slot_shift] : -1;
+        const bool run = r.t < p.T && slot0 >= 0 && (slot0 & 15) == 0 && slot0 / p.bs < p.nb &&
+                         r.slot == slot0 + gi;
+        stage = __syncthreads_and(run || !lane_live) != 0;
+        if (stage && gi == 0 && c == 0) group_slot0[lrow >> 4] = slot0;
+    }
+    uint16_t *vs_row = stage ? vstage + (lrow >> 4) * (p.D * 16) + gi : nullptr;
+    finish_kv_row<ELEM, FMT, LAYOUT>(p, r, c, d1, d2, kscale, vscale, vs_row);
+    if (!stage) return;
+    __syncthreads();
+    // one (group, head dim) segment of 16 tokens per thread
+    constexpr int esz = FMT == PA_FP8_CACHE_ELEM ? 2 : 1;
+    const int segs = (rpp >> 4) * p.D;
+    for (int j = threadIdx.x; j < segs; j += kRopeThreads) {
+        const int g = j / p.D, d = j - g * p.D;
+        const int64_t gg = ((tile - p.q_tiles) * rpp >> 4) + g;
+        const int h = int(gg % p.KH);
+        const int slot0 = group_slot0[g];
+        const int blk = slot0 / p.bs, pos0 = slot0 - blk * p.bs;
+        const int64_t off = LAYOUT == PA_FP8_KV_X_TRANS ? int64_t(pos0 >> 4) * (int64_t(p.D) * 16) + int64_t(d) * 16
+                                                        : int64_t(d) * p.bs + pos0;
+        uint8_t *dst = p.vc + (int64_t(blk) * p.svc_b + int64_t(h) * p.svc_h + off) * esz;
+        const uint16_t *src = vstage + (g * p.D + d) * 16;
+        if constexpr (FMT == PA_FP8_CACHE_ELEM) {
+            const uint4 *s4 = reinterpret_cast<const uint4 *>(src);
+            reinterpret_cast<uint4 *>(dst)[0] = s4[0];
+            reinterpret_cast<uint4 *>(dst)[1] = s4[1];
+        } else {
+            uint32_t wds[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                wds[q] = (src[4 * q] & 0xffu) | ((src[4 * q + 1] & 0xffu) << 8) | ((src[4 * q + 2] & 0xffu) << 16) |
+                         ((src[4 * q + 3] & 0xffu) << 24);
+            *reinterpret_cast<uint4 *>(dst) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
+        }
     }
 }
 
@@ -413,7 +554,6 @@ extern "C" int pa_fp8_rope_cache(const pa_fp8_rope_cache_args *a, void *hip_stre
     p.svc_t = a->stride_vc_token;
     p.sks_b = a->stride_ks_block;
     p.sks_h = a->stride_ks_head;
-    p.rows = int64_t(a->num_tokens) * (a->num_q_heads + a->num_kv_heads);
     p.QH = a->num_q_heads;
     p.KH = a->num_kv_heads;
     p.D = D;
@@ -425,9 +565,18 @@ extern "C" int pa_fp8_rope_cache(const pa_fp8_rope_cache_args *a, void *hip_stre
     p.reuse = a->reuse_freqs_front_part ? 1 : 0;
     p.lpr_log2 = lpr_log2;
     p.chunks = chunks;
-    const int64_t threads = p.rows << lpr_log2;
-    const int64_t blocks = (threads + kRopeThreads - 1) / kRopeThreads;
+    const int64_t rpp = kRopeThreads >> lpr_log2;
+    p.T = a->num_tokens;
+    p.q_rows = int64_t(a->num_tokens) * a->num_q_heads;
+    p.q_tiles = (p.q_rows + rpp - 1) / rpp;
+    const int64_t kv_rows = (int64_t(a->num_tokens) + 15) / 16 * 16 * a->num_kv_heads;
+    const int64_t blocks = p.q_tiles + (kv_rows + rpp - 1) / rpp;
     if (blocks > 0x7fffffffLL) return PA_FP8_ERR_SHAPE;
+    // staged V writes: whole 16-token groups per workgroup, 16-aligned runs inside a
+    // page, 16-byte aligned (block, head) tiles
+    const int64_t esz = a->cache_format == PA_FP8_CACHE_ELEM ? 2 : 1;
+    p.gather = rpp >= 16 && a->block_size % 16 == 0 && aligned(a->value_cache, 16) &&
+               (a->stride_vc_block * esz) % 16 == 0 && (a->stride_vc_head * esz) % 16 == 0;
     const dim3 grid((unsigned)blocks);
     hipStream_t s = static_cast<hipStream_t>(hip_stream);
     const hipError_t e = a->elem_dtype == PA_FP8_BF16

@@ -401,3 +401,39 @@ def test_write_then_decode(per_token):
         assert np.abs(kk - kref).max() <= np.abs(kref).max() / 8
         want = oatt.reference_masked_attention(_np(query)[b : b + 1], kk, vv, 1.0 / math.sqrt(D), True, 0)
         np.testing.assert_allclose(_np(out)[b : b + 1], want, atol=2e-2, rtol=2e-2)
+
+
+def _runs(kind, T, bs, nb, seed):
+    """Slot patterns around the staged V path (16-token groups of consecutive, 16-aligned slots)."""
+    g = torch.Generator().manual_seed(seed)
+    if kind == "aligned":
+        return torch.arange(T, dtype=torch.int32) + 3 * bs
+    if kind == "misaligned":
+        return torch.arange(T, dtype=torch.int32) + 5
+    if kind == "one_swap":
+        s = torch.arange(T, dtype=torch.int32) + bs
+        s[[17, 18]] = s[[18, 17]]
+        return s
+    if kind == "pages":  # every 16-token group in its own random page, aligned inside it
+        groups = (T + 15) // 16
+        starts = torch.randperm(nb * bs // 16, generator=g)[:groups].int() * 16
+        return (starts.repeat_interleave(16)[:T] + torch.arange(T, dtype=torch.int32) % 16).int()
+    if kind == "tail_negative":
+        s = torch.arange(T, dtype=torch.int32)
+        s[-3:] = -1
+        return s
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["aligned", "misaligned", "one_swap", "pages", "tail_negative"])
+@pytest.mark.parametrize("T", [50, 64, 200])
+@pytest.mark.parametrize("layout,fmt", [("x5", "fp8_tensor"), ("x4", "fp8_token"), ("x5", "elem"), ("x4", "elem")])
+def test_prefill_slot_runs(kind, T, layout, fmt):
+    bs, nb = 32, 24
+    run_case(T, 128, 8, 2, layout=layout, fmt=fmt, bs=bs, num_blocks=nb, slots=_runs(kind, T, bs, nb, T))
+
+
+@pytest.mark.parametrize("D,QH,KH", [(64, 8, 1), (256, 4, 2), (96, 6, 2), (512, 2, 1)])
+def test_prefill_runs_other_head_dims(D, QH, KH):
+    # D=512 has 8 rows per workgroup (fewer than a 16-token group): element-wise V writes
+    run_case(80, D, QH, KH, layout="x5", fmt="fp8_token", bs=16, num_blocks=12, slots=_runs("aligned", 80, 16, 12, 0))
