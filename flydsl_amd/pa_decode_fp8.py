@@ -710,14 +710,26 @@ def get_pa_metadata(
     num_query_heads: int,
     num_kv_heads: int,
     partition_size: int = KV_COMPUTE_BLOCK,
+    *,
+    graph_safe: bool = None,
 ):
     """Worklist metadata for the persistent decode (kernels/pa_decode_fp8.py:1729-1859).
 
     Runs the device scheduler ``get_pa_metadata_v1`` over
-    ``num_sm = (CUs * 3 // kv_heads) * kv_heads`` bins; work_info kv ranges are
-    cumulative ``partition_size``-token partition indices.  Synchronises once on
-    ``reduce_indptr[-1]`` to size the partial buffers, as the reference does.
+    ``num_sm = (CUs * 2 // kv_heads) * kv_heads`` bins; work_info kv ranges are
+    cumulative ``partition_size``-token partition indices.
+
+    By default it synchronises once on ``reduce_indptr[-1]`` to size the partial
+    buffers, as the reference does (:1832).  With ``graph_safe`` (the default
+    while the current stream is being captured into a graph) it reads nothing
+    back: the partial buffers are sized for the scheduler's bound on split
+    partials (``reduce_partial_map``'s length, kernels/pa_metadata.py:66-72), and
+    ``uniform_context`` is False.  Everything it launches is then capturable, so a
+    graph can hold the schedule and the decode together and be replayed over new
+    context lengths.  The reference's ``get_pa_metadata`` cannot be captured.
     """
+    if graph_safe is None:
+        graph_safe = _is_current_stream_capturing()
     dev = query.device
     batch_size = context_lengths.shape[0]
     query_length = query.shape[0] // batch_size
@@ -754,11 +766,15 @@ def get_pa_metadata(
         num_cu=num_sm,
     )
     work_info_flat = work_info.reshape(-1).contiguous()
-    # one host read (the reference reads reduce_indptr[-1] here too): the partial
-    # count, and whether every sequence has the same context length
-    ctx_i32 = context_lengths.to(torch.int32)
-    host = torch.stack([reduce_indptr[-1], (ctx_i32.max() == ctx_i32.min()).to(torch.int32)]).cpu()
-    num_partials, uniform = int(host[0]), bool(host[1])
+    if graph_safe:
+        # no host read: room for every partial the schedule can emit
+        num_partials, uniform = reduce_partial_map.numel(), False
+    else:
+        # one host read (the reference reads reduce_indptr[-1] here too): the partial
+        # count, and whether every sequence has the same context length
+        ctx_i32 = context_lengths.to(torch.int32)
+        host = torch.stack([reduce_indptr[-1], (ctx_i32.max() == ctx_i32.min()).to(torch.int32)]).cpu()
+        num_partials, uniform = int(host[0]), bool(host[1])
     partial_output = torch.empty(
         ((num_partials + 1) * query_length, 1, num_query_heads, head_size), dtype=torch.float32, device=dev
     )

@@ -92,8 +92,10 @@ def get_pa_metadata_v1(
     if work_info.numel() % _WORK_INFO_FIELDS:
         raise ValueError("work_info must hold 8 int32 per work")
     if work_metadata_ptrs is not None and work_metadata_ptrs.numel() >= 2:
-        work_metadata_ptrs[0] = work_indptr.data_ptr()
-        work_metadata_ptrs[1] = work_info.data_ptr()
+        # device fills (capturable into a graph), not host-to-device copies
+        ptrs = work_metadata_ptrs.view(torch.int64)
+        ptrs[0:1].fill_(work_indptr.data_ptr())
+        ptrs[1:2].fill_(work_info.data_ptr())
     a = _lib.MetadataArgs()
     a.seqlens_qo_indptr = seqlens_qo_indptr.data_ptr()
     a.context_lens = context_lens.data_ptr()
