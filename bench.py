@@ -103,7 +103,7 @@ _KERNEL_NAMES = {
     "decode_partitions": "pa_decode_partition_kernel",
     "lse_reduce": "pa_lse_reduce_kernel",
     "decode_worklist": "pa_decode_worklist_kernel",
-    "reduce_v1": "pa_reduce_v1_kernel",
+    "reduce_v1": "pa_reduce_v1_rows_kernel",
 }
 
 

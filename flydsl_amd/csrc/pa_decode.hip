@@ -148,6 +148,12 @@ __device__ __forceinline__ bf16x8 pack_bf16x8(f32x4 a, f32x4 b) {
 template <int MTPW>
 constexpr int kWavesPerSimd = MTPW == 1 ? 2 : 1;
 
+#ifndef PA_FP8_STAGED_WAVES
+#define PA_FP8_STAGED_WAVES 2  // waves per SIMD the LDS-staged layout is compiled for
+#endif
+template <int MTPW, int NS>
+constexpr int kWavesFor = NS == 0 ? PA_FP8_STAGED_WAVES : kWavesPerSimd<MTPW>;
+
 // Query rows of one wave: MTPW groups of 16 rows (r = qi*g + gi), the QK B
 // operands and the keys each row may see.  Lane (qrow l16, kg) holds dims
 // 32kg..32kg+31 of its row; keys visible to a row are [lo_n, hi_n) (causal bound
@@ -155,14 +161,65 @@ constexpr int kWavesPerSimd = MTPW == 1 ? 2 : 1;
 // wave's live rows (wave-uniform).
 template <int MTPW>
 struct RowSet {
+    static constexpr bool kFp8 = false;
     bf16x8 qop[MTPW][4];
     int lo_n[MTPW], hi_n[MTPW];
     int lo_max, hi_min;
 };
 
+// Query rows as a two-term fp8 split for the fp8 QK products: x = q * inv (inv =
+// 448 / amax of the row), hi = e4m3(x), lo = e4m3(x - hi), so q ~ (hi + lo) / inv
+// to about 8 significant bits (bf16's precision); dq = 1 / inv restores the logit.
 template <int MTPW>
-__device__ __forceinline__ void setup_rows(RowSet<MTPW> &rw, const DecodeParams &p, int b, int h, int ctx, int tok_lo,
+struct RowSetF8 {
+    static constexpr bool kFp8 = true;
+    i32x8 qh[MTPW], ql[MTPW];
+    float dq[MTPW];
+    int lo_n[MTPW], hi_n[MTPW];
+    int lo_max, hi_min;
+};
+
+// fp8 two-term split of one lane's 32 query values (dims 32kg .. 32kg+31 of its
+// row); the row's amax is reduced over its 4 lanes (kg = lane / 16).
+template <int MTPW>
+__device__ __forceinline__ void split_q_fp8(RowSetF8<MTPW> &rw, int mg, const bf16x8 (&q)[4], bool live) {
+    float x[32];
+    float amax = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            x[8 * s + i] = (float)q[s][i];
+            amax = fmaxf(amax, fabsf(x[8 * s + i]));
+        }
+    amax = fmaxf(amax, shfl_xor_f(amax, 16));
+    amax = fmaxf(amax, shfl_xor_f(amax, 32));
+    const float inv = (live && amax > 0.0f) ? 448.0f / amax : 1.0f;
+    rw.dq[mg] = 1.0f / inv;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+        float v[4], r[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = x[4 * w + i] * inv;
+        int hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+        hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], hi, true);
+        const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+        const f32x2 h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+        r[0] = v[0] - h01[0];
+        r[1] = v[1] - h01[1];
+        r[2] = v[2] - h23[0];
+        r[3] = v[3] - h23[1];
+        int lo = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
+        lo = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], lo, true);
+        rw.qh[mg][w] = hi;
+        rw.ql[mg][w] = lo;
+    }
+}
+
+template <class RW>
+__device__ __forceinline__ void setup_rows(RW &rw, const DecodeParams &p, int b, int h, int ctx, int tok_lo,
                                            int tok_hi, int row_group0, int l16, int kg) {
+    constexpr int MTPW = sizeof(rw.lo_n) / sizeof(int);
     rw.lo_max = tok_lo;
     rw.hi_min = tok_hi;
 #pragma unroll
@@ -173,13 +230,27 @@ __device__ __forceinline__ void setup_rows(RowSet<MTPW> &rw, const DecodeParams 
             const int gi = n - qi * p.g;
             const uint16_t *qrow =
                 p.query + (int64_t)(b * p.ql + qi) * p.s_q_seq + (int64_t)(h * p.g + gi) * p.s_q_head + 32 * kg;
+            bf16x8 q[4];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) rw.qop[mg][s] = load_q8(qrow + 8 * s, p.q_f16 != 0);
+            for (int s = 0; s < 4; ++s) q[s] = load_q8(qrow + 8 * s, p.q_f16 != 0);
+            if constexpr (RW::kFp8) {
+                split_q_fp8<MTPW>(rw, mg, q, true);
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) rw.qop[mg][s] = q[s];
+            }
             rw.hi_n[mg] = min(tok_hi, ctx + 1 - p.ql + qi);
             rw.lo_n[mg] = p.sw > 0 ? max(tok_lo, ctx - p.ql - p.sw + qi) : tok_lo;
         } else {
+            bf16x8 q[4];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) rw.qop[mg][s] = bf16x8{};
+            for (int s = 0; s < 4; ++s) q[s] = bf16x8{};
+            if constexpr (RW::kFp8) {
+                split_q_fp8<MTPW>(rw, mg, q, false);
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) rw.qop[mg][s] = q[s];
+            }
             rw.hi_n[mg] = tok_hi;  // padded rows: any finite value, never stored
             rw.lo_n[mg] = tok_lo;
         }
@@ -223,8 +294,13 @@ struct SmState {
 // tokens of group kg -- exactly the tokens of its PV operand row.  Writes the
 // bf16 probabilities of every row group to pop.  After the QK products, after_qk()
 // runs (the K registers are free again).
-template <int MTPW, bool PER_TOKEN, class AfterQk>
-__device__ __forceinline__ void step_qk_softmax(SmState<MTPW> &st, const RowSet<MTPW> &rw, const uint4 (&kr)[4][2],
+//
+// With the fp8 row set (RW::kFp8), QK runs on fp8 MFMAs straight from the K bytes
+// (the lane's 32 bytes of tile jt are exactly its A operand: dims 32kg .. 32kg+31),
+// two products per tile (hi and lo terms of the query), and the row's dequant
+// factor joins the logit scale; no K conversion.
+template <int MTPW, bool PER_TOKEN, class RW, class AfterQk>
+__device__ __forceinline__ void step_qk_softmax(SmState<MTPW> &st, const RW &rw, const uint4 (&kr)[4][2],
                                                 const f32x4 (&ksr)[4], const f32x4 (&vsr)[4], float k_fac, int t0,
                                                 int kg, bf16x8 (&pop)[MTPW][2], AfterQk &&after_qk) {
     const int trow = t0 + 16 * kg;  // token of (tile jt, i) = trow + 4jt + i
@@ -234,28 +310,47 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW> &st, const RowSet<
     f32x4 sc[MTPW][4];
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
-        const bf16x8 a0 = fp8x8_to_bf16x8(kr[jt][0].x, kr[jt][0].y);
-        const bf16x8 a1 = fp8x8_to_bf16x8(kr[jt][0].z, kr[jt][0].w);
-        const bf16x8 a2 = fp8x8_to_bf16x8(kr[jt][1].x, kr[jt][1].y);
-        const bf16x8 a3 = fp8x8_to_bf16x8(kr[jt][1].z, kr[jt][1].w);
+        if constexpr (RW::kFp8) {
+            const i32x8 a = {(int)kr[jt][0].x, (int)kr[jt][0].y, (int)kr[jt][0].z, (int)kr[jt][0].w,
+                             (int)kr[jt][1].x, (int)kr[jt][1].y, (int)kr[jt][1].z, (int)kr[jt][1].w};
 #pragma unroll
-        for (int mg = 0; mg < MTPW; ++mg) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            acc = mfma_bf16(a0, rw.qop[mg][0], acc);
-            acc = mfma_bf16(a1, rw.qop[mg][1], acc);
-            acc = mfma_bf16(a2, rw.qop[mg][2], acc);
-            acc = mfma_bf16(a3, rw.qop[mg][3], acc);
-            sc[mg][jt] = acc;
+            for (int mg = 0; mg < MTPW; ++mg) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                acc = mfma_fp8_k128(a, rw.qh[mg], acc);
+                acc = mfma_fp8_k128(a, rw.ql[mg], acc);
+                sc[mg][jt] = acc;
+            }
+        } else {
+            const bf16x8 a0 = fp8x8_to_bf16x8(kr[jt][0].x, kr[jt][0].y);
+            const bf16x8 a1 = fp8x8_to_bf16x8(kr[jt][0].z, kr[jt][0].w);
+            const bf16x8 a2 = fp8x8_to_bf16x8(kr[jt][1].x, kr[jt][1].y);
+            const bf16x8 a3 = fp8x8_to_bf16x8(kr[jt][1].z, kr[jt][1].w);
+#pragma unroll
+            for (int mg = 0; mg < MTPW; ++mg) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                acc = mfma_bf16(a0, rw.qop[mg][0], acc);
+                acc = mfma_bf16(a1, rw.qop[mg][1], acc);
+                acc = mfma_bf16(a2, rw.qop[mg][2], acc);
+                acc = mfma_bf16(a3, rw.qop[mg][3], acc);
+                sc[mg][jt] = acc;
+            }
         }
     }
     after_qk();
 
     f32x4 kf[4];
+    if constexpr (!RW::kFp8) {
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr[jt] * k_fac : f32x4{k_fac, k_fac, k_fac, k_fac};
+        for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr[jt] * k_fac : f32x4{k_fac, k_fac, k_fac, k_fac};
+    }
 
 #pragma unroll
     for (int mg = 0; mg < MTPW; ++mg) {
+        if constexpr (RW::kFp8) {
+            const float kq = k_fac * rw.dq[mg];
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr[jt] * kq : f32x4{kq, kq, kq, kq};
+        }
         float mx = -INFINITY;
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
@@ -382,7 +477,7 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
         return;
     }
     RowSet<MTPW> rw;
-    setup_rows<MTPW>(rw, p, b, h, ctx, tok_lo, tok_hi, rs * MTPW, l16, kg);
+    setup_rows(rw, p, b, h, ctx, tok_lo, tok_hi, rs * MTPW, l16, kg);
     const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
     const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
     SmState<MTPW> st;
@@ -734,8 +829,8 @@ __device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const
         emit_empty(p, NW * 64, sink);
         return;
     }
-    RowSet<MTPW> rw;
-    setup_rows<MTPW>(rw, p, b, h, ctx, tok_lo, tok_hi, wave * MTPW, l16, kg);
+    RowSetF8<MTPW> rw;
+    setup_rows(rw, p, b, h, ctx, tok_lo, tok_hi, wave * MTPW, l16, kg);
     const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
     const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
     SmState<MTPW> st;
@@ -789,7 +884,7 @@ __device__ __forceinline__ void attend(const DecodeParams &p, int b, int h, int 
 }
 
 template <int MTPW, int RS, int NS, bool PER_TOKEN>
-__global__ __launch_bounds__((kThreads<RS, NS>), kWavesPerSimd<MTPW>) void pa_decode_partition_kernel(const DecodeParams p) {
+__global__ __launch_bounds__((kThreads<RS, NS>), (kWavesFor<MTPW, NS>)) void pa_decode_partition_kernel(const DecodeParams p) {
     const int b = blockIdx.x;
     const int h = blockIdx.y;
     const int z = blockIdx.z;
@@ -869,7 +964,7 @@ struct WorkSink {
 // range-checked, so a malformed or overflowed worklist skips work instead of
 // touching memory outside the tensors.
 template <int MTPW, int RS, int NS, bool PER_TOKEN>
-__global__ __launch_bounds__((kThreads<RS, NS>), kWavesPerSimd<MTPW>) void pa_decode_worklist_kernel(const WorklistParams w) {
+__global__ __launch_bounds__((kThreads<RS, NS>), (kWavesFor<MTPW, NS>)) void pa_decode_worklist_kernel(const WorklistParams w) {
     const DecodeParams &p = w.kv;
     const int c = blockIdx.x;
     const int wbeg = max(__builtin_amdgcn_readfirstlane(w.work_indptr[c]), 0);
@@ -995,6 +1090,100 @@ __global__ __launch_bounds__(256) void pa_reduce_v1_kernel(const ReduceV1Params 
         *reinterpret_cast<uint32_t *>(reinterpret_cast<uint16_t *>(p.out) + off) = pk;
     }
     if (p.final_lse != nullptr && lane == 0)
+        p.final_lse[orow * p.s_lse_row + hd * p.s_lse_head] = wl > 0.f ? Ms + __logf(wl) : -INFINITY;
+}
+
+// The same merge with 16-byte accesses: one workgroup per (reduce group, query
+// row, 8 heads), thread t owning dims 4*(t%32) .. +3 of head 8*blockIdx.z + t/32.
+// The partial rows of a group are a uniform list (scalar loads); each thread then
+// issues its log-sum-exp loads and row loads together, so a group costs two
+// dependent memory round trips.  Partials are merged kRedBatch at a time when a
+// group has more.
+constexpr int kRedBatch = 8;
+
+__global__ __launch_bounds__(256) void pa_reduce_v1_rows_kernel(const ReduceV1Params p) {
+    const int grp = blockIdx.x, qi = blockIdx.y;
+    const int hd = blockIdx.z * 8 + (threadIdx.x >> 5);
+    const int d0 = (threadIdx.x & 31) * 4;
+    const int j0 = max(p.reduce_indptr[grp], 0);
+    const int j1 = min(p.reduce_indptr[grp + 1], p.partial_map_len);
+    if (j0 >= j1 || qi >= p.max_qlen || hd >= p.num_heads) return;
+    const int qo_start = p.final_map[2 * grp];
+    const int qo_end = p.final_map[2 * grp + 1];
+    if (qi >= qo_end - qo_start || qo_start < 0 || qo_start + qi >= p.output_rows) return;
+    const int np = j1 - j0;
+
+    // first batch of rows and every log-sum-exp, issued before any is used
+    float lse[kRedBatch];
+    float4 v[kRedBatch];
+    int rr[kRedBatch];
+#pragma unroll
+    for (int j = 0; j < kRedBatch; ++j) {
+        const int r = j < np ? p.partial_map[j0 + j] + qi : -1;
+        rr[j] = (r >= 0 && r < p.partial_rows) ? r : -1;
+        lse[j] = rr[j] >= 0 ? p.pl[rr[j] * p.s_pl_row + hd * p.s_pl_head] : -INFINITY;
+        v[j] = rr[j] >= 0 ? *reinterpret_cast<const float4 *>(p.po + rr[j] * p.s_po_row + hd * p.s_po_head + d0)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kRedBatch; ++j) mloc = fmaxf(mloc, lse[j]);
+    for (int j = kRedBatch; j < np; ++j) {
+        const int r = p.partial_map[j0 + j] + qi;
+        if (r >= 0 && r < p.partial_rows) mloc = fmaxf(mloc, p.pl[r * p.s_pl_row + hd * p.s_pl_head]);
+    }
+    const float Ms = mloc == -INFINITY ? 0.0f : mloc;
+    float wl = 0.f;
+#pragma unroll
+    for (int j = 0; j < kRedBatch; ++j) {
+        lse[j] = rr[j] >= 0 ? fast_exp2((lse[j] - Ms) * kLog2e) : 0.f;  // now the weight
+        wl += lse[j];
+    }
+    for (int j = kRedBatch; j < np; ++j) {
+        const int r = p.partial_map[j0 + j] + qi;
+        if (r >= 0 && r < p.partial_rows) wl += fast_exp2((p.pl[r * p.s_pl_row + hd * p.s_pl_head] - Ms) * kLog2e);
+    }
+    const float inv = wl > 0.f ? 1.0f / wl : 0.0f;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < kRedBatch; ++j) {
+        const float w = lse[j] * inv;
+        a.x += w * v[j].x;
+        a.y += w * v[j].y;
+        a.z += w * v[j].z;
+        a.w += w * v[j].w;
+    }
+    for (int jb = kRedBatch; jb < np; jb += kRedBatch) {
+#pragma unroll
+        for (int j = 0; j < kRedBatch; ++j) {
+            const int r = jb + j < np ? p.partial_map[j0 + jb + j] + qi : -1;
+            rr[j] = (r >= 0 && r < p.partial_rows) ? r : -1;
+            lse[j] = rr[j] >= 0 ? p.pl[rr[j] * p.s_pl_row + hd * p.s_pl_head] : -INFINITY;
+            v[j] = rr[j] >= 0 ? *reinterpret_cast<const float4 *>(p.po + rr[j] * p.s_po_row + hd * p.s_po_head + d0)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < kRedBatch; ++j) {
+            const float w = rr[j] >= 0 ? fast_exp2((lse[j] - Ms) * kLog2e) * inv : 0.f;
+            a.x += w * v[j].x;
+            a.y += w * v[j].y;
+            a.z += w * v[j].z;
+            a.w += w * v[j].w;
+        }
+    }
+    const int64_t orow = qo_start + qi;
+    const int64_t off = orow * p.s_out_row + hd * p.s_out_head + d0;
+    if (p.out_dtype == PA_FP8_F32) {
+        *reinterpret_cast<float4 *>(reinterpret_cast<float *>(p.out) + off) = a;
+    } else {
+        const bool f16 = p.out_dtype == PA_FP8_F16;
+        const uint32_t lo = f16 ? uint32_t(f32_to_f16_bits(a.x)) | (uint32_t(f32_to_f16_bits(a.y)) << 16)
+                                : uint32_t(f32_to_bf16_bits(a.x)) | (uint32_t(f32_to_bf16_bits(a.y)) << 16);
+        const uint32_t hi = f16 ? uint32_t(f32_to_f16_bits(a.z)) | (uint32_t(f32_to_f16_bits(a.w)) << 16)
+                                : uint32_t(f32_to_bf16_bits(a.z)) | (uint32_t(f32_to_bf16_bits(a.w)) << 16);
+        *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.out) + off) = make_uint2(lo, hi);
+    }
+    if (p.final_lse != nullptr && d0 == 0)
         p.final_lse[orow * p.s_lse_row + hd * p.s_lse_head] = wl > 0.f ? Ms + __logf(wl) : -INFINITY;
 }
 
@@ -1418,10 +1607,20 @@ int pa_fp8_reduce_v1(const pa_fp8_reduce_v1_args *a, void *stream) {
     p.output_rows = a->output_rows;
     p.partial_map_len = a->partial_map_len;
     p.out_dtype = a->out_dtype;
-    const int64_t rows = (int64_t)a->num_heads * a->max_qlen;  // (qi, head) rows of a group, four per workgroup
-    if ((rows + 3) / 4 > 65535) return PA_FP8_ERR_SHAPE;
-    hipLaunchKernelGGL(pa_reduce_v1_kernel, dim3(a->num_groups, (rows + 3) / 4), dim3(256), 0,
-                       reinterpret_cast<hipStream_t>(stream), p);
+    // 16-byte path: 16-byte aligned partial rows and heads, 4-element aligned output heads
+    const bool vec = (reinterpret_cast<uintptr_t>(a->partial_output) & 15) == 0 &&
+                     ((a->stride_po_row | a->stride_po_head) & 3) == 0 &&
+                     (reinterpret_cast<uintptr_t>(a->output) & (4 * esz - 1)) == 0 &&
+                     ((a->stride_out_row | a->stride_out_head) & 3) == 0;
+    if (vec) {
+        hipLaunchKernelGGL(pa_reduce_v1_rows_kernel, dim3(a->num_groups, a->max_qlen, (a->num_heads + 7) / 8), dim3(256),
+                           0, reinterpret_cast<hipStream_t>(stream), p);
+    } else {
+        const int64_t rows = (int64_t)a->num_heads * a->max_qlen;  // (qi, head) rows of a group, four per workgroup
+        if ((rows + 3) / 4 > 65535) return PA_FP8_ERR_SHAPE;
+        hipLaunchKernelGGL(pa_reduce_v1_kernel, dim3(a->num_groups, (rows + 3) / 4), dim3(256), 0,
+                           reinterpret_cast<hipStream_t>(stream), p);
+    }
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
 }

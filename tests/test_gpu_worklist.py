@@ -141,14 +141,18 @@ def test_plan_cache_does_not_reuse_internal_metadata():
     compare_outputs(w, out2, range(cfg.batch))
 
 
+@pytest.mark.parametrize("hq", [8, 12])
+@pytest.mark.parametrize("aligned", [True, False], ids=["vec16", "offset8"])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
-def test_pa_reduce_v1_api(out_dtype):
-    """The reduce on synthetic partials vs the oracle merge, with final_lse."""
+def test_pa_reduce_v1_api(out_dtype, aligned, hq):
+    """The reduce on synthetic partials vs the oracle merge, with final_lse.  Groups
+    of 0-19 partials (more than one batch of eight), head counts that are and are
+    not multiples of 8, and partial rows offset by 8 bytes (the element-pair path)."""
     from flydsl_amd import pa_reduce_v1
 
     rng = np.random.default_rng(3)
-    hq, ql, groups = 8, 2, 5
-    counts = [0, 3, 1, 7, 2]  # partials per group (0: a group with nothing to merge)
+    ql, groups = 2, 6
+    counts = [0, 3, 1, 7, 2, 19]  # partials per group (0: a group with nothing to merge)
     nparts = sum(counts)
     rows = nparts * ql + 3
     po = rng.standard_normal((rows, 1, hq, 128)).astype(np.float32)
@@ -161,7 +165,13 @@ def test_pa_reduce_v1_api(out_dtype):
     out = torch.full((groups * ql, hq, 128), 7.0, dtype=out_dtype, device=dev)
     lse = torch.full((groups * ql, hq), 7.0, device=dev)
     t = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
-    pa_reduce_v1(t(po), t(pl), t(ri), t(rfm), t(rpm), ql, out, lse)
+    po_t = t(po)
+    if not aligned:  # same values, data pointer 8 bytes past a 16-byte boundary
+        buf = torch.empty(po.size + 2, dtype=torch.float32, device=dev)
+        po_t = buf[2:].view(po.shape)
+        po_t.copy_(t(po))
+        assert po_t.data_ptr() % 16 == 8
+    pa_reduce_v1(po_t, t(pl), t(ri), t(rfm), t(rpm), ql, out, lse)
     torch.cuda.synchronize()
     exp = np.full((groups * ql, hq, 128), 7.0)
     exp_lse = oatt.reduce_v1(po[:, 0], pl[:, 0, :, 0], ri, rfm, rpm, ql, exp)
