@@ -858,11 +858,12 @@ __device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const
                 vsr[q4] = *reinterpret_cast<const f32x4 *>(sk + kStageS + 256 + kg * 64 + 16 * q4);
             }
         }
-        bf16x8 pop[MTPW][2];
-        step_qk_softmax<MTPW, PER_TOKEN>(st, rw, kr, ksr, vsr, k_fac, tok_lo + n * kStep, kg, pop, [] {});
+        // V is read with K, so its LDS latency hides under the QK products and softmax
 #pragma unroll
         for (int m = 0; m < 8; ++m)
             vr[m] = *reinterpret_cast<const uint4 *>(sk + kStageV + kg * 2048 + (16 * m + l16) * 16);
+        bf16x8 pop[MTPW][2];
+        step_qk_softmax<MTPW, PER_TOKEN>(st, rw, kr, ksr, vsr, k_fac, tok_lo + n * kStep, kg, pop, [] {});
         step_pv<MTPW>(st, vr, pop);
     }
     finish_rows<MTPW>(st, p, wave * MTPW, l16, kg, v_fac, sink);
