@@ -1,8 +1,10 @@
 // get_pa_metadata_v1 worklist scheduler on the device (kernels/pa_metadata.py:145-420).
 //
-// The schedule is a serial state machine over (CU bin, batch) pairs, so one
-// thread runs it (O(num_cu + batch) steps per kv head, reading LDS); it keeps
-// the caller free of a device->host copy of context_lens.  Buffers are written
+// The reference runs the schedule as a serial state machine over (CU bin, batch)
+// pairs.  Here a parallel kernel computes the same output in closed form for the
+// common case (pa_metadata_par_kernel) and the serial machine runs only where it
+// cannot (pa_metadata_v1_kernel); both keep the caller free of a device->host copy
+// of context_lens.  Buffers are written
 // exactly where the reference writes them, including its overwrite-safe
 // unconditional stores; only the valid prefixes are defined.  Every store is
 // bounds-checked against the buffer sizes the host passes; a schedule that
@@ -20,6 +22,8 @@ struct MetaParams {
     int32_t *reduce_indptr;
     int32_t *reduce_final_map;
     int32_t *reduce_partial_map;
+    int32_t *partition_indptr;  // optional outputs
+    int32_t *uniform_context;
     int32_t nb, gqa, nhk, num_cu, kv_gran, ql, max_work, max_split_tiles;
 };
 
@@ -31,6 +35,222 @@ constexpr int kStagedIndptr = 4097;    // work_indptr entries kept in LDS (num_c
 constexpr int kStagedReduce = 2048;    // batches whose reduce maps are kept in LDS
 constexpr int kStagedSplits = 4096;    // reduce_partial_map entries kept in LDS
 
+constexpr int kParThreads = 1024;
+constexpr int kParBatches = 4 * kParThreads;         // batches the parallel scheduler handles
+constexpr int32_t kSerialSentinel = INT32_MIN + 7;   // work_indptr[0]: "the serial scheduler runs"
+
+// Exclusive prefix of one value per thread over the 1024 threads; *total gets the sum.
+template <class T>
+__device__ __forceinline__ T block_scan_excl(T v, T *s_wave, T &total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    T x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const T y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) s_wave[wave] = x;
+    __syncthreads();
+    T before = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kParThreads / 64; ++w) {
+        const T t = s_wave[w];
+        before += w < wave ? t : T(0);
+        tot += t;
+    }
+    __syncthreads();  // s_wave is reused by the next scan
+    total = tot;
+    return before + x - v;
+}
+
+// The state machine's output in closed form, computed in parallel.  With
+// S = sum of partitions, avg = S / nspk, rem = S % nspk, bin c of a head takes the
+// global partitions [Qs(c), Qs(c+1)), Qs(c) = c*avg + min(c, rem); batch b holds
+// [P(b), P(b+1)).  The works of a batch are its non-empty intersections with the
+// bins, in bin order (an empty batch makes one empty work in the bin of the
+// partition before it, bin 0 if none); a batch with more than one work is split,
+// its works take consecutive partial rows and it forms the next reduce group.
+// When every bin has a partition (avg >= 1) or a head has one bin, head 0 ends in
+// its last bin and every head repeats its schedule nspk bins later, as in the
+// serial machine.  Otherwise (or with more than kParBatches batches, or more than
+// 2^31 partitions) it leaves kSerialSentinel in work_indptr[0] for the serial
+// kernel launched after it.
+__global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const MetaParams p) {
+    __shared__ int32_t s_P[kParBatches + 1];  // partitions before batch b
+    __shared__ int32_t s_W[kParBatches + 1];  // works of head 0 before batch b
+    __shared__ int32_t s_L[kParBatches + 1];  // works of split batches before batch b
+    __shared__ int32_t s_G[kParBatches + 1];  // split batches before batch b
+    __shared__ long long s_w64[kParThreads / 64];
+    __shared__ int32_t s_w32[kParThreads / 64];
+    __shared__ int32_t s_mm[2 * (kParThreads / 64)];
+    const int t = threadIdx.x;
+    const int nspk = p.num_cu / p.nhk;
+    // partitions per batch and their prefix (four consecutive batches per thread,
+    // chunks of kParBatches), the optional partition_indptr and uniform_context
+    int np4[4];
+    long long S64 = 0, run = 0;
+    int cmin = INT32_MAX, cmax = INT32_MIN;
+    for (int base = 0; base < max(p.nb, 1); base += kParBatches) {
+        long long loc = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int b = base + 4 * t + i;
+            const int c = b < p.nb ? p.ctx[b] : 0;
+            if (b < p.nb) {
+                cmin = min(cmin, c);
+                cmax = max(cmax, c);
+            }
+            np4[i] = b < p.nb ? cdiv_u(c, p.kv_gran) : 0;
+            loc += np4[i];
+        }
+        long long total;
+        run = S64 + block_scan_excl<long long>(loc, s_w64, total);
+        if (p.partition_indptr) {
+            long long r = run;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int b = base + 4 * t + i;
+                if (b < p.nb) p.partition_indptr[b] = (int)r;
+                r += np4[i];
+            }
+        }
+        S64 += total;
+    }
+    if (p.partition_indptr && t == 0) p.partition_indptr[p.nb] = (int)S64;
+    if (p.uniform_context) {
+#pragma unroll
+        for (int sh = 32; sh >= 1; sh >>= 1) {
+            cmin = min(cmin, __shfl_xor(cmin, sh, 64));
+            cmax = max(cmax, __shfl_xor(cmax, sh, 64));
+        }
+        if ((t & 63) == 0) {
+            s_mm[2 * (t >> 6)] = cmin;
+            s_mm[2 * (t >> 6) + 1] = cmax;
+        }
+        __syncthreads();
+        if (t == 0) {
+            int a = INT32_MAX, z = INT32_MIN;
+            for (int w = 0; w < kParThreads / 64; ++w) {
+                a = min(a, s_mm[2 * w]);
+                z = max(z, s_mm[2 * w + 1]);
+            }
+            p.uniform_context[0] = (p.nb == 0 || a == z) ? 1 : 0;
+        }
+    }
+    const bool ok = p.nb <= kParBatches && S64 <= 0x7fffffffLL && (S64 >= nspk || nspk == 1);
+    if (!ok) {  // uniform
+        if (t == 0) p.work_indptr[0] = kSerialSentinel;
+        return;
+    }
+    // one chunk (nb <= kParBatches): run and np4 are this thread's prefix and counts
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int b = 4 * t + i;
+        if (b <= p.nb) s_P[b] = (int)run;
+        run += np4[i];
+    }
+    if (t == 0) s_P[p.nb] = (int)S64;  // batch nb is past every thread's four when nb == kParBatches
+    __syncthreads();
+    const int S = (int)S64;
+    const int avg = S / nspk, rem = S % nspk;
+    const int big = rem * (avg + 1);
+    auto bin_of = [&](int x) { return nspk == 1 ? 0 : (x < big ? x / (avg + 1) : rem + (x - big) / avg); };
+    auto Qs = [&](int c) { return c * avg + min(c, rem); };
+    auto first_bin = [&](int b) {
+        const int pb = s_P[b], pe = s_P[b + 1];
+        return pe > pb ? bin_of(pb) : (pb == 0 ? 0 : bin_of(pb - 1));
+    };
+    auto works_of = [&](int b) {
+        const int pb = s_P[b], pe = s_P[b + 1];
+        return pe > pb ? bin_of(pe - 1) - bin_of(pb) + 1 : 1;
+    };
+    // works, split works and split batches before each batch
+    int w4[4], l4[4], g4[4];
+    int wl = 0, ll = 0, gl = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int b = 4 * t + i;
+        const int nw = b < p.nb ? works_of(b) : 0;
+        w4[i] = nw;
+        l4[i] = nw > 1 ? nw : 0;
+        g4[i] = nw > 1 ? 1 : 0;
+        wl += w4[i];
+        ll += l4[i];
+        gl += g4[i];
+    }
+    int W, Lt, G;
+    int wr = block_scan_excl<int>(wl, s_w32, W);
+    int lr = block_scan_excl<int>(ll, s_w32, Lt);
+    int gr = block_scan_excl<int>(gl, s_w32, G);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int b = 4 * t + i;
+        if (b <= p.nb) {
+            s_W[b] = wr;
+            s_L[b] = lr;
+            s_G[b] = gr;
+        }
+        wr += w4[i];
+        lr += l4[i];
+        gr += g4[i];
+    }
+    __syncthreads();
+    const bool overflow = (long long)p.nhk * W > p.max_work || Lt > p.max_split_tiles;
+
+    // work_info rows of every head
+    for (int b = t; b < p.nb; b += kParThreads) {
+        const int pb = s_P[b], pe = s_P[b + 1];
+        const int c0 = first_bin(b), nw = works_of(b);
+        const int wb = s_W[b], lb = s_L[b];
+        const int qs = p.sq[b], qe = p.sq[b + 1];
+        for (int j = 0; j < nw; ++j) {
+            const int c = c0 + j;
+            const int ks = pe > pb ? max(pb, Qs(c)) : pb;
+            const int ke = pe > pb ? min(pe, Qs(c + 1)) : pb;
+            const int ploc = nw > 1 ? p.ql * (lb + j) : -1;
+            for (int k = 0; k < p.nhk; ++k) {
+                const long long row = (long long)k * W + wb + j;
+                if (row >= p.max_work) continue;
+                const int32_t qhr = (int32_t)((((unsigned)(k + 1) * (unsigned)p.gqa) << 16) |
+                                              (((unsigned)k * (unsigned)p.gqa) & 0xFFFFu));
+                int4 *w = reinterpret_cast<int4 *>(p.work_info) + 2 * row;
+                w[0] = make_int4(b, ploc, qs, qe);
+                w[1] = make_int4(ks, ke, 0, qhr);
+            }
+        }
+    }
+    // work_indptr: entry k*nspk + c + 1 = k*W + works of head 0 in bins <= c
+    for (int c = t; c < nspk; c += kParThreads) {
+        int v = 0;
+        if (p.nb > 0) {
+            int lo = 0, hi = p.nb - 1;  // last batch whose first bin is <= c (batch 0's is 0)
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (first_bin(mid) <= c) lo = mid;
+                else hi = mid - 1;
+            }
+            v = s_W[lo] + min(c - first_bin(lo) + 1, works_of(lo));
+        }
+        for (int k = 0; k < p.nhk; ++k) p.work_indptr[k * nspk + c + 1] = k * W + v;
+    }
+    // reduce maps (the same for every head)
+    for (int b = t; b < p.nb; b += kParThreads) {
+        const int nw = works_of(b);
+        if (nw < 2) continue;
+        const int g = s_G[b], lb = s_L[b];
+        p.reduce_indptr[g + 1] = lb + nw;
+        p.reduce_final_map[2 * g] = p.sq[b];
+        p.reduce_final_map[2 * g + 1] = p.sq[b + 1];
+        for (int j = 0; j < nw; ++j)
+            if (lb + j < p.max_split_tiles) p.reduce_partial_map[lb + j] = p.ql * (lb + j);
+    }
+    for (int i = G + t; i <= p.nb; i += kParThreads) p.reduce_indptr[i] = Lt;
+    if (t == 0) {
+        if (G > 0) p.reduce_indptr[0] = 0;
+        p.work_indptr[0] = overflow ? -1 : 0;
+    }
+}
+
 // Every lane runs the same serial state machine on the same (uniform) values.
 // Its outputs go to LDS -- a ring of work_info rows, work_indptr and the reduce
 // maps -- and the 64 lanes copy them to global memory with coalesced stores, so
@@ -39,6 +259,7 @@ constexpr int kStagedSplits = 4096;    // reduce_partial_map entries kept in LDS
 // lanes).  Buffers larger than the LDS copies are written to global memory
 // directly by lane 0.
 __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaParams p) {
+    if (p.work_indptr[0] != kSerialSentinel) return;  // the parallel scheduler wrote the schedule
     __shared__ int32_t s_np[kStagedBatches];
     __shared__ int32_t s_sq[kStagedBatches + 1];
     __shared__ __attribute__((aligned(16))) int32_t s_ring[kRingRows * 8];
@@ -256,7 +477,13 @@ extern "C" int pa_fp8_metadata_v1(const pa_fp8_metadata_args *a, void *stream) {
     p.ql = a->query_length;
     p.max_work = a->max_work;
     p.max_split_tiles = a->max_split_tiles;
-    hipLaunchKernelGGL(pa_metadata_v1_kernel, dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), p);
-    const hipError_t err = hipGetLastError();
+    p.partition_indptr = a->partition_indptr;
+    p.uniform_context = a->uniform_context;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(pa_metadata_par_kernel, dim3(1), dim3(kParThreads), 0, s, p);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return PA_FP8_ERR_HIP + (int)err;
+    hipLaunchKernelGGL(pa_metadata_v1_kernel, dim3(1), dim3(64), 0, s, p);
+    err = hipGetLastError();
     return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
 }

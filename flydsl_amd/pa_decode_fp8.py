@@ -702,6 +702,22 @@ def _build_plan(
                              exp_sums, max_logits, temporary_output, is_graph_capturing, path, tag)
 
 
+_SEQLENS_CACHE: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+
+
+def _seqlens_qo_indptr(dev: torch.device, batch_size: int, query_length: int, graph_safe: bool) -> torch.Tensor:
+    """arange(B + 1) * ql on the device, cached per shape outside graph capture."""
+    key = (dev, batch_size, query_length)
+    t = _SEQLENS_CACHE.get(key)
+    if t is None:
+        t = torch.arange(batch_size + 1, dtype=torch.int32, device=dev) * query_length
+        if not graph_safe:
+            _SEQLENS_CACHE[key] = t
+            if len(_SEQLENS_CACHE) > 32:
+                _SEQLENS_CACHE.popitem(last=False)
+    return t
+
+
 def get_pa_metadata(
     query: torch.Tensor,
     key_cache: torch.Tensor,
@@ -736,44 +752,53 @@ def get_pa_metadata(
     head_size = query.shape[-1]
     num_sm = _device_cu_count(dev) * _PA_METADATA_GRID_OVERSUB
     num_sm = (num_sm // num_kv_heads) * num_kv_heads
-    seqlens_qo_indptr = torch.arange(batch_size + 1, dtype=torch.int32, device=dev) * query_length
-    parts = (context_lengths.to(torch.int32) + (partition_size - 1)) // partition_size
-    partition_indptr = torch.zeros(batch_size + 1, dtype=torch.int32, device=dev)
-    partition_indptr[1:] = torch.cumsum(parts, dim=0).to(torch.int32)
-    block_size = key_cache.shape[-2]
+    if num_sm <= 0 or partition_size <= 0 or partition_size & (partition_size - 1):
+        raise ValueError("get_pa_metadata needs num_kv_heads <= 2 * CUs and a power-of-two partition_size")
+    seqlens_qo_indptr = _seqlens_qo_indptr(dev, batch_size, query_length, graph_safe)
+    ctx = context_lengths if context_lengths.dtype == torch.int32 else context_lengths.to(torch.int32)
+    ctx = ctx.contiguous()
     infos = get_pa_metadata_info_v1(batch_size, num_kv_heads, num_cu=num_sm)
-    bufs = [torch.empty(shape, dtype=dtype, device=dev) for shape, dtype in infos]
-    work_metadata_ptrs, work_indptr, work_info, reduce_indptr, reduce_final_map, reduce_partial_map = bufs
-    get_pa_metadata_v1(
-        seqlens_qo_indptr,
-        kv_indptr,
-        context_lengths,
-        num_query_heads // num_kv_heads,
-        num_kv_heads,
-        True,
-        work_metadata_ptrs,
-        work_indptr,
-        work_info,
-        reduce_indptr,
-        reduce_final_map,
-        reduce_partial_map,
-        kv_granularity=partition_size,
-        block_size=block_size,
-        max_seqlen_qo=query_length,
-        uni_seqlen_qo=query_length,
-        fast_mode=True,
-        max_split_per_batch=-1,
-        num_cu=num_sm,
-    )
-    work_info_flat = work_info.reshape(-1).contiguous()
+    # every int32 output in one allocation; uniform_context sits right after
+    # reduce_indptr so that one two-int read returns it with the partial count
+    sizes = [int(torch.Size(shape).numel()) for shape, _ in infos[1:]]  # work_indptr .. reduce_partial_map
+    sizes[2] += 1  # reduce_indptr + uniform_context
+    sizes.append(batch_size + 1)  # partition_indptr
+    offs = [0]
+    for n in sizes:
+        offs.append(offs[-1] + (n + 3) // 4 * 4)  # 16-byte aligned pieces
+    buf = torch.empty(offs[-1], dtype=torch.int32, device=dev)
+    work_indptr = buf[offs[0] : offs[0] + sizes[0]]
+    work_info_flat = buf[offs[1] : offs[1] + sizes[1]]
+    reduce_indptr = buf[offs[2] : offs[2] + batch_size + 1]
+    reduce_final_map = buf[offs[3] : offs[3] + sizes[3]].view(batch_size, 2)
+    reduce_partial_map = buf[offs[4] : offs[4] + sizes[4]]
+    partition_indptr = buf[offs[5] : offs[5] + sizes[5]]
+    a = _lib.MetadataArgs()
+    a.seqlens_qo_indptr = seqlens_qo_indptr.data_ptr()
+    a.context_lens = ctx.data_ptr()
+    a.work_indptr = work_indptr.data_ptr()
+    a.work_info = work_info_flat.data_ptr()
+    a.reduce_indptr = reduce_indptr.data_ptr()
+    a.reduce_final_map = reduce_final_map.data_ptr()
+    a.reduce_partial_map = reduce_partial_map.data_ptr()
+    a.partition_indptr = partition_indptr.data_ptr()
+    a.uniform_context = buf[offs[2] + batch_size + 1 :].data_ptr()
+    a.num_batches = batch_size
+    a.gqa = num_query_heads // num_kv_heads
+    a.num_heads_k = num_kv_heads
+    a.num_cu = num_sm
+    a.kv_granularity = partition_size
+    a.query_length = query_length
+    a.max_work = sizes[1] // 8
+    a.max_split_tiles = sizes[4]
+    _lib.metadata_v1(a, torch.cuda.current_stream(dev).cuda_stream)
     if graph_safe:
         # no host read: room for every partial the schedule can emit
         num_partials, uniform = reduce_partial_map.numel(), False
     else:
         # one host read (the reference reads reduce_indptr[-1] here too): the partial
         # count, and whether every sequence has the same context length
-        ctx_i32 = context_lengths.to(torch.int32)
-        host = torch.stack([reduce_indptr[-1], (ctx_i32.max() == ctx_i32.min()).to(torch.int32)]).cpu()
+        host = buf[offs[2] + batch_size : offs[2] + batch_size + 2].cpu()
         num_partials, uniform = int(host[0]), bool(host[1])
     partial_output = torch.empty(
         ((num_partials + 1) * query_length, 1, num_query_heads, head_size), dtype=torch.float32, device=dev

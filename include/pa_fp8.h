@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define PA_FP8_ABI_VERSION 4
+#define PA_FP8_ABI_VERSION 5
 
 enum pa_fp8_status {
     PA_FP8_OK = 0,
@@ -241,12 +241,16 @@ typedef struct pa_fp8_reduce_v1_args {
 int pa_fp8_reduce_v1(const pa_fp8_reduce_v1_args *args, void *hip_stream);
 
 /*
- * get_pa_metadata_v1 worklist scheduler, run on the device by one thread
- * (the reference also runs it serially on one wave).  Writes work_indptr
+ * get_pa_metadata_v1 worklist scheduler on the device (the reference runs its
+ * state machine serially on one wave; here a parallel closed form covers the
+ * common case and the serial machine the rest).  Writes work_indptr
  * [num_cu+1], work_info [max_work, 8], reduce_indptr [B+1],
  * reduce_final_map [B, 2], reduce_partial_map [max_split_tiles]; only the
  * valid prefixes are defined.  kv_granularity must be a power of two and
- * num_cu a multiple of num_heads_k.
+ * num_cu a multiple of num_heads_k.  Optional outputs (NULL: not written):
+ * partition_indptr [B+1], the exclusive prefix of ceil(context_len /
+ * kv_granularity), and uniform_context [1], 1 when every context length is
+ * equal (get_pa_metadata's two derived values, so it needs no other launches).
  *
  * Replaces the launcher of `compile_pa_metadata_v1` (kernels/pa_metadata.py:422-447,
  * called from get_pa_metadata_v1 at :515-524).
@@ -267,6 +271,8 @@ typedef struct pa_fp8_metadata_args {
     int32_t query_length;
     int32_t max_work;
     int32_t max_split_tiles;
+    int32_t *partition_indptr;
+    int32_t *uniform_context;
 } pa_fp8_metadata_args;
 
 int pa_fp8_metadata_v1(const pa_fp8_metadata_args *args, void *hip_stream);

@@ -92,3 +92,86 @@ def test_device_scheduler_ring_wrap_and_large_bin_counts(b, nhk, num_cu):
     got, ref = run_device(ctx, 1, 4, nhk, num_cu, 256)
     for key, val in op.metadata_valid_prefixes(ref).items():
         np.testing.assert_array_equal(op.metadata_valid_prefixes(got)[key], val, err_msg=key)
+
+
+@pytest.mark.parametrize(
+    "case",
+    [
+        "empty_batches",  # zero-length contexts between others (closed-form path)
+        "few_partitions",  # fewer partitions than bins per head (serial path)
+        "one_bin_per_head",  # nspk == 1 (closed-form path, any partition count)
+        "all_empty_one_bin",  # every context 0 with one bin per head (closed-form path)
+        "all_empty",  # every context 0, several bins (serial path)
+        "max_parallel_batches",  # 4096 batches (closed-form path)
+        "serial_batches",  # 4097 batches (serial path)
+    ],
+)
+def test_device_scheduler_closed_form_and_serial_paths(case):
+    """The parallel closed-form scheduler and the serial state machine it falls back
+    to, on the shapes that select each one, bit-exact with the oracle."""
+    rng = np.random.default_rng(sum(map(ord, case)))
+    ql, gqa, gran = 2, 4, 256
+    if case == "empty_batches":
+        ctx = [int(x) if rng.random() < 0.7 else 0 for x in rng.integers(1, 4000, size=60)]
+        nhk, num_cu = 4, 64
+    elif case == "few_partitions":
+        ctx = [int(x) for x in rng.integers(1, 300, size=5)]
+        nhk, num_cu = 2, 64
+    elif case == "one_bin_per_head":
+        ctx = [int(x) for x in rng.integers(0, 3000, size=37)]
+        nhk, num_cu = 8, 8
+    elif case == "all_empty_one_bin":
+        ctx = [0] * 9
+        nhk, num_cu = 4, 4
+    elif case == "all_empty":
+        ctx = [0] * 9
+        nhk, num_cu = 4, 32
+    elif case == "max_parallel_batches":
+        ctx = [int(x) for x in rng.integers(0, 2000, size=4096)]
+        nhk, num_cu = 8, 512
+    else:
+        ctx = [int(x) for x in rng.integers(0, 2000, size=4097)]
+        nhk, num_cu = 8, 512
+    got, ref = run_device(ctx, ql, gqa, nhk, num_cu, gran)
+    for key, val in op.metadata_valid_prefixes(ref).items():
+        np.testing.assert_array_equal(op.metadata_valid_prefixes(got)[key], val, err_msg=key)
+
+
+@pytest.mark.parametrize("b,kind", [(1, "uniform"), (37, "ragged"), (37, "uniform"), (4096, "ragged"),
+                                    (9000, "ragged"), (9000, "uniform"), (9000, "last_differs")])
+def test_get_pa_metadata_partition_prefix_and_uniform_flag(b, kind):
+    """get_pa_metadata's partition_indptr (the exclusive prefix of ceil(ctx / 256),
+    computed by the scheduler kernel in chunks of 4096 batches) and its
+    uniform_context flag (every context length equal), against numpy; the
+    schedule itself against the oracle."""
+    from flydsl_amd import get_pa_metadata
+
+    rng = np.random.default_rng(b + len(kind))
+    if kind == "ragged":
+        ctx = rng.integers(1, 5000, size=b)
+    else:
+        ctx = np.full(b, 1777)
+        if kind == "last_differs":
+            ctx[-1] = 1778
+    dev = torch.device("cuda:0")
+    q = torch.zeros(b, 16, 128, dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros(1, 2, 8, 16, 16, dtype=torch.uint8, device=dev)
+    ctx_t = torch.tensor(ctx, dtype=torch.int32, device=dev)
+    kv = torch.zeros(b + 1, dtype=torch.int32, device=dev)
+    md = get_pa_metadata(q, kc, ctx_t, kv, 16, 2)
+    parts = (ctx.astype(np.int64) + 255) // 256
+    np.testing.assert_array_equal(md["partition_indptr"].cpu().numpy(), np.concatenate([[0], np.cumsum(parts)]))
+    assert md["uniform_context"] is (kind != "ragged" and kind != "last_differs")
+    ref = op.get_pa_metadata_v1(list(range(b + 1)), [int(c) for c in ctx], 8, 2, md["num_sm"], 256, 1)
+    v = op.metadata_valid_prefixes(ref)
+    np.testing.assert_array_equal(md["work_indptr"].cpu().numpy(), v["work_indptr"])
+    np.testing.assert_array_equal(md["reduce_indptr"].cpu().numpy(), v["reduce_indptr"])
+    nw = int(v["work_indptr"][-1])
+    np.testing.assert_array_equal(md["work_info_flat"].cpu().numpy()[: nw * 8].reshape(nw, 8), v["work_info"])
+    assert md["partial_output"].shape[0] == int(v["reduce_indptr"][-1]) + 1
+    # graph-safe: same schedule, no host read, partial buffers at the scheduler's bound
+    md_g = get_pa_metadata(q, kc, ctx_t, kv, 16, 2, graph_safe=True)
+    assert md_g["uniform_context"] is False
+    assert torch.equal(md_g["partition_indptr"], md["partition_indptr"])
+    assert torch.equal(md_g["work_indptr"], md["work_indptr"])
+    assert md_g["partial_output"].shape[0] == md_g["reduce_partial_map"].numel() + 1
