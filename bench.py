@@ -358,9 +358,14 @@ def main():
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
     print(f"[bench] building {cfg.name} x{args.copies}: {cfg.description}", file=sys.stderr, flush=True)
-    works = [build_workload(cfg, dev, seed=123 + i * 1000, context_lengths=None) for i in range(args.copies)]
-    # every copy shares the first copy's context lengths / block tables / query
-    base = works[0]
+    # every copy is built for the first copy's context lengths, so each cache holds
+    # exactly the pages the shared block tables index (a copy sized for other
+    # lengths would have some indices clamped to its last page by the kernel's
+    # bounds guard, and read those from L2); the copies share its block tables,
+    # page lists and query, and differ in their KV bytes and scales
+    base = build_workload(cfg, dev, seed=123, context_lengths=None)
+    works = [base] + [build_workload(cfg, dev, seed=123 + i * 1000, context_lengths=base["context_list"])
+                      for i in range(1, args.copies)]
     for w in works[1:]:
         for k in ("context_lengths", "block_tables", "query", "context_list", "block_table_np", "kv_page_indices",
                   "kv_indptr"):
