@@ -492,16 +492,21 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
     const int k_lane_off = (l16 & 3) * 16 + (2 * kg) * kchunk;
     const int v_lane_off = l16 * 16;
 
-    // lane's K group (QK row owner) is l16>>2, its V / scale group is kg
-    auto k_ptr = [&](int step) {
+    // A lane's K group (QK row owner) is l16>>2, its V / scale group is kg.  The
+    // page-table entries of a step are read one step of the wave earlier than its
+    // K / V: vector memory waits are in order, so waiting for entries read just
+    // before the step's K would also wait for the V loads still in flight.
+    auto page_of = [&](int step, int g) {
+        const int gs = min(tok_lo + step * kStep + 16 * g, last_group);
+        return bt_row[gs >> p.bs_log2];
+    };
+    auto k_ptr = [&](int step, int e) {
         const int gs = min(tok_lo + step * kStep + 16 * (l16 >> 2), last_group);
-        const int e = bt_row[gs >> p.bs_log2];
         const int phys = min(max(e, 0), p.num_blocks - 1);
         return kc_h + (int64_t)phys * p.s_k_block + ((gs & (bs - 1)) >> 4) * 256 + k_lane_off;
     };
-    auto v_loc = [&](int step, int64_t &vofs, int64_t &sofs) {
+    auto v_loc = [&](int step, int e, int64_t &vofs, int64_t &sofs) {
         const int gs = min(tok_lo + step * kStep + 16 * kg, last_group);
-        const int e = bt_row[gs >> p.bs_log2];
         const int phys = min(max(e, 0), p.num_blocks - 1);
         const int sub = (gs & (bs - 1)) >> 4;
         vofs = (int64_t)phys * p.s_v_block + sub * (D * 16) + v_lane_off;
@@ -531,22 +536,35 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
     };
 
     int step = ns;
+    int ek_next = 0, ev_next = 0;  // page-table entries of the wave's next step
     if (step < nsteps) {
+        const int ek = page_of(step, l16 >> 2), ev = page_of(step, kg);
+        if (step + NS < nsteps) {
+            ek_next = page_of(step + NS, l16 >> 2);
+            ev_next = page_of(step + NS, kg);
+        }
         int64_t vofs, sofs;
-        v_loc(step, vofs, sofs);
-        load_k(k_ptr(step));
+        v_loc(step, ev, vofs, sofs);
+        load_k(k_ptr(step, ek));
         if constexpr (PER_TOKEN) load_scales(sofs);
         load_v(vofs);
     }
     while (step < nsteps) {
         const int nxt = step + NS;
         const bool has_nxt = nxt < nsteps;
+        int ek_after = 0, ev_after = 0;
+        if (nxt + NS < nsteps) {
+            ek_after = page_of(nxt + NS, l16 >> 2);
+            ev_after = page_of(nxt + NS, kg);
+        }
         const uint8_t *nkb = nullptr;
         int64_t nvofs = 0, nsofs = 0;
         if (has_nxt) {
-            nkb = k_ptr(nxt);
-            v_loc(nxt, nvofs, nsofs);
+            nkb = k_ptr(nxt, ek_next);
+            v_loc(nxt, ev_next, nvofs, nsofs);
         }
+        ek_next = ek_after;
+        ev_next = ev_after;
         f32x4 ksc[4], vsc[4];
         if constexpr (PER_TOKEN) {
 #pragma unroll
