@@ -718,6 +718,7 @@ struct KvStager {
     static constexpr int VROWS = 8 / NW;    // V rows
     static constexpr int SLANES = 32 / NW;  // lanes of a wave loading 16 bytes of scales
     static constexpr int R = KROWS + VROWS + (PER_TOKEN ? 1 : 0);
+    static_assert(KROWS == VROWS, "K and V rows of a wave share their groups");
     static_assert(NW == 1 || NW == 2 || NW == 4, "1, 2 or 4 waves");
     static_assert((STAGES - 2) * R <= 63, "vmcnt range");
 
@@ -747,33 +748,35 @@ struct KvStager {
         const int lastg_page = min(tok_lo + q * kStep + 48, last_group) >> p.bs_log2;
         if (lastg_page - wbase >= kPageWin) load_window((tok_lo + q * kStep) >> p.bs_log2);
         const uint32_t sb = ring_addr + (uint32_t)((q % STAGES) * kStageBytes);
+        // every page-window read first, then the loads: each load's inline asm is a
+        // memory barrier to the compiler, so a window read placed between two loads
+        // would be waited for on its own
+        int phys[KROWS], sub[KROWS];
+#pragma unroll
+        for (int j = 0; j < KROWS; ++j) group_loc(q, (wave + NW * j) >> 1, phys[j], sub[j]);
+        const int piece = wave * SLANES + min(lane, SLANES - 1);
+        int sphys = 0, ssub = 0;
+        if constexpr (PER_TOKEN) group_loc(q, (piece & 15) >> 2, sphys, ssub);
 #pragma unroll
         for (int j = 0; j < KROWS; ++j) {  // K rows: (group g, chunks 4*half .. 4*half+3)
             const int r = wave + NW * j;
             const int g = r >> 1, half = r & 1;
-            int phys, sub;
-            group_loc(q, g, phys, sub);
-            const uint8_t *src =
-                kc_h + (int64_t)phys * p.s_k_block + (4 * half + (lane >> 4)) * kchunk + sub * 256 + (lane & 15) * 16;
+            const uint8_t *src = kc_h + (int64_t)phys[j] * p.s_k_block + (4 * half + (lane >> 4)) * kchunk +
+                                 sub[j] * 256 + (lane & 15) * 16;
             dma16(src, __builtin_amdgcn_readfirstlane(sb + g * kKGroupStride + half * 1024));
         }
 #pragma unroll
-        for (int j = 0; j < VROWS; ++j) {  // V rows: (group g, dims 64*half .. 64*half+63)
+        for (int j = 0; j < VROWS; ++j) {  // V rows: (group g, dims 64*half .. 64*half+63), the K rows' groups
             const int r = wave + NW * j;
             const int g = r >> 1, half = r & 1;
-            int phys, sub;
-            group_loc(q, g, phys, sub);
-            const uint8_t *src = vc_h + (int64_t)phys * p.s_v_block + sub * (kHeadDim * 16) + (64 * half + lane) * 16;
+            const uint8_t *src =
+                vc_h + (int64_t)phys[j] * p.s_v_block + sub[j] * (kHeadDim * 16) + (64 * half + lane) * 16;
             dma16(src, __builtin_amdgcn_readfirstlane(sb + kStageV + g * 2048 + half * 1024));
         }
         if constexpr (PER_TOKEN) {  // 32 pieces of 16 bytes: K scales of groups 0-3, then V scales
             if (lane < SLANES) {
-                const int piece = wave * SLANES + lane;
-                const int g = (piece & 15) >> 2;
-                int phys, sub;
-                group_loc(q, g, phys, sub);
-                const float *src = (piece < 16 ? p.ks : p.vs) + (int64_t)phys * p.s_ks_block +
-                                   (int64_t)h * p.s_ks_head + sub * 16 + 4 * (piece & 3);
+                const float *src = (piece < 16 ? p.ks : p.vs) + (int64_t)sphys * p.s_ks_block +
+                                   (int64_t)h * p.s_ks_head + ssub * 16 + 4 * (piece & 3);
                 dma16(src, __builtin_amdgcn_readfirstlane(sb + kStageS + wave * SLANES * 16));
             }
         }
