@@ -706,15 +706,18 @@ _SEQLENS_CACHE: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
 
 
 def _seqlens_qo_indptr(dev: torch.device, batch_size: int, query_length: int, graph_safe: bool) -> torch.Tensor:
-    """arange(B + 1) * ql on the device, cached per shape outside graph capture."""
+    """arange(B + 1) * ql on the device, cached per shape outside graph capture.  A
+    graph-safe call makes its own tensor: a captured graph must not hold a cached
+    one that a later eviction frees."""
+    if graph_safe:
+        return torch.arange(batch_size + 1, dtype=torch.int32, device=dev) * query_length
     key = (dev, batch_size, query_length)
     t = _SEQLENS_CACHE.get(key)
     if t is None:
         t = torch.arange(batch_size + 1, dtype=torch.int32, device=dev) * query_length
-        if not graph_safe:
-            _SEQLENS_CACHE[key] = t
-            if len(_SEQLENS_CACHE) > 32:
-                _SEQLENS_CACHE.popitem(last=False)
+        _SEQLENS_CACHE[key] = t
+        if len(_SEQLENS_CACHE) > 32:
+            _SEQLENS_CACHE.popitem(last=False)
     return t
 
 
