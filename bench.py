@@ -353,23 +353,15 @@ def main():
 
     from flydsl_amd import get_pa_metadata, pa_decode_ps_launch
     from flydsl_amd.pa_decode_fp8 import _PLAN_CACHE
-    from flydsl_amd.workloads import CONFIGS, build_workload, kv_bytes
+    from flydsl_amd.workloads import CONFIGS, build_workload_copies, kv_bytes
 
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
     print(f"[bench] building {cfg.name} x{args.copies}: {cfg.description}", file=sys.stderr, flush=True)
-    # every copy is built for the first copy's context lengths, so each cache holds
-    # exactly the pages the shared block tables index (a copy sized for other
-    # lengths would have some indices clamped to its last page by the kernel's
-    # bounds guard, and read those from L2); the copies share its block tables,
-    # page lists and query, and differ in their KV bytes and scales
-    base = build_workload(cfg, dev, seed=123, context_lengths=None)
-    works = [base] + [build_workload(cfg, dev, seed=123 + i * 1000, context_lengths=base["context_list"])
-                      for i in range(1, args.copies)]
-    for w in works[1:]:
-        for k in ("context_lengths", "block_tables", "query", "context_list", "block_table_np", "kv_page_indices",
-                  "kv_indptr"):
-            w[k] = base[k]
+    # the copies differ only in their KV bytes and scales; each cache holds exactly
+    # the pages the shared block tables index
+    works = build_workload_copies(cfg, dev, args.copies)
+    base = works[0]
     ctx = base["context_list"]
     max_parts = args.max_parts  # 0: the launcher's default for this kernel
     # partials are allocated by the launcher and reused across steps through its plan cache

@@ -209,6 +209,30 @@ def build_workload(cfg: DecodeConfig, device, seed: int = 123, context_lengths: 
     }
 
 
+# what the copies of build_workload_copies share with the first one
+SHARED_KEYS = ("context_lengths", "block_tables", "query", "context_list", "block_table_np", "kv_page_indices",
+               "kv_indptr")
+
+
+def build_workload_copies(cfg: DecodeConfig, device, copies: int, seed: int = 123) -> List[Dict]:
+    """``copies`` workloads of ``cfg`` that differ only in their KV bytes and scales.
+
+    Every copy is built for the first copy's context lengths, so each cache holds
+    exactly the pages the shared block tables and page lists index; the copies then
+    take the first copy's tables, page lists and query (``SHARED_KEYS``).  A copy
+    sized for other lengths would have indices past its last page, which the
+    kernels' bounds guard clamps to that page.
+    """
+    base = build_workload(cfg, device, seed=seed)
+    works = [base]
+    for i in range(1, copies):
+        w = build_workload(cfg, device, seed=seed + i * 1000, context_lengths=base["context_list"])
+        for k in SHARED_KEYS:
+            w[k] = base[k]
+        works.append(w)
+    return works
+
+
 def attended_tokens(ctx: List[int], query_length: int, sliding_window: int) -> List[int]:
     """Keys any query of the sequence attends: ctx, or min(ctx, sw + ql) with a window."""
     if sliding_window > 0:
