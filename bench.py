@@ -439,13 +439,16 @@ def main():
         step(i)
     torch.cuda.synchronize()
 
-    # ---- per-kernel durations: HIP events around each launch on the launch stream
+    # ---- per-kernel durations: HIP events around each launch on the launch stream.
+    # A GPU-side sleep holds the stream until every launch and event is queued, so
+    # no interval includes a wait for the host to submit its kernel.
     plans = [_PLAN_CACHE[k] for k in list(_PLAN_CACHE.keys())[-len(works):]]
     names = [fn.__name__ for fn, _ in plans[0].launches]
     handle = torch.cuda.current_stream(dev).cuda_stream
     nl = len(names)
     evs = _events(torch, (nl + 1) * args.steps)
     torch.cuda.synchronize()
+    torch.cuda._sleep(int(2.5e6 + 4e4 * args.steps))  # cycles: several ms of queue head start
     for i in range(args.steps):
         p = plans[i % len(plans)]
         evs[(nl + 1) * i].record()
