@@ -24,7 +24,6 @@
 #include "pa_common.h"
 #include "pa_fp8.h"
 
-#include <stdlib.h>
 
 using namespace pa;
 
@@ -149,7 +148,7 @@ template <int MTPW>
 constexpr int kWavesPerSimd = MTPW == 1 ? 2 : 1;
 
 #ifndef PA_FP8_STAGED_WAVES
-#define PA_FP8_STAGED_WAVES 2  // waves per SIMD the LDS-staged layout is compiled for
+#define PA_FP8_STAGED_WAVES 3  // waves per SIMD the LDS-staged layout is compiled for
 #endif
 template <int MTPW, int NS>
 constexpr int kWavesFor = NS == 0 ? PA_FP8_STAGED_WAVES : kWavesPerSimd<MTPW>;
@@ -299,9 +298,9 @@ struct SmState {
 // (the lane's 32 bytes of tile jt are exactly its A operand: dims 32kg .. 32kg+31),
 // two products per tile (hi and lo terms of the query), and the row's dequant
 // factor joins the logit scale; no K conversion.
-template <int MTPW, bool PER_TOKEN, class RW, class AfterQk>
+template <int MTPW, bool PER_TOKEN, class RW, class KScale, class VScale, class AfterQk>
 __device__ __forceinline__ void step_qk_softmax(SmState<MTPW> &st, const RW &rw, const uint4 (&kr)[4][2],
-                                                const f32x4 (&ksr)[4], const f32x4 (&vsr)[4], float k_fac, int t0,
+                                                const KScale &ksr, const VScale &vsr, float k_fac, int t0,
                                                 int kg, bf16x8 (&pop)[MTPW][2], AfterQk &&after_qk) {
     const int trow = t0 + 16 * kg;  // token of (tile jt, i) = trow + 4jt + i
     const bool interior = t0 >= rw.lo_max && t0 + kStep <= rw.hi_min;
@@ -341,7 +340,7 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW> &st, const RW &rw,
     f32x4 kf[4];
     if constexpr (!RW::kFp8) {
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr[jt] * k_fac : f32x4{k_fac, k_fac, k_fac, k_fac};
+        for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr(jt) * k_fac : f32x4{k_fac, k_fac, k_fac, k_fac};
     }
 
 #pragma unroll
@@ -349,7 +348,7 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW> &st, const RW &rw,
         if constexpr (RW::kFp8) {
             const float kq = k_fac * rw.dq[mg];
 #pragma unroll
-            for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr[jt] * kq : f32x4{kq, kq, kq, kq};
+            for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr(jt) * kq : f32x4{kq, kq, kq, kq};
         }
         float mx = -INFINITY;
 #pragma unroll
@@ -386,7 +385,7 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW> &st, const RW &rw,
                 psum += pv;
                 sc[mg][jt][i] = pv;
             }
-            if constexpr (PER_TOKEN) sc[mg][jt] *= vsr[jt];
+            if constexpr (PER_TOKEN) sc[mg][jt] *= vsr(jt);
         }
         st.l_run[mg] += psum;
         pop[mg][0] = pack_bf16x8(sc[mg][0], sc[mg][1]);
@@ -574,7 +573,8 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
             }
         }
         bf16x8 pop[MTPW][2];
-        step_qk_softmax<MTPW, PER_TOKEN>(st, rw, kr, ksc, vsc, k_fac, tok_lo + step * kStep, kg, pop, [&] {
+        step_qk_softmax<MTPW, PER_TOKEN>(st, rw, kr, [&](int jt) { return ksc[jt]; }, [&](int jt) { return vsc[jt]; },
+                                         k_fac, tok_lo + step * kStep, kg, pop, [&] {
             if (has_nxt) {
                 load_k(nkb);  // K registers are free again
                 if constexpr (PER_TOKEN) load_scales(nsofs);
@@ -674,13 +674,13 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
 // different banks), V [4 groups][128 dims][16 tokens], then the per-token K and V
 // scales [4 groups][16] f32 each.
 #ifndef PA_FP8_STAGES
-#define PA_FP8_STAGES 4  // ring depth (steps in flight + 1)
+#define PA_FP8_STAGES 3  // ring depth (steps in flight + 1)
 #endif
 #ifndef PA_FP8_KPAD
 #define PA_FP8_KPAD 64  // bytes of padding after each K group
 #endif
 #ifndef PA_FP8_PAGE_WINDOW
-#define PA_FP8_PAGE_WINDOW 1024  // page-row entries held in LDS at a time
+#define PA_FP8_PAGE_WINDOW 256  // page-row entries held in LDS at a time
 #endif
 constexpr int kStages = PA_FP8_STAGES;
 constexpr int kKGroupStride = 2048 + PA_FP8_KPAD;
@@ -864,27 +864,23 @@ __device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const
         if (n + kStages - 1 < sg.nsteps) sg.issue(n + kStages - 1);
         const uint8_t *sk = sg.stage(n);
         uint4 kr[4][2];
-        uint4 vr[8];
-        f32x4 ksr[4], vsr[4];
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
             const uint8_t *kp = sk + (l16 >> 2) * kKGroupStride + (2 * kg) * 256 + (4 * jt + (l16 & 3)) * 16;
             kr[jt][0] = *reinterpret_cast<const uint4 *>(kp);
             kr[jt][1] = *reinterpret_cast<const uint4 *>(kp + 256);
         }
-        if constexpr (PER_TOKEN) {
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                ksr[q4] = *reinterpret_cast<const f32x4 *>(sk + kStageS + kg * 64 + 16 * q4);
-                vsr[q4] = *reinterpret_cast<const f32x4 *>(sk + kStageS + 256 + kg * 64 + 16 * q4);
-            }
-        }
-        // V is read with K, so its LDS latency hides under the QK products and softmax
+        // the scales and V are read from the stage where they are used, which keeps
+        // them out of registers during the QK products and the softmax
+        const uint8_t *ss = sk + kStageS + kg * 64;
+        auto ks_at = [&](int jt) { return *reinterpret_cast<const f32x4 *>(ss + 16 * jt); };
+        auto vs_at = [&](int jt) { return *reinterpret_cast<const f32x4 *>(ss + 256 + 16 * jt); };
+        bf16x8 pop[MTPW][2];
+        step_qk_softmax<MTPW, PER_TOKEN>(st, rw, kr, ks_at, vs_at, k_fac, tok_lo + n * kStep, kg, pop, [] {});
+        uint4 vr[8];
 #pragma unroll
         for (int m = 0; m < 8; ++m)
             vr[m] = *reinterpret_cast<const uint4 *>(sk + kStageV + kg * 2048 + (16 * m + l16) * 16);
-        bf16x8 pop[MTPW][2];
-        step_qk_softmax<MTPW, PER_TOKEN>(st, rw, kr, ksr, vsr, k_fac, tok_lo + n * kStep, kg, pop, [] {});
         step_pv<MTPW>(st, vr, pop);
     }
     finish_rows<MTPW>(st, p, wave * MTPW, l16, kg, v_fac, sink);
@@ -1266,20 +1262,9 @@ hipError_t launch_decode(const DecodeParams &p, dim3 grid, hipStream_t s) {
 // Wave layout per number of 16-row query groups (ql * group_size / 16, rounded up):
 //   one group    -> <1,1,4>: four waves split the steps;
 //   two groups   -> <2,1,4>: every wave holds both groups, four waves split the steps;
-//   3 / 4 groups -> <2,2,2>: each wave holds two groups (one fp8 -> bf16 conversion of
-//                   K / V feeds both), two wave pairs split the rows, the pairs split
-//                   the steps.
+//   3 / 4 groups -> <1,4,0>: one wave per group, the workgroup's steps staged through
+//                   an LDS ring that every wave reads.
 // The waves of the one-group layout come with the launch (waves_per_slot).
-// Tuning knob (environment, read once): PA_FP8_WIDE picks the 3 / 4-group layout
-// (1: <1,4,1> one wave per group, 2: <2,2,2>, 4: <4,1,4>).
-int env_int(const char *name) {
-    const char *e = getenv(name);
-    return e ? atoi(e) : 0;
-}
-int env_wide() {
-    static const int v = env_int("PA_FP8_WIDE");
-    return v;
-}
 
 template <bool PT>
 hipError_t dispatch_decode(const DecodeParams &p, int mtp, int waves, dim3 grid, hipStream_t s) {
@@ -1292,13 +1277,7 @@ hipError_t dispatch_decode(const DecodeParams &p, int mtp, int waves, dim3 grid,
         default: return launch_decode<1, 1, 4, PT>(p, grid, s);
         }
     case 2: return launch_decode<2, 1, 4, PT>(p, grid, s);
-    default:
-        switch (env_wide()) {
-        case 1: return launch_decode<1, 4, 1, PT>(p, grid, s);
-        case 2: return launch_decode<2, 2, 2, PT>(p, grid, s);
-        case 5: return launch_decode<2, 2, 0, PT>(p, grid, s);
-        default: return launch_decode<1, 4, 0, PT>(p, grid, s);
-        }
+    default: return launch_decode<1, 4, 0, PT>(p, grid, s);
     }
 }
 
@@ -1313,13 +1292,7 @@ hipError_t dispatch_worklist(const WorklistParams &w, int mtp, dim3 grid, hipStr
     switch (mtp) {
     case 1: return launch_worklist<1, 1, 4, PT>(w, grid, s);
     case 2: return launch_worklist<2, 1, 4, PT>(w, grid, s);
-    default:
-        switch (env_wide()) {
-        case 1: return launch_worklist<1, 4, 1, PT>(w, grid, s);
-        case 2: return launch_worklist<2, 2, 2, PT>(w, grid, s);
-        case 5: return launch_worklist<2, 2, 0, PT>(w, grid, s);
-        default: return launch_worklist<1, 4, 0, PT>(w, grid, s);
-        }
+    default: return launch_worklist<1, 4, 0, PT>(w, grid, s);
     }
 }
 

@@ -25,11 +25,17 @@ from .pa_metadata import get_pa_metadata_info_v1, get_pa_metadata_v1
 from .pa_reduce import _reduce_v1_args
 
 KV_COMPUTE_BLOCK = 256  # tokens per context partition (kernels/pa_decode_fp8.py:36)
-# Worklist bins per CU.  The reference schedules 3 (kernels/pa_decode_fp8.py:37-40)
-# because about three of its workgroups fit a CU; two of ours fit (two 4-wave
-# workgroups per CU at two waves per SIMD), and one bin per resident workgroup
-# keeps every bin's share of the batch running from start to end.
+# Worklist bins per CU: one per workgroup of the worklist kernel that fits a CU, so
+# every bin's share of the batch runs from start to end.  The reference schedules 3
+# (kernels/pa_decode_fp8.py:37-40).  Two 4-wave workgroups of the register-streaming
+# kernel fit a CU (query rows per kv head ql * g <= 32); three of the LDS-staged one
+# (ql * g > 32: three waves per SIMD, a 52.5 KiB ring each).
 _PA_METADATA_GRID_OVERSUB = 2
+_PA_METADATA_GRID_OVERSUB_STAGED = 3
+
+
+def _metadata_bins_per_cu(query_length: int, query_group_size: int) -> int:
+    return _PA_METADATA_GRID_OVERSUB_STAGED if query_length * query_group_size > 32 else _PA_METADATA_GRID_OVERSUB
 _PA_DECODE_PS_SMALL_BLOCK_SIZES = (16, 64)  # kernels/pa_decode_fp8.py:1955
 HEAD_DIM = 128
 
@@ -735,8 +741,10 @@ def get_pa_metadata(
     """Worklist metadata for the persistent decode (kernels/pa_decode_fp8.py:1729-1859).
 
     Runs the device scheduler ``get_pa_metadata_v1`` over
-    ``num_sm = (CUs * 2 // kv_heads) * kv_heads`` bins; work_info kv ranges are
-    cumulative ``partition_size``-token partition indices.
+    ``num_sm = (CUs * n // kv_heads) * kv_heads`` bins, n the worklist kernel's
+    workgroups per CU (2, or 3 for the LDS-staged kernel that query_length *
+    num_query_heads / num_kv_heads > 32 selects); work_info kv ranges are cumulative
+    ``partition_size``-token partition indices.
 
     By default it synchronises once on ``reduce_indptr[-1]`` to size the partial
     buffers, as the reference does (:1832).  With ``graph_safe`` (the default
@@ -753,10 +761,11 @@ def get_pa_metadata(
     batch_size = context_lengths.shape[0]
     query_length = query.shape[0] // batch_size
     head_size = query.shape[-1]
-    num_sm = _device_cu_count(dev) * _PA_METADATA_GRID_OVERSUB
+    bins_per_cu = _metadata_bins_per_cu(query_length, num_query_heads // num_kv_heads)
+    num_sm = _device_cu_count(dev) * bins_per_cu
     num_sm = (num_sm // num_kv_heads) * num_kv_heads
     if num_sm <= 0 or partition_size <= 0 or partition_size & (partition_size - 1):
-        raise ValueError("get_pa_metadata needs num_kv_heads <= 2 * CUs and a power-of-two partition_size")
+        raise ValueError(f"get_pa_metadata needs num_kv_heads <= {bins_per_cu} * CUs and a power-of-two partition_size")
     seqlens_qo_indptr = _seqlens_qo_indptr(dev, batch_size, query_length, graph_safe)
     ctx = context_lengths if context_lengths.dtype == torch.int32 else context_lengths.to(torch.int32)
     ctx = ctx.contiguous()
