@@ -56,8 +56,10 @@ SMALL_CASES = {
     "mtp3_tok": dict(base="c5", batch=3, query_length=3, ctx_kind="uniform", ctx_a=3, ctx_b=1500),
     "mtp4_pt": dict(base="c5", batch=3, per_token=False, ctx_kind="uniform", ctx_a=4, ctx_b=1500),
     # 16-token pages and contexts past 16K tokens: a slot's pages outgrow the
-    # 1024-entry page window of the LDS-staged layout, which is then refilled
+    # 256-entry page window of the LDS-staged layout many times over, which is then
+    # refilled; and 64-token pages past 256 pages (16K tokens)
     "mtp4_g16_bs16_long": dict(base="c5", batch=2, block_size=16, ctx_kind="uniform", ctx_a=17000, ctx_b=40000),
+    "mtp4_g16_bs64_long": dict(base="c5", batch=2, ctx_kind="uniform", ctx_a=16500, ctx_b=30000),
 }
 
 

@@ -81,6 +81,7 @@ WORKLIST_CASES = {
     "bs512_mtp3_g4": dict(base="c2", batch=5, block_size=512, query_length=3, ctx_kind="uniform", ctx_a=3,
                           ctx_b=4000),
     "bs16_long_mtp4_g16": dict(base="c5", batch=2, block_size=16, ctx_kind="uniform", ctx_a=17000, ctx_b=40000),
+    "bs64_long_mtp4_g16": dict(base="c5", batch=2, ctx_kind="uniform", ctx_a=16500, ctx_b=30000),
     "bs1024_long": dict(base="c2", batch=2, num_q_heads=16, num_kv_heads=2, block_size=1024, ctx_kind="uniform",
                         ctx_a=9000, ctx_b=20000),
 }
