@@ -101,14 +101,32 @@ __device__ __forceinline__ float clean448(float x) {
     return x;
 }
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats rounded to bf16 (nearest even) by one v_cvt_pk_bf16_f32: the packed
+// pair (a in the low half) ...
+__device__ __forceinline__ uint32_t bf16_pair_bits(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+// ... and back as floats.
+__device__ __forceinline__ void round_pair_bf16(float &a, float &b) {
+    const uint32_t u = bf16_pair_bits(a, b);
+    a = __uint_as_float(u << 16);
+    b = __uint_as_float(u & 0xffff0000u);
+}
+
 // NeoX rotation of one lane's 8 (first-half) + 8 (second-half) elements, rounded
-// after each product and after the sum exactly as the element-dtype arithmetic.
+// after each product and after the sum exactly as the element-dtype arithmetic;
+// w1 / w2 get the results packed as the output row's 16-bit elements.
 // Contraction is off so that no product is fused with the add that follows it
 // (v_fma_f16 / v_fma_mix would skip the product's rounding).  f16 computes in
-// native IEEE f16 ops; bf16 in f32 with an explicit round after each step.
+// native IEEE f16 ops; bf16 in f32 with an explicit round after each step, two
+// values per conversion (the rounding of each value is that of a conversion of
+// its own), the final round of a pair of dims being also its packed output word.
 template <int ELEM>
 __device__ __forceinline__ void rotate(float (&x1)[8], float (&x2)[8], const float (&c1)[8], const float (&s1)[8],
-                                       const float (&c2)[8], const float (&s2)[8]) {
+                                       const float (&c2)[8], const float (&s2)[8], uint4 &w1, uint4 &w2) {
 #pragma clang fp contract(off)
     if constexpr (ELEM == PA_FP8_F16) {
         // native IEEE f16 products and sums (v_mul_f16 / v_sub_f16 / v_add_f16)
@@ -120,13 +138,29 @@ __device__ __forceinline__ void rotate(float (&x1)[8], float (&x2)[8], const flo
             x1[i] = (float)(_Float16)(p1 - p2);
             x2[i] = (float)(_Float16)(p3 + p4);
         }
+        w1 = pack8<ELEM>(x1);
+        w2 = pack8<ELEM>(x2);
     } else {
+        uint32_t u1[4], u2[4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float a = x1[i], b = x2[i];
-            x1[i] = rnd<ELEM>(rnd<ELEM>(a * c1[i]) - rnd<ELEM>(b * s1[i]));
-            x2[i] = rnd<ELEM>(rnd<ELEM>(b * c2[i]) + rnd<ELEM>(a * s2[i]));
+        for (int j = 0; j < 4; ++j) {
+            const int i = 2 * j;
+            float p1a = x1[i] * c1[i], p2a = x2[i] * s1[i], p3a = x2[i] * c2[i], p4a = x1[i] * s2[i];
+            float p1b = x1[i + 1] * c1[i + 1], p2b = x2[i + 1] * s1[i + 1];
+            float p3b = x2[i + 1] * c2[i + 1], p4b = x1[i + 1] * s2[i + 1];
+            round_pair_bf16(p1a, p2a);
+            round_pair_bf16(p3a, p4a);
+            round_pair_bf16(p1b, p2b);
+            round_pair_bf16(p3b, p4b);
+            u1[j] = bf16_pair_bits(p1a - p2a, p1b - p2b);  // dims i, i + 1 of the first half
+            u2[j] = bf16_pair_bits(p3a + p4a, p3b + p4b);  // and of the second half
+            x1[i] = __uint_as_float(u1[j] << 16);
+            x1[i + 1] = __uint_as_float(u1[j] & 0xffff0000u);
+            x2[i] = __uint_as_float(u2[j] << 16);
+            x2[i + 1] = __uint_as_float(u2[j] & 0xffff0000u);
         }
+        w1 = make_uint4(u1[0], u1[1], u1[2], u1[3]);
+        w2 = make_uint4(u2[0], u2[1], u2[2], u2[3]);
     }
 }
 
@@ -244,11 +278,12 @@ __device__ __forceinline__ void rotate_row(const RopeParams &p, const RowIn &r, 
     }
     unpack8<ELEM>(r.x1, x1);
     unpack8<ELEM>(r.x2, x2);
-    rotate<ELEM>(x1, x2, c1, s1, c2, s2);
+    uint4 w1, w2;
+    rotate<ELEM>(x1, x2, c1, s1, c2, s2, w1, w2);
     uint16_t *out = r.is_k ? p.ko + int64_t(r.t) * p.sko_t + int64_t(r.h) * p.sko_h
                            : p.qo + int64_t(r.t) * p.sqo_t + int64_t(r.h) * p.sqo_h;
-    st16v(out + d1, pack8<ELEM>(x1));
-    st16v(out + d2, pack8<ELEM>(x2));
+    st16v(out + d1, w1);
+    st16v(out + d2, w2);
 }
 
 // Cache element pattern of one value (16-bit element or fp8 code).
