@@ -31,6 +31,27 @@ namespace {
 
 constexpr int kRopeThreads = 256;
 
+// n / d for 0 <= n < 2^31 by multiplication (division by an invariant integer,
+// Granlund and Montgomery 1994): with l = ceil(log2 d) and
+// mul = floor(2^32 (2^l - d) / d) + 1, n / d = (mulhi(n, mul) + n) >> l.  The sum
+// stays below 2^32 because n < 2^31.  d = 1 gives mul = 1, l = 0 (n itself); a
+// power of two gives mul = 1 (a shift).
+struct FastDiv {
+    uint32_t mul, shift;
+    int32_t d;
+};
+
+FastDiv make_fastdiv(int d) {
+    uint32_t l = 0;
+    while ((uint64_t(1) << l) < uint64_t(d)) ++l;
+    const uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << l) - uint64_t(d))) / uint64_t(d) + 1;
+    return FastDiv{uint32_t(m), l, d};
+}
+
+__device__ __forceinline__ int fdiv(int n, const FastDiv &f) {
+    return int((__umulhi(uint32_t(n), f.mul) + uint32_t(n)) >> f.shift);
+}
+
 struct RopeParams {
     const uint16_t *q, *k, *v, *cos, *sin;
     const int32_t *pos, *slot;
@@ -46,6 +67,7 @@ struct RopeParams {
     int32_t QH, KH, D, bs, nb, max_pos;
     int32_t pos_shift, slot_shift;  // 1: int64 index tensor, low word at element 2t
     int32_t reuse, lpr_log2, chunks;
+    FastDiv div_qh, div_kh, div_bs, div_d;  // the launch's divisors (all rows, slots < 2^31)
 };
 
 template <int ELEM>
@@ -304,13 +326,13 @@ __device__ __forceinline__ void finish_kv_row(const RopeParams &p, const RowIn &
     bool write = false;
     if (r.live) {
         rotate_row<ELEM>(p, r, d1, d2, x1, x2);
-        write = r.slot >= 0 && r.slot / p.bs < p.nb;
+        write = r.slot >= 0 && fdiv(r.slot, p.div_bs) < p.nb;
         if (write) {
             unpack8<ELEM>(r.v1, v1);
             unpack8<ELEM>(r.v2, v2);
         }
     }
-    const int blk = write ? r.slot / p.bs : 0;
+    const int blk = write ? fdiv(r.slot, p.div_bs) : 0;
     const int bpos = write ? r.slot - blk * p.bs : 0;
 
     if constexpr (FMT == PA_FP8_CACHE_FP8_TENSOR) {
@@ -412,7 +434,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_cache_kernel(RopeParams p) 
         const int64_t row = tile * rpp + lrow;
         r.live = lane_live && row < p.q_rows;
         r.is_k = false;
-        r.t = r.live ? int(row / p.QH) : 0;
+        r.t = r.live ? fdiv(int(row), p.div_qh) : 0;
         r.h = r.live ? int(row - int64_t(r.t) * p.QH) : 0;
         load_row(p, d1, d2, r);
         load_freqs(p, d1, d2, r);
@@ -431,7 +453,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_cache_kernel(RopeParams p) 
     const int64_t krow = (tile - p.q_tiles) * rpp + lrow;
     const int64_t grp = krow >> 4;  // (token group, head) pair
     const int gi = int(krow & 15);  // token inside the group
-    const int64_t tg = grp / p.KH;
+    const int64_t tg = fdiv(int(grp), p.div_kh);
     r.h = int(grp - tg * p.KH);
     r.t = int(tg * 16 + gi);
     r.is_k = true;
@@ -444,7 +466,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_cache_kernel(RopeParams p) 
         // stage V through LDS when every row of every group in this tile sits at
         // slot0 + i of an aligned run (slot0 = the group's first slot)
         const int slot0 = tg * 16 < p.T ? p.slot[int64_t(tg * 16) << p.slot_shift] : -1;
-        const bool run = r.t < p.T && slot0 >= 0 && (slot0 & 15) == 0 && slot0 / p.bs < p.nb &&
+        const bool run = r.t < p.T && slot0 >= 0 && (slot0 & 15) == 0 && fdiv(slot0, p.div_bs) < p.nb &&
                          r.slot == slot0 + gi;
         stage = __syncthreads_and(run || !lane_live) != 0;
         if (stage && gi == 0 && c == 0) group_slot0[lrow >> 4] = slot0;
@@ -457,11 +479,11 @@ __global__ __launch_bounds__(kRopeThreads) void rope_cache_kernel(RopeParams p) 
     constexpr int esz = FMT == PA_FP8_CACHE_ELEM ? 2 : 1;
     const int segs = (rpp >> 4) * p.D;
     for (int j = threadIdx.x; j < segs; j += kRopeThreads) {
-        const int g = j / p.D, d = j - g * p.D;
+        const int g = fdiv(j, p.div_d), d = j - g * p.D;
         const int64_t gg = ((tile - p.q_tiles) * rpp >> 4) + g;
-        const int h = int(gg % p.KH);
+        const int h = int(gg - int64_t(fdiv(int(gg), p.div_kh)) * p.KH);
         const int slot0 = group_slot0[g];
-        const int blk = slot0 / p.bs, pos0 = slot0 - blk * p.bs;
+        const int blk = fdiv(slot0, p.div_bs), pos0 = slot0 - blk * p.bs;
         const int64_t off = LAYOUT == PA_FP8_KV_X_TRANS ? int64_t(pos0 >> 4) * (int64_t(p.D) * 16) + int64_t(d) * 16
                                                         : int64_t(d) * p.bs + pos0;
         uint8_t *dst = p.vc + (int64_t(blk) * p.svc_b + int64_t(h) * p.svc_h + off) * esz;
@@ -606,7 +628,13 @@ extern "C" int pa_fp8_rope_cache(const pa_fp8_rope_cache_args *a, void *hip_stre
     p.q_tiles = (p.q_rows + rpp - 1) / rpp;
     const int64_t kv_rows = (int64_t(a->num_tokens) + 15) / 16 * 16 * a->num_kv_heads;
     const int64_t blocks = p.q_tiles + (kv_rows + rpp - 1) / rpp;
-    if (blocks > 0x7fffffffLL) return PA_FP8_ERR_SHAPE;
+    // row indices, (token group, head) indices and slots are divided as 31-bit values
+    if (blocks > 0x7fffffffLL || (p.q_tiles + 1) * rpp > 0x7fffffffLL || kv_rows + rpp > 0x7fffffffLL)
+        return PA_FP8_ERR_SHAPE;
+    p.div_qh = make_fastdiv(a->num_q_heads);
+    p.div_kh = make_fastdiv(a->num_kv_heads);
+    p.div_bs = make_fastdiv(a->block_size);
+    p.div_d = make_fastdiv(D);
     // staged V writes: whole 16-token groups per workgroup, 16-aligned runs inside a
     // page, 16-byte aligned (block, head) tiles
     const int64_t esz = a->cache_format == PA_FP8_CACHE_ELEM ? 2 : 1;

@@ -437,3 +437,20 @@ def test_prefill_slot_runs(kind, T, layout, fmt):
 def test_prefill_runs_other_head_dims(D, QH, KH):
     # D=512 has 8 rows per workgroup (fewer than a 16-token group): element-wise V writes
     run_case(80, D, QH, KH, layout="x5", fmt="fp8_token", bs=16, num_blocks=12, slots=_runs("aligned", 80, 16, 12, 0))
+
+
+@pytest.mark.parametrize(
+    "layout,bs,fmt,kind",
+    [("flash", 24, "fp8_token", "random"), ("x4", 24, "elem", "random"), ("x5", 48, "fp8_tensor", "random"),
+     ("x5", 48, "fp8_token", "aligned"), ("x4", 48, "elem", "aligned")],
+)
+def test_divisors_that_are_not_powers_of_two(layout, bs, fmt, kind):
+    """12 query and 3 kv heads, head_dim 96 and 24- or 48-token pages: every index the
+    kernel divides (row / heads, (token group, head) / kv heads, slot / block size and
+    the staged segments' index / head_dim) has a divisor that is not a power of two."""
+    T, nb = 150, 12
+    if kind == "random":
+        slots = torch.randperm(nb * bs, generator=torch.Generator().manual_seed(bs))[:T].int()
+    else:  # consecutive slots from a 16-aligned start: the staged V writes
+        slots = _runs("aligned", T, bs, nb, T)
+    run_case(T, 96, 12, 3, layout=layout, fmt=fmt, bs=bs, num_blocks=nb, slots=slots)
