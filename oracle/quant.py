@@ -13,6 +13,8 @@ Layouts (all per physical block ``b`` and kv head ``h``):
                                                   tests/kernels/test_pa.py:419-429)
 * per-token scales ``s[nb, H, bs, 1]`` float32   (quantize_kv_cache_symmetric,
                                                   tests/kernels/test_pa.py:334-376)
+
+Parity unpinned: ``per_tensor_quant`` (aiter's quantiser is absent, see there).
 """
 
 from __future__ import annotations
@@ -44,7 +46,10 @@ def per_tensor_quant(x: np.ndarray, dtype_max: float = E4M3_MAX):
     """Single-scale symmetric fp8 quantisation: scale = amax / 448 (0 -> 1).
 
     aiter's ``per_tensor_quant`` (tests/kernels/test_pa.py:20-26, :408-409) is not
-    in the container; this follows the definition the BASELINE configs state.
+    in the container; this follows the benchmark configurations' definition
+    (scale = amax / 448, then the float8_e4m3fn cast).  Parity unpinned: no
+    reference output of aiter's quantiser exists here.  The decode kernels consume
+    whatever codes and scale they are given, so their parity does not rest on it.
     Returns (uint8 codes, float32 scale of shape [1]).
     """
     x = np.asarray(x, dtype=np.float32)
