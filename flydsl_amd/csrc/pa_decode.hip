@@ -305,8 +305,13 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW> &st, const RW &rw,
     const int trow = t0 + 16 * kg;  // token of (tile jt, i) = trow + 4jt + i
     const bool interior = t0 >= rw.lo_max && t0 + kStep <= rw.hi_min;
 
-    // QK: S[token][qrow] for 4 tiles of 16 tokens
+    // QK: S[token][qrow] for 4 tiles of 16 tokens.  The wave runs its products and
+    // softmax here, and its PV products in step_pv, at raised issue priority (its
+    // loads, LDS reads and barrier waits at the base level), so the SIMD keeps
+    // feeding the matrix pipe of a wave that reached its products while the other
+    // waves' VALU work fills the pipe's busy cycles.
     f32x4 sc[MTPW][4];
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
         if constexpr (RW::kFp8) {
@@ -391,12 +396,14 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW> &st, const RW &rw,
         pop[mg][0] = pack_bf16x8(sc[mg][0], sc[mg][1]);
         pop[mg][1] = pack_bf16x8(sc[mg][2], sc[mg][3]);
     }
+    __builtin_amdgcn_s_setprio(0);
 }
 
 // PV of one step: O[dim][qrow] += V^T P^T over its 64 tokens; vr[m] holds the 16
 // tokens of group kg of head dim 16m + l16.
 template <int MTPW>
 __device__ __forceinline__ void step_pv(SmState<MTPW> &st, const uint4 (&vr)[8], const bf16x8 (&pop)[MTPW][2]) {
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
         const bf16x8 v0 = fp8x8_to_bf16x8(vr[m].x, vr[m].y);
@@ -407,6 +414,7 @@ __device__ __forceinline__ void step_pv(SmState<MTPW> &st, const uint4 (&vr)[8],
             st.o[mg][m] = mfma_bf16(v1, pop[mg][1], st.o[mg][m]);
         }
     }
+    __builtin_amdgcn_s_setprio(0);
 }
 
 // Rows of a wave that ran every step of the range itself: sum the four kg-lane
