@@ -306,10 +306,10 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW> &st, const RW &rw,
     const bool interior = t0 >= rw.lo_max && t0 + kStep <= rw.hi_min;
 
     // QK: S[token][qrow] for 4 tiles of 16 tokens.  The wave runs its products and
-    // softmax here, and its PV products in step_pv, at raised issue priority (its
-    // loads, LDS reads and barrier waits at the base level), so the SIMD keeps
-    // feeding the matrix pipe of a wave that reached its products while the other
-    // waves' VALU work fills the pipe's busy cycles.
+    // softmax here at raised issue priority (1), and its PV products in step_pv
+    // higher still (2); its loads, LDS reads and barrier waits stay at the base
+    // level.  The SIMD then keeps feeding the matrix pipe of a wave that reached
+    // its products while the other waves' VALU work fills the pipe's busy cycles.
     f32x4 sc[MTPW][4];
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -403,7 +403,7 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW> &st, const RW &rw,
 // tokens of group kg of head dim 16m + l16.
 template <int MTPW>
 __device__ __forceinline__ void step_pv(SmState<MTPW> &st, const uint4 (&vr)[8], const bf16x8 (&pop)[MTPW][2]) {
-    __builtin_amdgcn_s_setprio(1);
+    __builtin_amdgcn_s_setprio(2);
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
         const bf16x8 v0 = fp8x8_to_bf16x8(vr[m].x, vr[m].y);
