@@ -869,7 +869,10 @@ __device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const
     sg.prologue();
     for (int n = 0; n < sg.nsteps; ++n) {
         sg.wait_step(n);
+        // the ring loads go out ahead of the other waves' products on the SIMD
+        __builtin_amdgcn_s_setprio(3);
         if (n + kStages - 1 < sg.nsteps) sg.issue(n + kStages - 1);
+        __builtin_amdgcn_s_setprio(0);
         const uint8_t *sk = sg.stage(n);
         uint4 kr[4][2];
 #pragma unroll
