@@ -412,16 +412,23 @@ __device__ __forceinline__ void finish_kv_row(const RopeParams &p, const RowIn &
 // dim-major layouts are staged in LDS and each (head, dim) segment of 16 tokens is
 // written with one 16-byte store (two for 16-bit caches); otherwise (decode: one
 // token per sequence) each lane writes its own elements.
-// Workgroups are dealt round-robin to the 8 XCDs (workgroup w runs on XCD w % 8);
-// the remapped index gives XCD x one contiguous range of tiles, so that cache
-// entries of neighbouring tokens written element-wise merge in one L2.
+// Workgroups are dealt round-robin to the 8 XCDs (workgroup w runs on XCD w % 8).
+// The remapped index gives XCD x its even share of the Q tiles and of the K/V
+// tiles, each a contiguous range: K/V tiles move twice the bytes of Q tiles, so one
+// range over both kinds would leave some XCDs all the K/V work, and cache entries
+// of neighbouring tokens written element-wise merge in one L2.
 template <int ELEM, int FMT, int LAYOUT>
 __global__ __launch_bounds__(kRopeThreads) void rope_cache_kernel(RopeParams p) {
     __shared__ __align__(16) uint16_t vstage[kRopeThreads * 16];
     __shared__ int group_slot0[16];
-    const uint32_t nwg = gridDim.x, w = blockIdx.x;
-    const uint32_t xcd = w & 7u, per = nwg >> 3, rem = nwg & 7u;
-    const int64_t tile = int64_t(xcd * per + min(xcd, rem) + (w >> 3));
+    const int64_t nwg = gridDim.x, w = blockIdx.x;  // nwg = all tiles
+    const int64_t x = w & 7, j = w >> 3;
+    // XCD x runs n_x = ceil((nwg - x) / 8) workgroups: nq_x Q tiles from qs_x, then
+    // the rest K/V tiles from ks_x (the sums of the earlier XCDs' shares)
+    const int64_t nq = p.q_tiles > x ? (p.q_tiles - x + 7) >> 3 : 0;
+    const int64_t qs = x * (p.q_tiles >> 3) + min(x, p.q_tiles & 7);
+    const int64_t ks = x * (nwg >> 3) + min(x, nwg & 7) - qs;
+    const int64_t tile = j < nq ? qs + j : p.q_tiles + ks + (j - nq);
     const int lpr_log2 = p.lpr_log2;
     const int c = int(threadIdx.x & ((1u << lpr_log2) - 1));
     const int rpp = kRopeThreads >> lpr_log2;  // rows per tile
