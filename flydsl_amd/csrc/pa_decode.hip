@@ -958,6 +958,7 @@ struct WorklistParams {
     int64_t s_out_seq, s_out_head;
     int64_t s_po_row, s_pl_row;
     int32_t batch, num_kv_heads, num_pages, max_work, partial_rows, output_rows, out_dtype;
+    int32_t bin_groups;  // > 1: bin group a runs on the workgroups of dispatch round a
 };
 
 // Where a work's rows go: output[qo_start + qi, qhead] when the work holds its
@@ -988,14 +989,25 @@ struct WorkSink {
 };
 
 // Persistent decode over the get_pa_metadata_v1 worklist: workgroup c runs the
-// works [work_indptr[c], work_indptr[c+1]) one after another
-// (kernels/pa_decode_fp8.py:941-1721).  Every field read from the worklist is
+// works [work_indptr[c], work_indptr[c+1]) of its bin one after another
+// (kernels/pa_decode_fp8.py:941-1721).  With bin_groups = G the device takes the
+// workgroups in G rounds of gridDim/G (one per CU each), and workgroup c of round
+// a = c / (gridDim/G) runs a bin of group a of some head: a schedule weighted by
+// group then gives the workgroups dispatched first, which issue ahead of the later
+// ones on their CU, the larger quotas.  Every field read from the worklist is
 // range-checked, so a malformed or overflowed worklist skips work instead of
 // touching memory outside the tensors.
 template <int MTPW, int RS, int NS, bool PER_TOKEN>
 __global__ __launch_bounds__((kThreads<RS, NS>), (kWavesFor<MTPW, NS>)) void pa_decode_worklist_kernel(const WorklistParams w) {
     const DecodeParams &p = w.kv;
-    const int c = blockIdx.x;
+    int c = blockIdx.x;
+    if (w.bin_groups > 1) {
+        const int per_round = gridDim.x / w.bin_groups;  // workgroups per dispatch round
+        const int per_group = per_round / w.num_kv_heads;  // bins of one head in one group
+        const int a = c / per_round, u = c - a * per_round;
+        const int k = u / per_group, j = u - k * per_group;
+        c = k * (per_round * w.bin_groups / w.num_kv_heads) + a * per_group + j;
+    }
     const int wbeg = max(__builtin_amdgcn_readfirstlane(w.work_indptr[c]), 0);
     const int wend = min(__builtin_amdgcn_readfirstlane(w.work_indptr[c + 1]), w.max_work);
     for (int wi = wbeg; wi < wend; ++wi) {
@@ -1563,6 +1575,9 @@ int pa_fp8_decode_worklist(const pa_fp8_worklist_args *a, void *stream) {
     w.partial_rows = a->partial_rows;
     w.output_rows = a->output_rows;
     w.out_dtype = a->out_dtype;
+    w.bin_groups = a->bin_groups > 1 && a->bin_groups <= 4 && a->num_cu % (a->bin_groups * a->num_kv_heads) == 0
+                       ? a->bin_groups
+                       : 1;
 
     const dim3 grid(a->num_cu);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);

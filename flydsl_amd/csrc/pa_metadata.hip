@@ -25,6 +25,8 @@ struct MetaParams {
     int32_t *partition_indptr;  // optional outputs
     int32_t *uniform_context;
     int32_t nb, gqa, nhk, num_cu, kv_gran, ql, max_work, max_split_tiles;
+    int32_t bin_groups;      // > 1: weighted quotas over this many equal groups of each head's bins
+    int32_t bin_weight[4];   // weight of group g (bins [g*nspk/G, (g+1)*nspk/G) of every head)
 };
 
 __device__ __forceinline__ int cdiv_u(int a, int b) { return (int)(((unsigned)a + (unsigned)b - 1u) / (unsigned)b); }
@@ -75,6 +77,12 @@ __device__ __forceinline__ T block_scan_excl(T v, T *s_wave, T &total) {
 // serial machine.  Otherwise (or with more than kParBatches batches, or more than
 // 2^31 partitions) it leaves kSerialSentinel in work_indptr[0] for the serial
 // kernel launched after it.
+// With bin_groups = G > 1 (get_pa_metadata's option, off for get_pa_metadata_v1)
+// the quotas are weighted instead: the bins of each head form G equal groups and
+// bin c takes Qs(c) = floor(S * Wc(c) / Wt), Wc(c) the weights of the bins before
+// it.  Every head keeps the same schedule, so the reduce maps are unchanged in
+// form.  The weights apply when every bin still gets at least one partition
+// (S >= 4 * nspk); otherwise the even split is used.
 __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const MetaParams p) {
     __shared__ int32_t s_P[kParBatches + 1];  // partitions before batch b
     __shared__ int32_t s_W[kParBatches + 1];  // works of head 0 before batch b
@@ -154,8 +162,27 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
     const int S = (int)S64;
     const int avg = S / nspk, rem = S % nspk;
     const int big = rem * (avg + 1);
-    auto bin_of = [&](int x) { return nspk == 1 ? 0 : (x < big ? x / (avg + 1) : rem + (x - big) / avg); };
-    auto Qs = [&](int c) { return c * avg + min(c, rem); };
+    const int ng = p.bin_groups;
+    const bool weighted = ng > 1 && ng <= 4 && nspk % ng == 0 && (long long)S >= 4LL * nspk;
+    const int gm = weighted ? nspk / ng : 1;
+    long long wt = 0;
+    for (int g = 0; g < (weighted ? ng : 0); ++g) wt += p.bin_weight[g] * (long long)gm;
+    auto wc = [&](int c) {  // weights of the bins before c
+        long long a = 0;
+        for (int g = 0; g < ng; ++g) a += p.bin_weight[g] * (long long)min(max(c - g * gm, 0), gm);
+        return a;
+    };
+    auto Qs = [&](int c) { return weighted ? (int)(S64 * wc(c) / wt) : c * avg + min(c, rem); };
+    auto bin_of = [&](int x) {
+        if (!weighted) return nspk == 1 ? 0 : (x < big ? x / (avg + 1) : rem + (x - big) / avg);
+        int lo = 0, hi = nspk - 1;  // last bin whose first partition is <= x
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (Qs(mid) <= x) lo = mid;
+            else hi = mid - 1;
+        }
+        return lo;
+    };
     auto first_bin = [&](int b) {
         const int pb = s_P[b], pe = s_P[b + 1];
         return pe > pb ? bin_of(pb) : (pb == 0 ? 0 : bin_of(pb - 1));
@@ -461,6 +488,11 @@ extern "C" int pa_fp8_metadata_v1(const pa_fp8_metadata_args *a, void *stream) {
         !a->reduce_final_map || !a->reduce_partial_map)
         return PA_FP8_ERR_NULL_POINTER;
     if (a->max_work < 0 || a->max_split_tiles < 0) return PA_FP8_ERR_SHAPE;
+    if (a->bin_groups > 1) {
+        if (a->bin_groups > 4) return PA_FP8_ERR_SHAPE;
+        for (int g = 0; g < a->bin_groups; ++g)
+            if (a->bin_weight[g] < 1 || a->bin_weight[g] > 1000) return PA_FP8_ERR_SHAPE;
+    }
     MetaParams p;
     p.sq = a->seqlens_qo_indptr;
     p.ctx = a->context_lens;
@@ -479,6 +511,8 @@ extern "C" int pa_fp8_metadata_v1(const pa_fp8_metadata_args *a, void *stream) {
     p.max_split_tiles = a->max_split_tiles;
     p.partition_indptr = a->partition_indptr;
     p.uniform_context = a->uniform_context;
+    p.bin_groups = a->bin_groups;
+    for (int g = 0; g < 4; ++g) p.bin_weight[g] = a->bin_weight[g];
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(pa_metadata_par_kernel, dim3(1), dim3(kParThreads), 0, s, p);
     hipError_t err = hipGetLastError();

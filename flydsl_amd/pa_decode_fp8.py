@@ -34,6 +34,14 @@ _PA_METADATA_GRID_OVERSUB = 2
 _PA_METADATA_GRID_OVERSUB_STAGED = 3
 
 
+# Quota weights of the bin groups, first-dispatched group first.  Workgroups that
+# share a CU progress at different rates (the one dispatched first issues ahead of
+# the others): with even quotas, c5's three per CU ran 287 / 308 / 329 us and
+# c3's two per CU 145 / 153 us.  The weights are the fastest of a sweep
+# (three per CU: 108..145 for the first group; two per CU: 105..120).
+_BIN_WEIGHTS = {2: (105, 100), 3: (130, 114, 100)}
+
+
 def _metadata_bins_per_cu(query_length: int, query_group_size: int) -> int:
     return _PA_METADATA_GRID_OVERSUB_STAGED if query_length * query_group_size > 32 else _PA_METADATA_GRID_OVERSUB
 _PA_DECODE_PS_SMALL_BLOCK_SIZES = (16, 64)  # kernels/pa_decode_fp8.py:1955
@@ -484,6 +492,7 @@ def _worklist_plan(
     w.kv_page_indices = kv_page_indices.data_ptr()
     w.kv_indptr = kv_indptr.data_ptr()
     w.partition_indptr = partition_indptr.data_ptr()
+    w.bin_groups = int(metadata.get("bin_groups", 0))  # the schedule's quota groups, by dispatch round
     w.stride_q_seq, w.stride_q_head = query.stride(0), query.stride(1)
     w.stride_k_block, w.stride_k_head = key_cache.stride(0), key_cache.stride(1)
     w.stride_v_block, w.stride_v_head = value_cache.stride(0), value_cache.stride(1)
@@ -519,7 +528,8 @@ def _worklist_plan(
 def _mkey(metadata):
     if metadata is None:
         return None
-    return tuple((k, _tkey(metadata[k])) for k in _METADATA_KEYS if k in metadata) + (("num_sm", metadata.get("num_sm")),)
+    return tuple((k, _tkey(metadata[k])) for k in _METADATA_KEYS if k in metadata) + (
+        ("num_sm", metadata.get("num_sm")), ("bin_groups", metadata.get("bin_groups")))
 
 
 def pa_decode_ps_launch(
@@ -795,6 +805,16 @@ def get_pa_metadata(
     a.reduce_partial_map = reduce_partial_map.data_ptr()
     a.partition_indptr = partition_indptr.data_ptr()
     a.uniform_context = buf[offs[2] + batch_size + 1 :].data_ptr()
+    # quotas weighted by dispatch round, when every round holds whole groups of bins
+    # and the parallel scheduler runs (the serial one, past 4096 batches, splits evenly)
+    bin_groups = bins_per_cu if (num_sm % (bins_per_cu * num_kv_heads) == 0 and batch_size <= 4096
+                                 and num_sm == _device_cu_count(dev) * bins_per_cu) else 0
+    if bin_groups in _BIN_WEIGHTS:
+        a.bin_groups = bin_groups
+        for g, wgt in enumerate(_BIN_WEIGHTS[bin_groups]):
+            a.bin_weight[g] = wgt
+    else:
+        bin_groups = 0
     a.num_batches = batch_size
     a.gqa = num_query_heads // num_kv_heads
     a.num_heads_k = num_kv_heads
@@ -824,6 +844,8 @@ def get_pa_metadata(
         "reduce_final_map": reduce_final_map,
         "reduce_partial_map": reduce_partial_map,
         "num_sm": num_sm,
+        "bin_groups": bin_groups,
+        "bin_weight": _BIN_WEIGHTS.get(bin_groups),
         "partial_output": partial_output,
         "partial_lse": partial_lse,
         "stride_po_partial": query_length * num_query_heads * head_size,

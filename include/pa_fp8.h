@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define PA_FP8_ABI_VERSION 5
+#define PA_FP8_ABI_VERSION 6
 
 enum pa_fp8_status {
     PA_FP8_OK = 0,
@@ -199,6 +199,14 @@ typedef struct pa_fp8_worklist_args {
     int32_t query_dtype;
     int32_t out_dtype;
     float softmax_scale;
+    /* bin_groups = G > 1 (with num_cu a multiple of G * num_kv_heads): workgroup c
+     * runs bin k*nspk + a*(nspk/G) + j instead of bin c, where a = c / (num_cu/G) is
+     * the workgroup's dispatch round (the order in which it joined its CU, when the
+     * device takes num_cu/G workgroups per round) and c % (num_cu/G) = k*(nspk/G) + j,
+     * nspk = num_cu / num_kv_heads.  So bin group a of every head (see
+     * pa_fp8_metadata_args.bin_weight) runs on the workgroups of round a.  Any
+     * permutation of the bins gives the same outputs. */
+    int32_t bin_groups;
 } pa_fp8_worklist_args;
 
 int pa_fp8_decode_worklist(const pa_fp8_worklist_args *args, void *hip_stream);
@@ -251,6 +259,14 @@ int pa_fp8_reduce_v1(const pa_fp8_reduce_v1_args *args, void *hip_stream);
  * partition_indptr [B+1], the exclusive prefix of ceil(context_len /
  * kv_granularity), and uniform_context [1], 1 when every context length is
  * equal (get_pa_metadata's two derived values, so it needs no other launches).
+ * bin_groups = G > 1 (get_pa_metadata's option; 0 gives the reference's
+ * schedule): the bins of each kv head form G equal groups and the parallel
+ * scheduler splits the partitions in proportion to bin_weight[g] (1..1000) of
+ * each bin's group instead of evenly, when every bin still gets a partition
+ * (sum of partitions >= 4 * bins per head).  Workgroups that share a CU progress
+ * at different rates (issue arbitration favours the one dispatched first), and
+ * pa_fp8_decode_worklist with the same bin_groups runs group a on the
+ * workgroups of dispatch round a.
  *
  * Replaces the launcher of `compile_pa_metadata_v1` (kernels/pa_metadata.py:422-447,
  * called from get_pa_metadata_v1 at :515-524).
@@ -273,6 +289,8 @@ typedef struct pa_fp8_metadata_args {
     int32_t max_split_tiles;
     int32_t *partition_indptr;
     int32_t *uniform_context;
+    int32_t bin_groups;
+    int32_t bin_weight[4];
 } pa_fp8_metadata_args;
 
 int pa_fp8_metadata_v1(const pa_fp8_metadata_args *args, void *hip_stream);

@@ -7,7 +7,7 @@ for the bit-exact partition / block-table / worklist indexing of the HIP path.
 
 from __future__ import annotations
 
-from typing import Dict, List, Sequence, Tuple
+from typing import Callable, Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -154,8 +154,13 @@ def get_pa_metadata_v1(
     num_cu: int,
     kv_granularity: int = KV_COMPUTE_BLOCK,
     query_length: int = 1,
+    quota_of: Optional[Callable[[int, int], int]] = None,
 ) -> Dict[str, np.ndarray]:
     """Serial CU x batch worklist scheduler (kernels/pa_metadata.py:145-420).
+
+    ``quota_of(i, sum_blocks)``, when given, replaces the reference's even quota of
+    bin i of a head (:203-206) -- for schedules that split the partitions
+    unevenly over a head's bins; the state machine is otherwise the reference's.
 
     Buffers start POISON-filled (they are torch.empty in the reference) and are
     written exactly where the reference kernel writes, including its
@@ -186,6 +191,8 @@ def get_pa_metadata_v1(
     average, reminder = sum_blocks // nspk, sum_blocks % nspk  # :200-201
 
     def quota(cid: int) -> int:  # :203-206
+        if quota_of is not None:
+            return quota_of(cid % nspk, sum_blocks)
         return average + (1 if (cid % nspk) < reminder else 0)
 
     cid = 0

@@ -10,6 +10,32 @@ from oracle import planners as op
 pytestmark = pytest.mark.gpu
 
 
+def weighted_quota(weights, nspk):
+    """get_pa_metadata's weighted split as a per-bin quota for the oracle's state
+    machine: a head's bins form len(weights) equal groups and bin i starts at
+    floor(S * Wc(i) / Wt), Wc(i) the weights of the bins before it, when
+    nspk % groups == 0 and S >= 4 * nspk; otherwise the reference's even quota."""
+    ng = len(weights)
+    m = nspk // ng
+
+    def wc(i):
+        return sum(w * min(max(i - g * m, 0), m) for g, w in enumerate(weights))
+
+    def quota(i, total):
+        if nspk % ng or total < 4 * nspk:
+            return total // nspk + (1 if i < total % nspk else 0)
+        wt = wc(nspk)
+        return total * wc(i + 1) // wt - total * wc(i) // wt
+
+    return quota
+
+
+def expected_schedule(md, sq, ctx, gqa, nhk, gran=256, ql=1):
+    """The oracle's schedule for a get_pa_metadata result (weighted or even)."""
+    qf = weighted_quota(md["bin_weight"], md["num_sm"] // nhk) if md.get("bin_groups", 0) > 1 else None
+    return op.get_pa_metadata_v1(sq, ctx, gqa, nhk, md["num_sm"], gran, ql, quota_of=qf)
+
+
 def run_device(ctx, ql, gqa, nhk, num_cu, gran):
     from flydsl_amd import get_pa_metadata_info_v1, get_pa_metadata_v1
 
@@ -61,7 +87,8 @@ def test_get_pa_metadata_c3_shape():
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     num_sm = (cus * 2 // 8) * 8  # two bins per CU: two worklist workgroups fit a CU
     assert md["num_sm"] == num_sm
-    ref = op.get_pa_metadata_v1(list(range(129)), ctx, 4, 8, num_sm, 256, 1)
+    assert md["bin_groups"] == 2 and md["bin_weight"] is not None  # c3's 1749 partitions >= 4 * 64
+    ref = expected_schedule(md, list(range(129)), ctx, 4, 8)
     v = op.metadata_valid_prefixes(ref)
     np.testing.assert_array_equal(md["work_indptr"].cpu().numpy(), v["work_indptr"])
     nw = int(v["work_indptr"][-1])
@@ -71,6 +98,43 @@ def test_get_pa_metadata_c3_shape():
     np.testing.assert_array_equal(md["partition_indptr"].cpu().numpy(), np.concatenate([[0], np.cumsum(parts)]))
     npart = int(v["reduce_indptr"][-1])
     assert md["partial_output"].shape == ((npart + 1) * 1, 1, 32, 128)
+
+
+def test_get_pa_metadata_c5_shape_weighted_quotas():
+    """The staged kernel's schedule (three bins per CU) on the c5 shape: quotas
+    weighted by dispatch round, against the oracle's state machine run with the
+    same per-bin quotas; the first round's bins hold the most partitions."""
+    from flydsl_amd import get_pa_metadata
+    from flydsl_amd.workloads import CONFIGS, context_lengths_for
+
+    ctx = context_lengths_for(CONFIGS["c5"])
+    b, ql, hq, hk = 256, 4, 64, 4
+    dev = torch.device("cuda:0")
+    q = torch.zeros(b * ql, hq, 128, dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros(1, hk, 8, 64, 16, dtype=torch.uint8, device=dev)
+    md = get_pa_metadata(q, kc, torch.tensor(ctx, dtype=torch.int32, device=dev),
+                         torch.zeros(b + 1, dtype=torch.int32, device=dev), hq, hk)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    assert md["num_sm"] == (cus * 3 // hk) * hk
+    if md["bin_groups"] != 3:
+        pytest.skip("the device's CU count does not split into whole groups of bins")
+    ref = expected_schedule(md, [ql * i for i in range(b + 1)], ctx, hq // hk, hk, ql=ql)
+    v = op.metadata_valid_prefixes(ref)
+    np.testing.assert_array_equal(md["work_indptr"].cpu().numpy(), v["work_indptr"])
+    nw = int(v["work_indptr"][-1])
+    info = md["work_info_flat"].cpu().numpy()[: nw * 8].reshape(nw, 8)
+    np.testing.assert_array_equal(info, v["work_info"])
+    np.testing.assert_array_equal(md["reduce_indptr"].cpu().numpy(), v["reduce_indptr"])
+    ng = int(v["reduce_indptr"][-1])
+    np.testing.assert_array_equal(md["reduce_partial_map"].cpu().numpy()[:ng], v["reduce_partial_map"][:ng])
+    # partitions per bin of head 0, by group
+    nspk = md["num_sm"] // hk
+    wi = md["work_indptr"].cpu().numpy()
+    per_bin = [int((info[wi[c]:wi[c + 1], 5] - info[wi[c]:wi[c + 1], 4]).sum()) for c in range(nspk)]
+    m = nspk // 3
+    g = [np.mean(per_bin[k * m:(k + 1) * m]) for k in range(3)]
+    assert g[0] > g[1] > g[2]
+    assert sum(per_bin) == sum((c + 255) // 256 for c in ctx)
 
 
 def test_device_scheduler_past_the_lds_staging_capacity():
@@ -162,7 +226,7 @@ def test_get_pa_metadata_partition_prefix_and_uniform_flag(b, kind):
     parts = (ctx.astype(np.int64) + 255) // 256
     np.testing.assert_array_equal(md["partition_indptr"].cpu().numpy(), np.concatenate([[0], np.cumsum(parts)]))
     assert md["uniform_context"] is (kind != "ragged" and kind != "last_differs")
-    ref = op.get_pa_metadata_v1(list(range(b + 1)), [int(c) for c in ctx], 8, 2, md["num_sm"], 256, 1)
+    ref = expected_schedule(md, list(range(b + 1)), [int(c) for c in ctx], 8, 2)
     v = op.metadata_valid_prefixes(ref)
     np.testing.assert_array_equal(md["work_indptr"].cpu().numpy(), v["work_indptr"])
     np.testing.assert_array_equal(md["reduce_indptr"].cpu().numpy(), v["reduce_indptr"])
