@@ -248,3 +248,41 @@ def test_c3_shaped_schedule(c_oracle):
     cc = run_c_metadata(c_oracle, sq, ctx, 4, 8, 768, 256, 1)
     for key, val in op.metadata_valid_prefixes(md).items():
         np.testing.assert_array_equal(val, op.metadata_valid_prefixes(cc)[key])
+
+
+def test_scheduler_with_uneven_quotas_covers_every_partition_once():
+    """get_pa_metadata_v1 with per-bin quotas (quota_of): every head's works still
+    cover each partition exactly once, in order, and each bin takes exactly its
+    quota; with the reference's even quota passed explicitly the schedule is the
+    reference's."""
+    rng = np.random.default_rng(5)
+    for _ in range(40):
+        b = int(rng.integers(1, 200))
+        nhk = int(rng.choice([1, 2, 4]))
+        nspk = int(rng.integers(1, 30))
+        ctx = [int(x) for x in rng.integers(1, 6000, size=b)]
+        total = sum((c + 255) // 256 for c in ctx)
+        if total < nspk:
+            continue
+        w = [int(x) for x in rng.integers(1, 5, size=nspk)]
+        cw = np.concatenate([[0], np.cumsum(w)])
+
+        def quota(i, s, cw=cw):
+            return s * int(cw[i + 1]) // int(cw[-1]) - s * int(cw[i]) // int(cw[-1])
+
+        md = op.get_pa_metadata_v1(list(range(b + 1)), ctx, 4, nhk, nspk * nhk, 256, 1, quota_of=quota)
+        v = op.metadata_valid_prefixes(md)
+        info, wi = v["work_info"], v["work_indptr"]
+        for k in range(nhk):
+            rows = info[(info[:, 7] & 0xFFFF) == 4 * k]
+            assert (rows[:, 4] == np.concatenate([[0], rows[:-1, 5]])).all()  # contiguous, in order
+            assert rows[-1, 5] == total
+            for i in range(nspk):  # bin i of head k holds its quota
+                c = k * nspk + i
+                got = int((info[wi[c]:wi[c + 1], 5] - info[wi[c]:wi[c + 1], 4]).sum())
+                assert got == quota(i, total)
+        even = op.get_pa_metadata_v1(list(range(b + 1)), ctx, 4, nhk, nspk * nhk, 256, 1,
+                                     quota_of=lambda i, s: s // nspk + (1 if i < s % nspk else 0))
+        ref = op.get_pa_metadata_v1(list(range(b + 1)), ctx, 4, nhk, nspk * nhk, 256, 1)
+        for key, val in op.metadata_valid_prefixes(ref).items():
+            np.testing.assert_array_equal(op.metadata_valid_prefixes(even)[key], val)
