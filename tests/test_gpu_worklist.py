@@ -67,6 +67,28 @@ def test_baseline_configs_with_metadata(name):
     compare_outputs(w, out, _spread(cfg.batch, 6))
 
 
+@pytest.mark.parametrize("name", ["c3", "c5"])
+def test_dispatch_round_bin_remap_is_a_permutation(name):
+    """get_pa_metadata's weighted schedule run with its workgroups remapped by
+    dispatch round (bin_groups) and with workgroup c on bin c: each work runs
+    exactly once either way and a work's arithmetic does not depend on the
+    workgroup, so the outputs are bit-identical."""
+    from flydsl_amd import get_pa_metadata
+
+    cfg = CONFIGS[name]
+    print(f"[worklist] {name} bin remap", flush=True)
+    w = build_workload(cfg, "cuda")
+    md = get_pa_metadata(w["query"], w["key_cache"], w["context_lengths"], w["kv_indptr"], cfg.num_q_heads,
+                         cfg.num_kv_heads)
+    md["uniform_context"] = False
+    if md["bin_groups"] <= 1:
+        pytest.skip("the device's CU count does not split into whole groups of bins")
+    out_remap, _, _ = launch(w, metadata=md)
+    out_plain, _, _ = launch(w, metadata=dict(md, bin_groups=0))
+    assert torch.equal(out_remap, out_plain)
+    compare_outputs(w, out_remap, _spread(cfg.batch, 4))
+
+
 WORKLIST_CASES = {
     "bs16_tok_g4": dict(base="c3", batch=6, ctx_kind="uniform", ctx_a=1, ctx_b=3000),
     "bs16_pt_mtp2_g8": dict(base="c2", batch=4, num_q_heads=16, num_kv_heads=2, query_length=2, ctx_kind="uniform",
