@@ -86,6 +86,7 @@ def _worklist_kernel_bytes(cfg, ctx, metadata):
     from flydsl_amd.workloads import algorithmic_bytes, HEAD_DIM
 
     total = algorithmic_bytes(cfg, ctx)
+    metadata = metadata.get("tuned") or metadata  # the schedule the launcher runs
     winfo = metadata["work_info_flat"].cpu().numpy()
     nw = int(metadata["work_indptr"][-1].item())
     ploc = winfo[: nw * 8].reshape(nw, 8)[:, 1]

@@ -13,7 +13,7 @@ from pathlib import Path
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("PA_FP8_LIB", str(_HERE / "libpa_fp8.so")))
 
-PA_FP8_ABI_VERSION = 6
+PA_FP8_ABI_VERSION = 7
 PA_FP8_BF16, PA_FP8_F16, PA_FP8_F32 = 0, 1, 2
 PA_FP8_CACHE_ELEM, PA_FP8_CACHE_FP8_TENSOR, PA_FP8_CACHE_FP8_TOKEN = 0, 1, 2
 PA_FP8_KV_FLASH, PA_FP8_KV_X_PACKED, PA_FP8_KV_X_TRANS = 0, 1, 2
@@ -202,6 +202,7 @@ class MetadataArgs(ctypes.Structure):
         ("uniform_context", _vp),
         ("bin_groups", _i32),
         ("bin_weight", _i32 * 4),
+        ("partial_count", _vp),
     ]
 
 
@@ -263,6 +264,7 @@ EXPORTED_SYMBOLS = (
     "pa_fp8_decode_worklist",
     "pa_fp8_reduce_v1",
     "pa_fp8_metadata_v1",
+    "pa_fp8_metadata_multi",
     "pa_fp8_rope_cache",
     "pa_fp8_status_string",
     "pa_fp8_abi_version",
@@ -299,6 +301,8 @@ def _load() -> ctypes.CDLL:
     lib.pa_fp8_reduce_v1.restype = ctypes.c_int
     lib.pa_fp8_metadata_v1.argtypes = [ctypes.POINTER(MetadataArgs), _vp]
     lib.pa_fp8_metadata_v1.restype = ctypes.c_int
+    lib.pa_fp8_metadata_multi.argtypes = [ctypes.POINTER(MetadataArgs), ctypes.c_int32, _vp]
+    lib.pa_fp8_metadata_multi.restype = ctypes.c_int
     lib.pa_fp8_rope_cache.argtypes = [ctypes.POINTER(RopeCacheArgs), _vp]
     lib.pa_fp8_rope_cache.restype = ctypes.c_int
     lib.pa_fp8_status_string.argtypes = [ctypes.c_int]
@@ -332,6 +336,11 @@ def reduce_v1(args: ReduceV1Args, stream: int) -> None:
 
 def metadata_v1(args: MetadataArgs, stream: int) -> None:
     check("pa_fp8_metadata_v1", LIB.pa_fp8_metadata_v1(ctypes.byref(args), _vp(stream)))
+
+
+def metadata_multi(args, stream: int) -> None:
+    """Several schedules in one launch: ``args`` is a ctypes array of MetadataArgs."""
+    check("pa_fp8_metadata_multi", LIB.pa_fp8_metadata_multi(args, len(args), _vp(stream)))
 
 
 def rope_cache(args: RopeCacheArgs, stream: int) -> None:

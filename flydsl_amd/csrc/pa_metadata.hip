@@ -24,6 +24,7 @@ struct MetaParams {
     int32_t *reduce_partial_map;
     int32_t *partition_indptr;  // optional outputs
     int32_t *uniform_context;
+    int32_t *partial_count;     // reduce_indptr[nb]: split partials of the schedule
     int32_t nb, gqa, nhk, num_cu, kv_gran, ql, max_work, max_split_tiles;
     int32_t bin_groups;      // > 1: weighted quotas over this many equal groups of each head's bins
     int32_t bin_weight[4];   // weight of group g (bins [g*nspk/G, (g+1)*nspk/G) of every head)
@@ -37,9 +38,16 @@ constexpr int kStagedIndptr = 4097;    // work_indptr entries kept in LDS (num_c
 constexpr int kStagedReduce = 2048;    // batches whose reduce maps are kept in LDS
 constexpr int kStagedSplits = 4096;    // reduce_partial_map entries kept in LDS
 
+constexpr int kMaxSchedules = 4;       // schedules one launch computes (one workgroup each)
 constexpr int kParThreads = 1024;
 constexpr int kParBatches = 4 * kParThreads;         // batches the parallel scheduler handles
+constexpr int kParBins = 4096;                       // bins per head the weighted quota table holds
 constexpr int32_t kSerialSentinel = INT32_MIN + 7;   // work_indptr[0]: "the serial scheduler runs"
+
+// The schedules of one launch: workgroup i of each kernel computes p[i].
+struct MetaSchedules {
+    MetaParams p[kMaxSchedules];
+};
 
 // Exclusive prefix of one value per thread over the 1024 threads; *total gets the sum.
 template <class T>
@@ -82,12 +90,17 @@ __device__ __forceinline__ T block_scan_excl(T v, T *s_wave, T &total) {
 // bin c takes Qs(c) = floor(S * Wc(c) / Wt), Wc(c) the weights of the bins before
 // it.  Every head keeps the same schedule, so the reduce maps are unchanged in
 // form.  The weights apply when every bin still gets at least one partition
-// (S >= 4 * nspk); otherwise the even split is used.
-__global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const MetaParams p) {
+// (S >= 4 * nspk and S * min weight >= 2 * Wt) and a head has at most kParBins
+// bins; otherwise the even split is used.
+// Workgroup i computes schedule sched.p[i] (one launch can hold several).
+__global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const MetaSchedules sched) {
+    const MetaParams &p = sched.p[blockIdx.x];
     __shared__ int32_t s_P[kParBatches + 1];  // partitions before batch b
     __shared__ int32_t s_W[kParBatches + 1];  // works of head 0 before batch b
     __shared__ int32_t s_L[kParBatches + 1];  // works of split batches before batch b
     __shared__ int32_t s_G[kParBatches + 1];  // split batches before batch b
+    __shared__ int32_t s_F[kParBatches];      // first bin of batch b
+    __shared__ int32_t s_Q[kParBins + 1];     // weighted quotas: first partition of bin c
     __shared__ long long s_w64[kParThreads / 64];
     __shared__ int32_t s_w32[kParThreads / 64];
     __shared__ int32_t s_mm[2 * (kParThreads / 64)];
@@ -163,41 +176,53 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
     const int avg = S / nspk, rem = S % nspk;
     const int big = rem * (avg + 1);
     const int ng = p.bin_groups;
-    const bool weighted = ng > 1 && ng <= 4 && nspk % ng == 0 && (long long)S >= 4LL * nspk;
-    const int gm = weighted ? nspk / ng : 1;
-    long long wt = 0;
-    for (int g = 0; g < (weighted ? ng : 0); ++g) wt += p.bin_weight[g] * (long long)gm;
-    auto wc = [&](int c) {  // weights of the bins before c
-        long long a = 0;
-        for (int g = 0; g < ng; ++g) a += p.bin_weight[g] * (long long)min(max(c - g * gm, 0), gm);
-        return a;
-    };
-    auto Qs = [&](int c) { return weighted ? (int)(S64 * wc(c) / wt) : c * avg + min(c, rem); };
-    auto bin_of = [&](int x) {
+    // Weighted quotas apply when every bin keeps at least one partition: S >= 4 nspk
+    // and S * (least weight) >= 2 * Wt (a bin's quota is at least S w / Wt - 1).
+    bool weighted = ng > 1 && ng <= 4 && nspk % ng == 0 && (long long)S >= 4LL * nspk && nspk <= kParBins;
+    long long wt = 0, wmin = 1000;
+    if (weighted) {
+        for (int g = 0; g < ng; ++g) {
+            wt += p.bin_weight[g] * (long long)(nspk / ng);
+            wmin = min(wmin, (long long)p.bin_weight[g]);
+        }
+        weighted = S64 * wmin >= 2 * wt;
+    }
+    // The first partition of every bin, Qs(c) = floor(S * Wc(c) / Wt), tabulated once
+    // in LDS (bins are then found by a binary search over the table).
+    if (weighted) {
+        const int gm = nspk / ng;
+        for (int c = t; c <= nspk; c += kParThreads) {
+            long long wc = 0;  // weights of the bins before c
+            for (int g = 0; g < ng; ++g) wc += p.bin_weight[g] * (long long)min(max(c - g * gm, 0), gm);
+            s_Q[c] = (int)(S64 * wc / wt);
+        }
+        __syncthreads();
+    }
+    auto Qs = [&](int c) { return weighted ? s_Q[c] : c * avg + min(c, rem); };
+    auto bin_of = [&](int x) {  // the bin holding global partition x
         if (!weighted) return nspk == 1 ? 0 : (x < big ? x / (avg + 1) : rem + (x - big) / avg);
         int lo = 0, hi = nspk - 1;  // last bin whose first partition is <= x
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (Qs(mid) <= x) lo = mid;
+            if (s_Q[mid] <= x) lo = mid;
             else hi = mid - 1;
         }
         return lo;
     };
-    auto first_bin = [&](int b) {
-        const int pb = s_P[b], pe = s_P[b + 1];
-        return pe > pb ? bin_of(pb) : (pb == 0 ? 0 : bin_of(pb - 1));
-    };
-    auto works_of = [&](int b) {
-        const int pb = s_P[b], pe = s_P[b + 1];
-        return pe > pb ? bin_of(pe - 1) - bin_of(pb) + 1 : 1;
-    };
-    // works, split works and split batches before each batch
+    // first bin and works of each batch, then the works, split works and split
+    // batches before each batch (block scans)
     int w4[4], l4[4], g4[4];
     int wl = 0, ll = 0, gl = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int b = 4 * t + i;
-        const int nw = b < p.nb ? works_of(b) : 0;
+        int nw = 0;
+        if (b < p.nb) {
+            const int pb = s_P[b], pe = s_P[b + 1];
+            const int fb = pe > pb ? bin_of(pb) : (pb == 0 ? 0 : bin_of(pb - 1));
+            nw = pe > pb ? bin_of(pe - 1) - fb + 1 : 1;
+            s_F[b] = fb;
+        }
         w4[i] = nw;
         l4[i] = nw > 1 ? nw : 0;
         g4[i] = nw > 1 ? 1 : 0;
@@ -222,12 +247,13 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
         gr += g4[i];
     }
     __syncthreads();
+    auto works_of = [&](int b) { return s_W[b + 1] - s_W[b]; };
     const bool overflow = (long long)p.nhk * W > p.max_work || Lt > p.max_split_tiles;
 
     // work_info rows of every head
     for (int b = t; b < p.nb; b += kParThreads) {
         const int pb = s_P[b], pe = s_P[b + 1];
-        const int c0 = first_bin(b), nw = works_of(b);
+        const int c0 = s_F[b], nw = works_of(b);
         const int wb = s_W[b], lb = s_L[b];
         const int qs = p.sq[b], qe = p.sq[b + 1];
         for (int j = 0; j < nw; ++j) {
@@ -253,10 +279,10 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
             int lo = 0, hi = p.nb - 1;  // last batch whose first bin is <= c (batch 0's is 0)
             while (lo < hi) {
                 const int mid = (lo + hi + 1) >> 1;
-                if (first_bin(mid) <= c) lo = mid;
+                if (s_F[mid] <= c) lo = mid;
                 else hi = mid - 1;
             }
-            v = s_W[lo] + min(c - first_bin(lo) + 1, works_of(lo));
+            v = s_W[lo] + min(c - s_F[lo] + 1, works_of(lo));
         }
         for (int k = 0; k < p.nhk; ++k) p.work_indptr[k * nspk + c + 1] = k * W + v;
     }
@@ -274,6 +300,7 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
     for (int i = G + t; i <= p.nb; i += kParThreads) p.reduce_indptr[i] = Lt;
     if (t == 0) {
         if (G > 0) p.reduce_indptr[0] = 0;
+        if (p.partial_count) p.partial_count[0] = Lt;
         p.work_indptr[0] = overflow ? -1 : 0;
     }
 }
@@ -285,7 +312,8 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
 // counts and qo offsets are staged in LDS first (and the counts summed by all
 // lanes).  Buffers larger than the LDS copies are written to global memory
 // directly by lane 0.
-__global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaParams p) {
+__global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaSchedules sched) {
+    const MetaParams &p = sched.p[blockIdx.x];
     if (p.work_indptr[0] != kSerialSentinel) return;  // the parallel scheduler wrote the schedule
     __shared__ int32_t s_np[kStagedBatches];
     __shared__ int32_t s_sq[kStagedBatches + 1];
@@ -473,12 +501,12 @@ __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaParams p) 
     if (rpm_lds)
         for (int i = lane; i < min(lri + 1, p.max_split_tiles); i += 64) p.reduce_partial_map[i] = s_rpm[i];
     __syncthreads();
+    if (lead && p.partial_count) p.partial_count[0] = lri;
     if (lead && overflow) p.work_indptr[0] = -1;
 }
 
-}  // namespace
-
-extern "C" int pa_fp8_metadata_v1(const pa_fp8_metadata_args *a, void *stream) {
+// Checks one schedule's arguments and fills its kernel parameters.
+int meta_params(const pa_fp8_metadata_args *a, MetaParams &p) {
     if (!a) return PA_FP8_ERR_NULL_POINTER;
     if (a->num_batches < 0 || a->gqa <= 0 || a->num_heads_k <= 0 || a->num_cu <= 0 || a->query_length <= 0)
         return PA_FP8_ERR_SHAPE;
@@ -493,7 +521,6 @@ extern "C" int pa_fp8_metadata_v1(const pa_fp8_metadata_args *a, void *stream) {
         for (int g = 0; g < a->bin_groups; ++g)
             if (a->bin_weight[g] < 1 || a->bin_weight[g] > 1000) return PA_FP8_ERR_SHAPE;
     }
-    MetaParams p;
     p.sq = a->seqlens_qo_indptr;
     p.ctx = a->context_lens;
     p.work_indptr = a->work_indptr;
@@ -511,13 +538,31 @@ extern "C" int pa_fp8_metadata_v1(const pa_fp8_metadata_args *a, void *stream) {
     p.max_split_tiles = a->max_split_tiles;
     p.partition_indptr = a->partition_indptr;
     p.uniform_context = a->uniform_context;
+    p.partial_count = a->partial_count;
     p.bin_groups = a->bin_groups;
     for (int g = 0; g < 4; ++g) p.bin_weight[g] = a->bin_weight[g];
+    return PA_FP8_OK;
+}
+
+}  // namespace
+
+extern "C" int pa_fp8_metadata_multi(const pa_fp8_metadata_args *args, int32_t count, void *stream) {
+    if (!args) return PA_FP8_ERR_NULL_POINTER;
+    if (count < 1 || count > kMaxSchedules) return PA_FP8_ERR_SHAPE;
+    MetaSchedules sched = {};
+    for (int i = 0; i < count; ++i) {
+        const int st = meta_params(&args[i], sched.p[i]);
+        if (st != PA_FP8_OK) return st;
+    }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(pa_metadata_par_kernel, dim3(1), dim3(kParThreads), 0, s, p);
+    hipLaunchKernelGGL(pa_metadata_par_kernel, dim3(count), dim3(kParThreads), 0, s, sched);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return PA_FP8_ERR_HIP + (int)err;
-    hipLaunchKernelGGL(pa_metadata_v1_kernel, dim3(1), dim3(64), 0, s, p);
+    hipLaunchKernelGGL(pa_metadata_v1_kernel, dim3(count), dim3(64), 0, s, sched);
     err = hipGetLastError();
     return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
+}
+
+extern "C" int pa_fp8_metadata_v1(const pa_fp8_metadata_args *a, void *stream) {
+    return pa_fp8_metadata_multi(a, 1, stream);
 }

@@ -32,6 +32,7 @@ KV_COMPUTE_BLOCK = 256  # tokens per context partition (kernels/pa_decode_fp8.py
 # (ql * g > 32: three waves per SIMD, a 52.5 KiB ring each).
 _PA_METADATA_GRID_OVERSUB = 2
 _PA_METADATA_GRID_OVERSUB_STAGED = 3
+_REFERENCE_BINS_PER_CU = 3  # the reference's _PA_METADATA_GRID_OVERSUB (kernels/pa_decode_fp8.py:37-40)
 
 
 # Quota weights of the bin groups, first-dispatched group first.  Workgroups that
@@ -361,6 +362,7 @@ def _partitioned_plan(
             f"and `temporary_output` for the {path_name} path."
         )
     output_5d = output.view(batch_size, query_length, num_kv_heads, query_group_size, head_size)
+    given_es, given_ml, given_to = exp_sums is not None, max_logits is not None, temporary_output is not None
     direct = max_parts == 1
     if direct:
         # one slot per sequence: the partition kernel writes the output itself
@@ -374,6 +376,8 @@ def _partitioned_plan(
         if temporary_output is None:
             temporary_output = torch.empty(shape + (head_size,), device=dev, dtype=torch.bfloat16)
         _check_intermediates(exp_sums, max_logits, temporary_output, shape, head_size)
+    own = tuple(t for t, given in ((exp_sums, given_es), (max_logits, given_ml), (temporary_output, given_to))
+                if t is not None and not given)
     dargs = _decode_args(
         query=query,
         key_cache=_u8(key_cache),
@@ -404,12 +408,13 @@ def _partitioned_plan(
         rargs = None
     else:
         rargs = _reduce_args(output_5d, exp_sums, max_logits, temporary_output, max_parts, out_dtype)
-    return _Plan(tag, (exp_sums, max_logits, temporary_output, key_scale, value_scale), max_parts, dargs=dargs,
-                 rargs=rargs)
+    return _Plan(tag, own, max_parts, dargs=dargs, rargs=rargs)
 
 
 _METADATA_KEYS = ("work_indptr", "work_info_flat", "partition_indptr", "reduce_indptr", "reduce_final_map",
                   "reduce_partial_map", "partial_output", "partial_lse")
+_SCHEDULE_KEYS = ("work_indptr", "work_info_flat", "reduce_indptr", "reduce_final_map", "reduce_partial_map",
+                  "partial_output", "partial_lse", "num_sm")
 
 
 def _worklist_plan(
@@ -445,25 +450,28 @@ def _worklist_plan(
     _check_int32("kv_indptr", kv_indptr, 1)
     if kv_indptr.shape[0] != batch_size + 1 or not kv_indptr.is_contiguous() or not kv_page_indices.is_contiguous():
         raise ValueError(f"kv_indptr must be a contiguous [{batch_size + 1}] tensor and kv_page_indices contiguous")
-    cacheable = True
+    own = None  # metadata the launcher built itself (kept alive by the plan, which is not cached)
     if metadata is None:
         if is_graph_capturing:
             raise ValueError(
                 "CUDA graph capture requires precomputed `metadata`; "
                 "call `get_pa_metadata()` before capture and pass it via `metadata=`."
             )
-        metadata = get_pa_metadata(query, key_cache, context_lengths, kv_indptr, num_query_heads, num_kv_heads)
-        cacheable = False
+        metadata = own = get_pa_metadata(query, key_cache, context_lengths, kv_indptr, num_query_heads, num_kv_heads)
     missing = [k for k in _METADATA_KEYS + ("num_sm",) if k not in metadata]
     if missing:
         raise ValueError(f"metadata is missing {missing}; build it with get_pa_metadata()")
-    num_sm = int(metadata["num_sm"])
-    work_indptr, work_info = metadata["work_indptr"], metadata["work_info_flat"]
+    # get_pa_metadata's own schedule for this kernel when present, else the reference's
+    sched = metadata.get("tuned") or metadata
+    missing = [k for k in _SCHEDULE_KEYS if k not in sched]
+    if missing:
+        raise ValueError(f"metadata['tuned'] is missing {missing}; build it with get_pa_metadata()")
+    num_sm = int(sched["num_sm"])
+    work_indptr, work_info = sched["work_indptr"], sched["work_info_flat"]
     partition_indptr = metadata["partition_indptr"]
-    po, pl = metadata["partial_output"], metadata["partial_lse"]
-    for name in ("work_indptr", "work_info_flat", "partition_indptr", "reduce_indptr", "reduce_final_map",
-                 "reduce_partial_map"):
-        t = metadata[name]
+    po, pl = sched["partial_output"], sched["partial_lse"]
+    for name, t in [(k, sched[k]) for k in ("work_indptr", "work_info_flat", "reduce_indptr", "reduce_final_map",
+                                          "reduce_partial_map")] + [("partition_indptr", partition_indptr)]:
         if t.dtype != torch.int32 or not t.is_contiguous() or t.device != dev:
             raise ValueError(f"metadata[{name!r}] must be a contiguous int32 tensor on {dev}")
     if work_indptr.numel() != num_sm + 1 or work_info.numel() % 8 != 0:
@@ -492,7 +500,7 @@ def _worklist_plan(
     w.kv_page_indices = kv_page_indices.data_ptr()
     w.kv_indptr = kv_indptr.data_ptr()
     w.partition_indptr = partition_indptr.data_ptr()
-    w.bin_groups = int(metadata.get("bin_groups", 0))  # the schedule's quota groups, by dispatch round
+    w.bin_groups = int(sched.get("bin_groups", 0))  # the schedule's quota groups, by dispatch round
     w.stride_q_seq, w.stride_q_head = query.stride(0), query.stride(1)
     w.stride_k_block, w.stride_k_head = key_cache.stride(0), key_cache.stride(1)
     w.stride_v_block, w.stride_v_head = value_cache.stride(0), value_cache.stride(1)
@@ -519,17 +527,25 @@ def _worklist_plan(
     # no partial rows past the first query_length: nothing was split, so there is nothing to merge
     v = None
     if po.shape[0] > query_length:
-        v = _reduce_v1_args(po[query_length:], pl[query_length:], metadata["reduce_indptr"],
-                            metadata["reduce_final_map"], metadata["reduce_partial_map"], query_length, output)
-    keep = (metadata, key_scale, value_scale, kv_page_indices, kv_indptr)
-    return _Plan("ps_split_reduce", keep, wargs=w, vargs=v, cacheable=cacheable)
+        v = _reduce_v1_args(po[query_length:], pl[query_length:], sched["reduce_indptr"],
+                            sched["reduce_final_map"], sched["reduce_partial_map"], query_length, output)
+    # A cached plan holds pointers only: every caller tensor it reads is part of the
+    # cache key (pointer, shape, strides), so a later call hits the plan only with
+    # tensors at the same addresses; it keeps nothing of the caller alive.
+    return _Plan("ps_split_reduce", (own,), wargs=w, vargs=v, cacheable=own is None)
 
 
 def _mkey(metadata):
     if metadata is None:
         return None
-    return tuple((k, _tkey(metadata[k])) for k in _METADATA_KEYS if k in metadata) + (
-        ("num_sm", metadata.get("num_sm")), ("bin_groups", metadata.get("bin_groups")))
+
+    def one(d):
+        return tuple((k, _tkey(d[k])) for k in _METADATA_KEYS if k in d) + (
+            ("num_sm", d.get("num_sm")), ("bin_groups", d.get("bin_groups")))
+
+    t = metadata.get("tuned")
+    return one(metadata) + (("uniform_context", bool(metadata.get("uniform_context", False))),
+                            ("tuned", one(t) if t else None))
 
 
 def pa_decode_ps_launch(
@@ -632,8 +648,34 @@ def _build_plan(
     num_kv_heads = key_cache.shape[1]
     query_input_dtype = _get_query_input_dtype(query)
     dev = query.device
+    given_scales = (key_scale, value_scale)
     key_scale = _prepare_scale_tensor("key_scale", key_scale, device=dev, is_graph_capturing=is_graph_capturing)
     value_scale = _prepare_scale_tensor("value_scale", value_scale, device=dev, is_graph_capturing=is_graph_capturing)
+    # Scales the launcher made itself: a float becomes a new tensor of that value
+    # (the cache key holds the value), a tensor of another device or dtype a
+    # converted copy, which must not be reused once the caller's tensor changes.
+    made = tuple(s for s, g in zip((key_scale, value_scale), given_scales) if s is not g)
+    copied = any(isinstance(g, torch.Tensor) and s is not g for s, g in zip((key_scale, value_scale), given_scales))
+    plan = _build_plan_checked(
+        output, query, key_cache, value_cache, context_lengths, softmax_scale, key_scale, value_scale,
+        sliding_window, block_tables, max_context_partition_num, exp_sums, max_logits, temporary_output,
+        is_graph_capturing, query_input_dtype, kv_page_indices, kv_indptr, metadata,
+    )
+    if made:
+        plan.keepalive = tuple(plan.keepalive) + made
+    if copied:
+        plan.cacheable = False
+    return plan
+
+
+def _build_plan_checked(
+    output, query, key_cache, value_cache, context_lengths, softmax_scale, key_scale, value_scale,
+    sliding_window, block_tables, max_context_partition_num, exp_sums, max_logits, temporary_output,
+    is_graph_capturing, query_input_dtype, kv_page_indices, kv_indptr, metadata,
+) -> _Plan:
+    num_query_heads = query.shape[1]
+    num_kv_heads = key_cache.shape[1]
+    dev = query.device
     if query_input_dtype == "packed_fp8":
         raise ValueError(
             "`pa_decode_ps_launch` no longer accepts host query_scale and only supports "
@@ -703,9 +745,14 @@ def _build_plan(
         raise ValueError("block_tables must be [num_seqs, max_blocks] on the query device with a unit last stride")
 
     if max_context_partition_num == 0:
-        max_context_partition_num = _auto_partitions(
-            dev, batch_size, num_kv_heads, block_tables.shape[1] * block_size, sliding_window, query_length
-        )
+        if exp_sums is not None:
+            # the caller sized the partials: the reference sizes them with
+            # get_recommended_splits and launches that many slots (:2890-2896, :3024-3029)
+            max_context_partition_num = exp_sums.shape[2] if exp_sums.dim() == 4 else 0
+        else:
+            max_context_partition_num = _auto_partitions(
+                dev, batch_size, num_kv_heads, block_tables.shape[1] * block_size, sliding_window, query_length
+            )
     if max_context_partition_num < 1 or max_context_partition_num > 65535:
         raise ValueError(f"max_context_partition_num={max_context_partition_num} out of range [1, 65535]")
     if sliding_window > 0:
@@ -737,6 +784,37 @@ def _seqlens_qo_indptr(dev: torch.device, batch_size: int, query_length: int, gr
     return t
 
 
+def _schedule_layout(batch_size: int, num_kv_heads: int, num_sm: int) -> list:
+    """int32 element counts of one schedule's buffers: work_indptr, work_info (flat),
+    reduce_indptr, reduce_final_map (flat), reduce_partial_map."""
+    infos = get_pa_metadata_info_v1(batch_size, num_kv_heads, num_cu=num_sm)
+    return [int(torch.Size(shape).numel()) for shape, _ in infos[1:]]
+
+
+def _schedule_args(a, bufs, seqlens_qo_indptr, ctx, batch_size, gqa, num_kv_heads, num_sm, partition_size,
+                   query_length, bin_groups, partial_count):
+    work_indptr, work_info, reduce_indptr, reduce_final_map, reduce_partial_map = bufs
+    a.seqlens_qo_indptr = seqlens_qo_indptr.data_ptr()
+    a.context_lens = ctx.data_ptr()
+    a.work_indptr = work_indptr.data_ptr()
+    a.work_info = work_info.data_ptr()
+    a.reduce_indptr = reduce_indptr.data_ptr()
+    a.reduce_final_map = reduce_final_map.data_ptr()
+    a.reduce_partial_map = reduce_partial_map.data_ptr()
+    a.partial_count = partial_count.data_ptr()
+    a.num_batches = batch_size
+    a.gqa = gqa
+    a.num_heads_k = num_kv_heads
+    a.num_cu = num_sm
+    a.kv_granularity = partition_size
+    a.query_length = query_length
+    a.max_work = work_info.numel() // 8
+    a.max_split_tiles = reduce_partial_map.numel()
+    a.bin_groups = bin_groups
+    for g, wgt in enumerate(_BIN_WEIGHTS.get(bin_groups, ())):
+        a.bin_weight[g] = wgt
+
+
 def get_pa_metadata(
     query: torch.Tensor,
     key_cache: torch.Tensor,
@@ -747,20 +825,29 @@ def get_pa_metadata(
     partition_size: int = KV_COMPUTE_BLOCK,
     *,
     graph_safe: bool = None,
+    tuned: bool = True,
 ):
     """Worklist metadata for the persistent decode (kernels/pa_decode_fp8.py:1729-1859).
 
-    Runs the device scheduler ``get_pa_metadata_v1`` over
-    ``num_sm = (CUs * n // kv_heads) * kv_heads`` bins, n the worklist kernel's
-    workgroups per CU (2, or 3 for the LDS-staged kernel that query_length *
-    num_query_heads / num_kv_heads > 32 selects); work_info kv ranges are cumulative
+    The keys the reference returns hold the reference's schedule, byte for byte:
+    ``get_pa_metadata_v1`` over ``num_sm = (CUs * 3 // kv_heads) * kv_heads`` bins
+    with even quotas (:1764-1771), ``partition_indptr`` and the partial buffers
+    sized for its split partials.  work_info kv ranges are cumulative
     ``partition_size``-token partition indices.
 
-    By default it synchronises once on ``reduce_indptr[-1]`` to size the partial
-    buffers, as the reference does (:1832).  With ``graph_safe`` (the default
-    while the current stream is being captured into a graph) it reads nothing
-    back: the partial buffers are sized for the scheduler's bound on split
-    partials (``reduce_partial_map``'s length, kernels/pa_metadata.py:66-72), and
+    With ``tuned`` (the default) the dict also holds ``"tuned"``: this build's
+    schedule for its worklist kernel, which ``pa_decode_ps_launch`` runs when
+    present -- one bin per resident workgroup (2 per CU for the register-streaming
+    kernel, 3 for the LDS-staged one that query_length * num_query_heads /
+    num_kv_heads > 32 selects) with quotas weighted by dispatch round
+    (``bin_groups``, ``bin_weight``), and its own partial buffers.  Both schedules
+    come from one scheduler launch.
+
+    By default it synchronises once to size the partial buffers, as the reference
+    does on ``reduce_indptr[-1]`` (:1832).  With ``graph_safe`` (the default while
+    the current stream is being captured into a graph) it reads nothing back: the
+    partial buffers are sized for the scheduler's bound on split partials
+    (``reduce_partial_map``'s length, kernels/pa_metadata.py:66-72), and
     ``uniform_context`` is False.  Everything it launches is then capturable, so a
     graph can hold the schedule and the decode together and be replayed over new
     context lengths.  The reference's ``get_pa_metadata`` cannot be captured.
@@ -771,83 +858,86 @@ def get_pa_metadata(
     batch_size = context_lengths.shape[0]
     query_length = query.shape[0] // batch_size
     head_size = query.shape[-1]
-    bins_per_cu = _metadata_bins_per_cu(query_length, num_query_heads // num_kv_heads)
-    num_sm = _device_cu_count(dev) * bins_per_cu
-    num_sm = (num_sm // num_kv_heads) * num_kv_heads
+    gqa = num_query_heads // num_kv_heads
+    cus = _device_cu_count(dev)
+    num_sm = (cus * _REFERENCE_BINS_PER_CU // num_kv_heads) * num_kv_heads  # kernels/pa_decode_fp8.py:1769-1771
     if num_sm <= 0 or partition_size <= 0 or partition_size & (partition_size - 1):
-        raise ValueError(f"get_pa_metadata needs num_kv_heads <= {bins_per_cu} * CUs and a power-of-two partition_size")
+        raise ValueError(
+            f"get_pa_metadata needs num_kv_heads <= {_REFERENCE_BINS_PER_CU} * CUs and a power-of-two partition_size"
+        )
+    schedules = [(num_sm, 0)]
+    if tuned:
+        bins_per_cu = _metadata_bins_per_cu(query_length, gqa)
+        t_sm = (cus * bins_per_cu // num_kv_heads) * num_kv_heads
+        # quotas weighted by dispatch round, when every round holds whole groups of bins
+        # and the parallel scheduler runs (the serial one, past 4096 batches, splits evenly)
+        t_groups = bins_per_cu if (t_sm == cus * bins_per_cu and t_sm % (bins_per_cu * num_kv_heads) == 0
+                                   and batch_size <= 4096 and bins_per_cu in _BIN_WEIGHTS) else 0
+        if t_sm <= 0:
+            tuned = False
+        else:
+            schedules.append((t_sm, t_groups))
     seqlens_qo_indptr = _seqlens_qo_indptr(dev, batch_size, query_length, graph_safe)
     ctx = context_lengths if context_lengths.dtype == torch.int32 else context_lengths.to(torch.int32)
     ctx = ctx.contiguous()
-    infos = get_pa_metadata_info_v1(batch_size, num_kv_heads, num_cu=num_sm)
-    # every int32 output in one allocation; uniform_context sits right after
-    # reduce_indptr so that one two-int read returns it with the partial count
-    sizes = [int(torch.Size(shape).numel()) for shape, _ in infos[1:]]  # work_indptr .. reduce_partial_map
-    sizes[2] += 1  # reduce_indptr + uniform_context
+    # Every int32 output in one allocation: four counters first (the reference
+    # schedule's split partials, uniform_context, the tuned schedule's split
+    # partials), so one three-int read returns what the host needs; then each
+    # schedule's buffers and partition_indptr, in 16-byte aligned pieces.
+    sizes = [4]
+    for s_sm, _ in schedules:
+        sizes += _schedule_layout(batch_size, num_kv_heads, s_sm)
     sizes.append(batch_size + 1)  # partition_indptr
     offs = [0]
     for n in sizes:
-        offs.append(offs[-1] + (n + 3) // 4 * 4)  # 16-byte aligned pieces
+        offs.append(offs[-1] + (n + 3) // 4 * 4)
     buf = torch.empty(offs[-1], dtype=torch.int32, device=dev)
-    work_indptr = buf[offs[0] : offs[0] + sizes[0]]
-    work_info_flat = buf[offs[1] : offs[1] + sizes[1]]
-    reduce_indptr = buf[offs[2] : offs[2] + batch_size + 1]
-    reduce_final_map = buf[offs[3] : offs[3] + sizes[3]].view(batch_size, 2)
-    reduce_partial_map = buf[offs[4] : offs[4] + sizes[4]]
-    partition_indptr = buf[offs[5] : offs[5] + sizes[5]]
-    a = _lib.MetadataArgs()
-    a.seqlens_qo_indptr = seqlens_qo_indptr.data_ptr()
-    a.context_lens = ctx.data_ptr()
-    a.work_indptr = work_indptr.data_ptr()
-    a.work_info = work_info_flat.data_ptr()
-    a.reduce_indptr = reduce_indptr.data_ptr()
-    a.reduce_final_map = reduce_final_map.data_ptr()
-    a.reduce_partial_map = reduce_partial_map.data_ptr()
-    a.partition_indptr = partition_indptr.data_ptr()
-    a.uniform_context = buf[offs[2] + batch_size + 1 :].data_ptr()
-    # quotas weighted by dispatch round, when every round holds whole groups of bins
-    # and the parallel scheduler runs (the serial one, past 4096 batches, splits evenly)
-    bin_groups = bins_per_cu if (num_sm % (bins_per_cu * num_kv_heads) == 0 and batch_size <= 4096
-                                 and num_sm == _device_cu_count(dev) * bins_per_cu) else 0
-    if bin_groups in _BIN_WEIGHTS:
-        a.bin_groups = bin_groups
-        for g, wgt in enumerate(_BIN_WEIGHTS[bin_groups]):
-            a.bin_weight[g] = wgt
-    else:
-        bin_groups = 0
-    a.num_batches = batch_size
-    a.gqa = num_query_heads // num_kv_heads
-    a.num_heads_k = num_kv_heads
-    a.num_cu = num_sm
-    a.kv_granularity = partition_size
-    a.query_length = query_length
-    a.max_work = sizes[1] // 8
-    a.max_split_tiles = sizes[4]
-    _lib.metadata_v1(a, torch.cuda.current_stream(dev).cuda_stream)
+    piece = [buf[offs[k]: offs[k] + sizes[k]] for k in range(len(sizes))]
+    counts, partition_indptr = piece[0], piece[-1]
+    args = (_lib.MetadataArgs * len(schedules))()
+    sched_bufs = []
+    for k, (s_sm, s_groups) in enumerate(schedules):
+        bufs = piece[1 + 5 * k: 6 + 5 * k]
+        _schedule_args(args[k], bufs, seqlens_qo_indptr, ctx, batch_size, gqa, num_kv_heads, s_sm, partition_size,
+                       query_length, s_groups, counts[2 * k: 2 * k + 1])
+        sched_bufs.append(bufs)
+    # the first schedule also writes the derived per-batch values
+    args[0].partition_indptr = partition_indptr.data_ptr()
+    args[0].uniform_context = counts[1:2].data_ptr()
+    _lib.metadata_multi(args, torch.cuda.current_stream(dev).cuda_stream)
     if graph_safe:
-        # no host read: room for every partial the schedule can emit
-        num_partials, uniform = reduce_partial_map.numel(), False
+        # no host read: room for every partial a schedule can emit
+        nparts = [int(b[4].numel()) for b in sched_bufs]
+        uniform = False
     else:
-        # one host read (the reference reads reduce_indptr[-1] here too): the partial
-        # count, and whether every sequence has the same context length
-        host = buf[offs[2] + batch_size : offs[2] + batch_size + 2].cpu()
-        num_partials, uniform = int(host[0]), bool(host[1])
-    partial_output = torch.empty(
-        ((num_partials + 1) * query_length, 1, num_query_heads, head_size), dtype=torch.float32, device=dev
-    )
-    partial_lse = torch.empty(((num_partials + 1) * query_length, 1, num_query_heads, 1), dtype=torch.float32, device=dev)
-    return {
-        "work_indptr": work_indptr,
-        "work_info_flat": work_info_flat,
+        # one host read (the reference reads reduce_indptr[-1] here too): the split
+        # partial counts and whether every sequence has the same context length
+        host = counts[:3].cpu().tolist()
+        nparts = [host[0], host[2]][: len(schedules)]
+        uniform = bool(host[1])
+
+    def partials(n):
+        rows = (n + 1) * query_length
+        return (torch.empty((rows, 1, num_query_heads, head_size), dtype=torch.float32, device=dev),
+                torch.empty((rows, 1, num_query_heads, 1), dtype=torch.float32, device=dev))
+
+    def entry(k):
+        wi, winfo, ri, rfm, rpm = sched_bufs[k]
+        po, pl = partials(nparts[k])
+        return {
+            "work_indptr": wi,
+            "work_info_flat": winfo,
+            "reduce_indptr": ri,
+            "reduce_final_map": rfm.view(batch_size, 2),
+            "reduce_partial_map": rpm,
+            "num_sm": schedules[k][0],
+            "partial_output": po,
+            "partial_lse": pl,
+        }
+
+    md = entry(0)
+    md.update({
         "partition_indptr": partition_indptr,
-        "reduce_indptr": reduce_indptr,
-        "reduce_final_map": reduce_final_map,
-        "reduce_partial_map": reduce_partial_map,
-        "num_sm": num_sm,
-        "bin_groups": bin_groups,
-        "bin_weight": _BIN_WEIGHTS.get(bin_groups),
-        "partial_output": partial_output,
-        "partial_lse": partial_lse,
         "stride_po_partial": query_length * num_query_heads * head_size,
         "stride_pl_partial": query_length * num_query_heads,
         "stride_po_ql": num_query_heads * head_size,
@@ -856,7 +946,13 @@ def get_pa_metadata(
         # equal context lengths: fixed partition slots are already balanced, so the
         # small-block path keeps its partition kernel instead of the worklist
         "uniform_context": uniform,
-    }
+    })
+    if tuned:
+        t = entry(1)
+        t["bin_groups"] = schedules[1][1]
+        t["bin_weight"] = _BIN_WEIGHTS.get(schedules[1][1])
+        md["tuned"] = t
+    return md
 
 
 def softmax_scale_for(head_dim: int = HEAD_DIM) -> float:

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define PA_FP8_ABI_VERSION 6
+#define PA_FP8_ABI_VERSION 7
 
 enum pa_fp8_status {
     PA_FP8_OK = 0,
@@ -263,7 +263,8 @@ int pa_fp8_reduce_v1(const pa_fp8_reduce_v1_args *args, void *hip_stream);
  * schedule): the bins of each kv head form G equal groups and the parallel
  * scheduler splits the partitions in proportion to bin_weight[g] (1..1000) of
  * each bin's group instead of evenly, when every bin still gets a partition
- * (sum of partitions >= 4 * bins per head).  Workgroups that share a CU progress
+ * (sum of partitions S >= 4 * bins per head, S * least weight >= 2 * Wt with Wt
+ * the sum of every bin's weight, at most 4096 bins per head).  Workgroups that share a CU progress
  * at different rates (issue arbitration favours the one dispatched first), and
  * pa_fp8_decode_worklist with the same bin_groups runs group a on the
  * workgroups of dispatch round a.
@@ -291,9 +292,19 @@ typedef struct pa_fp8_metadata_args {
     int32_t *uniform_context;
     int32_t bin_groups;
     int32_t bin_weight[4];
+    int32_t *partial_count;      /* optional [1]: reduce_indptr[num_batches], the split partials */
 } pa_fp8_metadata_args;
 
 int pa_fp8_metadata_v1(const pa_fp8_metadata_args *args, void *hip_stream);
+
+/*
+ * `count` (1..4) independent schedules in one launch: schedule i from args[i],
+ * each exactly as pa_fp8_metadata_v1 computes it (one workgroup per schedule, so
+ * they run side by side).  get_pa_metadata computes the reference's schedule and
+ * its own tuned one this way.  No counterpart in the reference, which builds one
+ * schedule per call (kernels/pa_metadata.py:450-524).
+ */
+int pa_fp8_metadata_multi(const pa_fp8_metadata_args *args, int32_t count, void *hip_stream);
 
 /* KV-cache formats written by pa_fp8_rope_cache */
 enum pa_fp8_cache_format {

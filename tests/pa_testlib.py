@@ -166,6 +166,14 @@ def metadata_with_bins(w: Dict, num_cu: int) -> Dict:
     }
 
 
+def schedule_of(md: Dict) -> Dict:
+    """The schedule pa_decode_ps_launch runs for a metadata dict: get_pa_metadata's
+    tuned schedule when present, else the reference's keys."""
+    if md.get("tuned"):
+        return dict(md["tuned"], partition_indptr=md["partition_indptr"])
+    return md
+
+
 def check_worklist_partials(w: Dict, md: Dict) -> int:
     """Every partial row the worklist kernel wrote vs the oracle's per-work
     restatement (oatt.worklist_decode) on the same worklist: the work -> token

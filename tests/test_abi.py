@@ -38,7 +38,8 @@ def declared_functions():
 def test_header_declares_the_expected_api():
     assert declared_functions() == sorted(
         ["pa_fp8_decode_partitions", "pa_fp8_lse_reduce", "pa_fp8_decode_worklist", "pa_fp8_reduce_v1",
-         "pa_fp8_metadata_v1", "pa_fp8_rope_cache", "pa_fp8_status_string", "pa_fp8_abi_version"]
+         "pa_fp8_metadata_v1", "pa_fp8_metadata_multi", "pa_fp8_rope_cache", "pa_fp8_status_string",
+         "pa_fp8_abi_version"]
     )
 
 

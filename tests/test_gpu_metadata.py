@@ -22,18 +22,41 @@ def weighted_quota(weights, nspk):
         return sum(w * min(max(i - g * m, 0), m) for g, w in enumerate(weights))
 
     def quota(i, total):
-        if nspk % ng or total < 4 * nspk:
-            return total // nspk + (1 if i < total % nspk else 0)
         wt = wc(nspk)
+        if nspk % ng or total < 4 * nspk or nspk > 4096 or total * min(weights) < 2 * wt:
+            return total // nspk + (1 if i < total % nspk else 0)
         return total * wc(i + 1) // wt - total * wc(i) // wt
 
     return quota
 
 
 def expected_schedule(md, sq, ctx, gqa, nhk, gran=256, ql=1):
-    """The oracle's schedule for a get_pa_metadata result (weighted or even)."""
+    """The oracle's schedule for one schedule of a get_pa_metadata result (the
+    reference's even one, or the tuned one with its weights)."""
     qf = weighted_quota(md["bin_weight"], md["num_sm"] // nhk) if md.get("bin_groups", 0) > 1 else None
     return op.get_pa_metadata_v1(sq, ctx, gqa, nhk, md["num_sm"], gran, ql, quota_of=qf)
+
+
+def reference_num_sm(nhk):
+    """The reference's bin count (kernels/pa_decode_fp8.py:1764-1771)."""
+    cus = torch.cuda.get_device_properties(torch.device("cuda:0")).multi_processor_count
+    return (cus * 3 // nhk) * nhk
+
+
+def assert_schedule_equal(md, ref, label):
+    """Every byte of the valid prefixes the reference defines."""
+    v = op.metadata_valid_prefixes(ref)
+    np.testing.assert_array_equal(md["work_indptr"].cpu().numpy(), v["work_indptr"], err_msg=label)
+    nw = int(v["work_indptr"][-1])
+    np.testing.assert_array_equal(md["work_info_flat"].cpu().numpy()[: nw * 8].reshape(nw, 8), v["work_info"],
+                                  err_msg=label)
+    np.testing.assert_array_equal(md["reduce_indptr"].cpu().numpy(), v["reduce_indptr"], err_msg=label)
+    ng = len(v["reduce_final_map"])
+    np.testing.assert_array_equal(md["reduce_final_map"].cpu().numpy()[:ng], v["reduce_final_map"], err_msg=label)
+    npart = int(v["reduce_indptr"][-1])
+    np.testing.assert_array_equal(md["reduce_partial_map"].cpu().numpy()[:npart], v["reduce_partial_map"],
+                                  err_msg=label)
+    return v
 
 
 def run_device(ctx, ql, gqa, nhk, num_cu, gran):
@@ -73,48 +96,59 @@ def test_device_scheduler_matches_oracle(seed):
         np.testing.assert_array_equal(op.metadata_valid_prefixes(got)[key], val, err_msg=key)
 
 
-def test_get_pa_metadata_c3_shape():
-    """The host entry point on the ragged benchmark shape (512 bins on 256 CUs)."""
+def _metadata_for(name):
     from flydsl_amd import get_pa_metadata
     from flydsl_amd.workloads import CONFIGS, context_lengths_for
 
-    ctx = context_lengths_for(CONFIGS["c3"])
+    cfg = CONFIGS[name]
+    ctx = context_lengths_for(cfg)
+    b, ql, hq, hk, bs = len(ctx), cfg.query_length, cfg.num_q_heads, cfg.num_kv_heads, cfg.block_size
     dev = torch.device("cuda:0")
-    q = torch.zeros(128, 32, 128, dtype=torch.bfloat16, device=dev)
-    kc = torch.zeros(1, 8, 8, 16, 16, dtype=torch.uint8, device=dev)
+    q = torch.zeros(b * ql, hq, 128, dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros(1, hk, 8, bs, 16, dtype=torch.uint8, device=dev)
     md = get_pa_metadata(q, kc, torch.tensor(ctx, dtype=torch.int32, device=dev),
-                         torch.zeros(129, dtype=torch.int32, device=dev), 32, 8)
-    cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    num_sm = (cus * 2 // 8) * 8  # two bins per CU: two worklist workgroups fit a CU
-    assert md["num_sm"] == num_sm
-    assert md["bin_groups"] == 2 and md["bin_weight"] is not None  # c3's 1749 partitions >= 4 * 64
-    ref = expected_schedule(md, list(range(129)), ctx, 4, 8)
-    v = op.metadata_valid_prefixes(ref)
-    np.testing.assert_array_equal(md["work_indptr"].cpu().numpy(), v["work_indptr"])
-    nw = int(v["work_indptr"][-1])
-    np.testing.assert_array_equal(md["work_info_flat"].cpu().numpy()[: nw * 8].reshape(nw, 8), v["work_info"])
-    np.testing.assert_array_equal(md["reduce_indptr"].cpu().numpy(), v["reduce_indptr"])
+                         torch.zeros(b + 1, dtype=torch.int32, device=dev), hq, hk)
+    return md, ctx, b, ql, hq, hk
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
+def test_get_pa_metadata_reference_keys_are_the_reference_schedule(name):
+    """The keys the reference returns hold the reference's schedule byte for byte:
+    (3 CUs // Hkv) * Hkv bins with even quotas (kernels/pa_decode_fp8.py:1764-1771,
+    kernels/pa_metadata.py:197-206), partial buffers sized by its split count."""
+    md, ctx, b, ql, hq, hk = _metadata_for(name)
+    assert md["num_sm"] == reference_num_sm(hk)
+    ref = op.get_pa_metadata_v1([ql * i for i in range(b + 1)], ctx, hq // hk, hk, md["num_sm"], 256, ql)
+    v = assert_schedule_equal(md, ref, name)
+    npart = int(v["reduce_indptr"][-1])
+    assert md["partial_output"].shape == ((npart + 1) * ql, 1, hq, 128)
+    assert md["partial_lse"].shape == ((npart + 1) * ql, 1, hq, 1)
     parts = (np.asarray(ctx) + 255) // 256
     np.testing.assert_array_equal(md["partition_indptr"].cpu().numpy(), np.concatenate([[0], np.cumsum(parts)]))
+    assert "bin_groups" not in md  # the weights belong to the tuned schedule only
+
+
+def test_get_pa_metadata_c3_tuned_schedule():
+    """The tuned schedule on the ragged benchmark shape: two bins per CU (two
+    register-streaming worklist workgroups fit a CU), quotas weighted by dispatch
+    round, against the oracle's state machine run with the same per-bin quotas."""
+    md, ctx, b, ql, hq, hk = _metadata_for("c3")
+    t = md["tuned"]
+    cus = torch.cuda.get_device_properties(torch.device("cuda:0")).multi_processor_count
+    assert t["num_sm"] == (cus * 2 // 8) * 8
+    assert t["bin_groups"] == 2 and t["bin_weight"] is not None  # c3's 1749 partitions >= 4 * 64
+    v = assert_schedule_equal(t, expected_schedule(t, list(range(129)), ctx, 4, 8), "c3 tuned")
     npart = int(v["reduce_indptr"][-1])
-    assert md["partial_output"].shape == ((npart + 1) * 1, 1, 32, 128)
+    assert t["partial_output"].shape == ((npart + 1) * 1, 1, 32, 128)
 
 
 def test_get_pa_metadata_c5_shape_weighted_quotas():
     """The staged kernel's schedule (three bins per CU) on the c5 shape: quotas
     weighted by dispatch round, against the oracle's state machine run with the
     same per-bin quotas; the first round's bins hold the most partitions."""
-    from flydsl_amd import get_pa_metadata
-    from flydsl_amd.workloads import CONFIGS, context_lengths_for
-
-    ctx = context_lengths_for(CONFIGS["c5"])
-    b, ql, hq, hk = 256, 4, 64, 4
-    dev = torch.device("cuda:0")
-    q = torch.zeros(b * ql, hq, 128, dtype=torch.bfloat16, device=dev)
-    kc = torch.zeros(1, hk, 8, 64, 16, dtype=torch.uint8, device=dev)
-    md = get_pa_metadata(q, kc, torch.tensor(ctx, dtype=torch.int32, device=dev),
-                         torch.zeros(b + 1, dtype=torch.int32, device=dev), hq, hk)
-    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    md, ctx, b, ql, hq, hk = _metadata_for("c5")
+    md = md["tuned"]
+    cus = torch.cuda.get_device_properties(torch.device("cuda:0")).multi_processor_count
     assert md["num_sm"] == (cus * 3 // hk) * hk
     if md["bin_groups"] != 3:
         pytest.skip("the device's CU count does not split into whole groups of bins")
@@ -226,16 +260,43 @@ def test_get_pa_metadata_partition_prefix_and_uniform_flag(b, kind):
     parts = (ctx.astype(np.int64) + 255) // 256
     np.testing.assert_array_equal(md["partition_indptr"].cpu().numpy(), np.concatenate([[0], np.cumsum(parts)]))
     assert md["uniform_context"] is (kind != "ragged" and kind != "last_differs")
-    ref = expected_schedule(md, list(range(b + 1)), [int(c) for c in ctx], 8, 2)
-    v = op.metadata_valid_prefixes(ref)
-    np.testing.assert_array_equal(md["work_indptr"].cpu().numpy(), v["work_indptr"])
-    np.testing.assert_array_equal(md["reduce_indptr"].cpu().numpy(), v["reduce_indptr"])
-    nw = int(v["work_indptr"][-1])
-    np.testing.assert_array_equal(md["work_info_flat"].cpu().numpy()[: nw * 8].reshape(nw, 8), v["work_info"])
-    assert md["partial_output"].shape[0] == int(v["reduce_indptr"][-1]) + 1
-    # graph-safe: same schedule, no host read, partial buffers at the scheduler's bound
+    sq, cl = list(range(b + 1)), [int(c) for c in ctx]
+    for label, s in (("reference", md), ("tuned", md["tuned"])):
+        v = assert_schedule_equal(s, expected_schedule(s, sq, cl, 8, 2), f"{b} {kind} {label}")
+        assert s["partial_output"].shape[0] == int(v["reduce_indptr"][-1]) + 1
+    assert md["num_sm"] == reference_num_sm(2)
+    # graph-safe: same schedules, no host read, partial buffers at the scheduler's bound
     md_g = get_pa_metadata(q, kc, ctx_t, kv, 16, 2, graph_safe=True)
     assert md_g["uniform_context"] is False
     assert torch.equal(md_g["partition_indptr"], md["partition_indptr"])
-    assert torch.equal(md_g["work_indptr"], md["work_indptr"])
-    assert md_g["partial_output"].shape[0] == md_g["reduce_partial_map"].numel() + 1
+    for s_g, s in ((md_g, md), (md_g["tuned"], md["tuned"])):
+        assert torch.equal(s_g["work_indptr"], s["work_indptr"])
+        assert s_g["partial_output"].shape[0] == s_g["reduce_partial_map"].numel() + 1
+    # tuned=False: the reference's dict only
+    md_r = get_pa_metadata(q, kc, ctx_t, kv, 16, 2, tuned=False)
+    assert "tuned" not in md_r and torch.equal(md_r["work_indptr"], md["work_indptr"])
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_get_pa_metadata_random_shapes_both_schedules(seed):
+    """Random batches, heads, query lengths and group sizes: the reference keys
+    against the oracle's even schedule over the reference's bin count, the tuned
+    entry against the oracle run with its weights."""
+    from flydsl_amd import get_pa_metadata
+
+    rng = np.random.default_rng(1000 + seed)
+    hk = int(rng.choice([1, 2, 4, 8]))
+    g = int(rng.choice([1, 4, 8, 16]))
+    ql = int(rng.integers(1, 5))
+    b = int(rng.integers(1, 300))
+    ctx = rng.integers(0, int(rng.choice([600, 9000, 40000])), size=b)
+    dev = torch.device("cuda:0")
+    q = torch.zeros(b * ql, hk * g, 128, dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros(1, hk, 8, 16, 16, dtype=torch.uint8, device=dev)
+    md = get_pa_metadata(q, kc, torch.tensor(ctx, dtype=torch.int32, device=dev),
+                         torch.zeros(b + 1, dtype=torch.int32, device=dev), hk * g, hk)
+    sq, cl = [ql * i for i in range(b + 1)], [int(c) for c in ctx]
+    assert md["num_sm"] == reference_num_sm(hk)
+    for label, s in (("reference", md), ("tuned", md["tuned"])):
+        v = assert_schedule_equal(s, expected_schedule(s, sq, cl, g, hk, ql=ql), f"seed {seed} {label}")
+        assert s["partial_output"].shape[0] == (int(v["reduce_indptr"][-1]) + 1) * ql

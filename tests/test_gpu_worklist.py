@@ -18,7 +18,7 @@ import torch
 
 from flydsl_amd.workloads import CONFIGS, build_workload, scaled
 from oracle import attention as oatt
-from tests.pa_testlib import check_worklist_partials, compare_outputs, launch, metadata_with_bins
+from tests.pa_testlib import check_worklist_partials, compare_outputs, launch, metadata_with_bins, schedule_of
 
 pytestmark = pytest.mark.gpu
 
@@ -81,10 +81,10 @@ def test_dispatch_round_bin_remap_is_a_permutation(name):
     md = get_pa_metadata(w["query"], w["key_cache"], w["context_lengths"], w["kv_indptr"], cfg.num_q_heads,
                          cfg.num_kv_heads)
     md["uniform_context"] = False
-    if md["bin_groups"] <= 1:
+    if md["tuned"]["bin_groups"] <= 1:
         pytest.skip("the device's CU count does not split into whole groups of bins")
     out_remap, _, _ = launch(w, metadata=md)
-    out_plain, _, _ = launch(w, metadata=dict(md, bin_groups=0))
+    out_plain, _, _ = launch(w, metadata=dict(md, tuned=dict(md["tuned"], bin_groups=0)))
     assert torch.equal(out_remap, out_plain)
     compare_outputs(w, out_remap, _spread(cfg.batch, 4))
 
@@ -110,28 +110,31 @@ WORKLIST_CASES = {
 
 
 @pytest.mark.parametrize("case", sorted(WORKLIST_CASES))
-@pytest.mark.parametrize("bins_per_head", [1, 3, 16, 0])
+@pytest.mark.parametrize("bins_per_head", [1, 3, 16, 0, -1])
 def test_worklist_partials_and_outputs(case, bins_per_head):
-    """Ragged shapes over schedules with few bins (many splits) and with
-    get_pa_metadata's own bin count (bins_per_head 0): every output row and
+    """Ragged shapes over schedules with few bins (many splits), with
+    get_pa_metadata's tuned schedule (bins_per_head 0) and with the reference's
+    schedule it returns under the reference's keys (-1): every output row and
     every partial row checked."""
     kw = dict(WORKLIST_CASES[case])
     cfg = scaled(CONFIGS[kw.pop("base")], name=case, **kw)
     print(f"[worklist] {case} bins/head {bins_per_head}", flush=True)
     w = build_workload(cfg, "cuda", seed=7)
-    if bins_per_head:
+    if bins_per_head > 0:
         md = metadata_with_bins(w, bins_per_head * cfg.num_kv_heads)
     else:
         from flydsl_amd import get_pa_metadata
 
         md = get_pa_metadata(w["query"], w["key_cache"], w["context_lengths"], w["kv_indptr"], cfg.num_q_heads,
-                             cfg.num_kv_heads)
-        md["partial_output"].fill_(float("nan"))
-        md["partial_lse"].fill_(float("nan"))
+                             cfg.num_kv_heads, tuned=bins_per_head == 0)
+        md["uniform_context"] = False
+        sched = schedule_of(md)
+        sched["partial_output"].fill_(float("nan"))
+        sched["partial_lse"].fill_(float("nan"))
     out, tag, _ = launch(w, metadata=md)
     assert tag == ("ps_small_block" if cfg.block_size in (16, 64) else "ps_split_reduce")
     compare_outputs(w, out, range(cfg.batch))
-    n = check_worklist_partials(w, md)
+    n = check_worklist_partials(w, schedule_of(md))
     if bins_per_head == 1:
         assert n == 0  # one bin per head holds every sequence whole: direct writes only
     print(f"[worklist] {case}: {n} partial rows checked", flush=True)

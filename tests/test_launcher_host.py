@@ -275,3 +275,112 @@ def test_small_block_with_metadata_runs_the_worklist(bs):
     # the reference's graph-capture rule for this path still holds
     with pytest.raises(ValueError, match="small-block PS path"):
         plan(t, capturing=True)
+
+
+def test_default_partition_count_follows_caller_partials():
+    """max_context_partition_num=0 with caller-sized partials: the reference sizes them
+    with get_recommended_splits and launches that many slots
+    (kernels/pa_decode_fp8.py:3024-3029), so the launcher takes the count from them."""
+    t = make()
+    for parts in (8, 3):
+        shape = (3, 2, parts, 4)
+        es, ml = torch.empty(shape), torch.empty(shape)
+        to = torch.empty(shape + (128,), dtype=torch.bfloat16)
+        p = plan(t, max_parts=0, exp_sums=es, max_logits=ml, temporary_output=to)
+        assert p.max_parts == parts and p.rargs.max_context_partition_num == parts
+        assert p.dargs.exp_sums == es.data_ptr() and p.dargs.tmp_out == to.data_ptr()
+        assert p.keepalive == ()  # nothing launcher-made to keep
+    # sliding window: the same rule
+    shape = (3, 2, 17, 4)
+    es, ml = torch.empty(shape), torch.empty(shape)
+    to = torch.empty(shape + (128,), dtype=torch.bfloat16)
+    p = plan(t, sliding_window=4096, max_parts=0, exp_sums=es, max_logits=ml, temporary_output=to)
+    assert p.max_parts == 17 and p.tag == "ps_sw_partitioned"
+    # without caller partials the launcher's own count (one direct slot here)
+    assert plan(t, max_parts=0).max_parts == 1
+
+
+@pytest.fixture
+def recorded_launches(monkeypatch):
+    """pa_decode_ps_launch with the kernel launches replaced by a record of the plans."""
+    seen = []
+
+    def launch(self, stream_handle):
+        seen.append(self)
+        return self.tag
+
+    monkeypatch.setattr(pdf._Plan, "launch", launch)
+    pdf._PLAN_CACHE.clear()
+    yield seen
+    pdf._PLAN_CACHE.clear()
+
+
+def _launch(t, **kw):
+    args = {**t, **kw}
+    return pdf.pa_decode_ps_launch(
+        args["output"], args["query"], args["key_cache"], args["value_cache"], args["context_lengths"],
+        args.get("kv_page_indices"), args.get("kv_indptr"), 1 / math.sqrt(128), args["key_scale"],
+        args["value_scale"], block_tables=args.get("block_tables"), metadata=args.get("metadata"),
+        max_context_partition_num=args.get("max_parts", 0), stream=0)
+
+
+def test_cached_plans_release_caller_metadata(recorded_launches):
+    """Callers rebuild the metadata every step (its contents follow the context
+    lengths); plans cached on it must not keep the old dicts, and their partial
+    buffers, alive."""
+    import gc
+    import weakref
+
+    t = make_paged(per_token=True)
+    refs = []
+    for _ in range(5):
+        md = cpu_metadata(t, 4)
+        refs.append(weakref.ref(md["partial_output"]))
+        assert _launch(t, metadata=md) == "ps_split_reduce"
+        del md
+    gc.collect()
+    assert all(r() is None for r in refs)
+    assert len(pdf._PLAN_CACHE) >= 1 and all(p.keepalive in ((), (None,)) for p in pdf._PLAN_CACHE.values())
+
+
+def test_converted_scales_are_not_reused_stale(recorded_launches):
+    """A scale tensor the launcher has to convert (here float64) is copied; a plan
+    holding the copy must not be reused after the caller updates the original."""
+    t = make()
+    ks = torch.tensor([0.5], dtype=torch.float64)
+    _launch(t, key_scale=ks, max_parts=4)
+    ks[0] = 0.25
+    _launch(t, key_scale=ks, max_parts=4)
+    a0, a1 = recorded_launches[0].dargs, recorded_launches[1].dargs
+    val = lambda ptr: ctypes_float(ptr)  # noqa: E731
+    assert val(a0.key_scale) == 0.5 and val(a1.key_scale) == 0.25
+    # a float32 tensor is used as is, so its plan is cached and reads the live value
+    ks32 = torch.tensor([0.5])
+    _launch(t, key_scale=ks32, max_parts=4)
+    ks32[0] = 0.125
+    _launch(t, key_scale=ks32, max_parts=4)
+    assert recorded_launches[3] is recorded_launches[2] and val(recorded_launches[3].dargs.key_scale) == 0.125
+
+
+def ctypes_float(ptr):
+    import ctypes
+
+    return ctypes.c_float.from_address(ptr).value
+
+
+def test_worklist_prefers_the_tuned_schedule():
+    """get_pa_metadata's dict carries the reference's schedule under the reference's
+    keys and this build's own under "tuned"; the worklist kernel runs the tuned one
+    when present."""
+    t = make_paged(per_token=True)
+    ref = cpu_metadata(t, 4)
+    tuned = cpu_metadata(t, 2)
+    tuned["bin_groups"] = 0
+    md = dict(ref, tuned=tuned)
+    p = plan(t, metadata=md, max_parts=0)
+    assert p.wargs.num_cu == 2 and p.wargs.work_indptr == tuned["work_indptr"].data_ptr()
+    assert p.wargs.partial_output == tuned["partial_output"].data_ptr()
+    p_ref = plan(t, metadata=ref, max_parts=0)
+    assert p_ref.wargs.num_cu == 4 and p_ref.wargs.work_indptr == ref["work_indptr"].data_ptr()
+    with pytest.raises(ValueError, match="tuned"):
+        plan(t, metadata=dict(ref, tuned={"num_sm": 2}), max_parts=0)
