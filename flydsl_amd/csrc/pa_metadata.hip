@@ -246,8 +246,14 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
         lr += l4[i];
         gr += g4[i];
     }
+    if (t == 0) {  // batch nb is past every thread's four when nb == kParBatches
+        s_W[p.nb] = W;
+        s_L[p.nb] = Lt;
+        s_G[p.nb] = G;
+    }
     __syncthreads();
-    auto works_of = [&](int b) { return s_W[b + 1] - s_W[b]; };
+    // a batch's works lie in consecutive bins of one head, so at most nspk of them
+    auto works_of = [&](int b) { return min(max(s_W[b + 1] - s_W[b], 0), nspk); };
     const bool overflow = (long long)p.nhk * W > p.max_work || Lt > p.max_split_tiles;
 
     // work_info rows of every head
