@@ -17,6 +17,7 @@ PA_FP8_ABI_VERSION = 7
 PA_FP8_BF16, PA_FP8_F16, PA_FP8_F32 = 0, 1, 2
 PA_FP8_CACHE_ELEM, PA_FP8_CACHE_FP8_TENSOR, PA_FP8_CACHE_FP8_TOKEN = 0, 1, 2
 PA_FP8_KV_FLASH, PA_FP8_KV_X_PACKED, PA_FP8_KV_X_TRANS = 0, 1, 2
+PA_FP8_V_TRANS, PA_FP8_V_4D = 0, 1
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -73,7 +74,7 @@ class DecodeArgs(ctypes.Structure):
         ("stride_o_head", _i64),
         ("stride_o_group", _i64),
         ("waves_per_slot", _i32),
-        ("reserved", _i32),
+        ("value_layout", _i32),
     ]
 
 
@@ -150,6 +151,7 @@ class WorklistArgs(ctypes.Structure):
         ("out_dtype", _i32),
         ("softmax_scale", _f32),
         ("bin_groups", _i32),
+        ("value_layout", _i32),
     ]
 
 

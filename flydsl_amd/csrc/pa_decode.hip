@@ -1,118 +1,16 @@
-// gfx950 split-context FP8-KV paged-attention decode and its log-sum-exp reduce.
-//
-// Work decomposition (grid = (batch, kv_heads, partition slots), one workgroup per
-// slot, NW waves per workgroup):
-//   * slot z of sequence b covers the 256-token partitions [z*pps, min((z+1)*pps, T))
-//     with T = ceil(ctx/256), pps = ceil(T/P) (kernels/pa_decode_fp8.py:2311-2320);
-//     with a sliding window the partitions start at tile max(ctx-ql-sw,0)/256
-//     (kernels/pa_decode_swa.py:1359-1368) and the first window tile is trimmed
-//     to the 16-token group holding the window start.
-//   * the slot's tokens are cut into 64-token steps (4 groups of 16 tokens); wave w
-//     takes steps w, w+NW, ... and runs its own online softmax; the waves merge
-//     through LDS at the end and write one partial (exp_sum, max_logit, bf16 out).
-//
-// Per step a lane issues eight 16-byte K loads and eight 16-byte V loads (the
-// 16 KiB a wave consumes per step); the next step is prefetched while the current
-// one is computed.  fp8 e4m3fn is converted exactly to bf16 in registers
-// (v_cvt_scalef32_pk_bf16_fp8) and both products run on v_mfma_f32_16x16x32_bf16:
-//   QK : C[token][qrow] = sum_d K[token][d] Q[qrow][d]   (4 tiles x 4 k-steps)
-//   PV : C[dim][qrow]   = sum_t V[t][dim] P[qrow][t]     (8 dim tiles x 2 k-steps)
-// QK tile jt, row 4*kg+i holds token 16*kg + 4*jt + i of the step, so the QK
-// output lane (qrow, kg) owns exactly the 16 tokens of group kg -- the tokens its
-// PV operand needs (one 16-byte trans_v row of group kg) -- and P goes from the QK
-// accumulators to the PV MFMA without any cross-lane movement.
-#include "pa_common.h"
+// C ABI of the gfx950 FP8-KV paged-attention decode (include/pa_fp8.h) and the
+// two merges of split work: the log-sum-exp reduce of the split-context partials
+// (pa_lse_reduce_kernel) and the merge of split worklist partials
+// (pa_reduce_v1_*_kernel, the role of aiter's pa_reduce_v1).  The decode kernels
+// themselves are in pa_decode_kernels.h, built per head dim in pa_decode_hd.hip.
+#include "pa_decode_params.h"
 #include "pa_fp8.h"
-
 
 using namespace pa;
 
 namespace {
 
-struct DecodeParams {
-    float *exp_sums;
-    float *max_logits;
-    uint16_t *tmp_out;
-    const uint16_t *query;
-    const uint8_t *kc;
-    const uint8_t *vc;
-    const int32_t *bt;
-    const int32_t *ctx;
-    const float *ks;
-    const float *vs;
-    int64_t s_q_seq, s_q_head;
-    int64_t s_k_block, s_k_head;
-    int64_t s_v_block, s_v_head;
-    int64_t s_es_seq, s_es_head, s_es_part;
-    int64_t s_to_seq, s_to_head, s_to_part, s_to_group;
-    int64_t s_bt_seq;
-    int64_t s_ks_block, s_ks_head;
-    int32_t g, ql, eqgs, bs_log2;
-    int32_t num_blocks, max_blocks, max_parts, sw;
-    int32_t q_f16;
-    float qk_scale;  // softmax_scale * log2(e)
-    // direct output (one partition slot): final rows go to out[b, qi, h, gi, :]
-    void *out;
-    int64_t s_o_seq, s_o_len, s_o_head, s_o_group;
-    int32_t out_dtype;
-    int32_t direct;
-};
-
-// N consecutive values to the output tensor at element offset off, converted to
-// out_dtype (bf16 / f16 round to nearest even, f32 stored as is).
-template <int N>
-__device__ __forceinline__ void store_out(void *out, int out_dtype, int64_t off, const float (&v)[N]) {
-    if (out_dtype == PA_FP8_F32) {
-        float *dst = reinterpret_cast<float *>(out) + off;
-#pragma unroll
-        for (int j = 0; j < N; j += 4) *reinterpret_cast<float4 *>(dst + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
-        return;
-    }
-    uint32_t pk[N / 2];
-#pragma unroll
-    for (int j = 0; j < N; j += 2) {
-        if (out_dtype == PA_FP8_F16)
-            pk[j / 2] = uint32_t(f32_to_f16_bits(v[j])) | (uint32_t(f32_to_f16_bits(v[j + 1])) << 16);
-        else
-            pk[j / 2] = uint32_t(f32_to_bf16_bits(v[j])) | (uint32_t(f32_to_bf16_bits(v[j + 1])) << 16);
-    }
-    uint16_t *dst = reinterpret_cast<uint16_t *>(out) + off;
-    if constexpr (N == 8) *reinterpret_cast<uint4 *>(dst) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    else *reinterpret_cast<uint2 *>(dst) = make_uint2(pk[0], pk[1]);
-}
-
-// Where the partition kernel puts the result of one slot: the bf16 partial row
-// plus (exp_sum, max_logit), or (direct mode) the final row out[b, qi, h, gi, :].
-struct SlotSink {
-    const DecodeParams &p;
-    uint16_t *to;
-    float *es;
-    float *ml;
-    int b, h;
-
-    template <int N>
-    __device__ __forceinline__ void row(int r, int d0, const float (&v)[N]) const {
-        if (!p.direct) {
-            uint32_t pk[N / 2];
-#pragma unroll
-            for (int j = 0; j < N; j += 2)
-                pk[j / 2] = uint32_t(f32_to_bf16_bits(v[j])) | (uint32_t(f32_to_bf16_bits(v[j + 1])) << 16);
-            uint16_t *dst = to + r * p.s_to_group + d0;
-            if constexpr (N == 8) *reinterpret_cast<uint4 *>(dst) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-            else *reinterpret_cast<uint2 *>(dst) = make_uint2(pk[0], pk[1]);
-            return;
-        }
-        const int qi = r / p.g, gi = r - (r / p.g) * p.g;
-        store_out<N>(p.out, p.out_dtype, b * p.s_o_seq + qi * p.s_o_len + h * p.s_o_head + gi * p.s_o_group + d0, v);
-    }
-    // L = sum of exp2(logit2 - m2) over the slot, m2 = running max in log2 units
-    __device__ __forceinline__ void stats(int r, float L, float m2) const {
-        if (!p.direct) {
-            es[r] = L;
-            ml[r] = L > 0.f ? m2 * kLn2 : -INFINITY;
-        }
-    }
-};
+constexpr int kMaxHeadDim = 256;
 
 struct ReduceParams {
     void *out;
@@ -122,923 +20,8 @@ struct ReduceParams {
     int64_t s_o_seq, s_o_len, s_o_head, s_o_group;
     int64_t s_es_seq, s_es_head, s_es_part;
     int64_t s_to_seq, s_to_head, s_to_part, s_to_group;
-    int32_t g, max_parts;
+    int32_t g, max_parts, head_dim;
 };
-
-__device__ __forceinline__ bf16x8 load_q8(const uint16_t *p, bool f16) {
-    uint4 raw = *reinterpret_cast<const uint4 *>(p);
-    if (!f16) return __builtin_bit_cast(bf16x8, raw);
-    f16x8 hv = __builtin_bit_cast(f16x8, raw);
-    bf16x8 r;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = (__bf16)(float)hv[i];
-    return r;
-}
-
-__device__ __forceinline__ bf16x8 pack_bf16x8(f32x4 a, f32x4 b) {
-    bf16x4 x = __builtin_convertvector(a, bf16x4);
-    bf16x4 y = __builtin_convertvector(b, bf16x4);
-    return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
-// Waves per SIMD the decode kernels are compiled for: one 16-row group per wave
-// fits two waves (<= 256 registers each); more row groups per wave hold their
-// accumulators in AGPRs and run one wave per SIMD.
-template <int MTPW>
-constexpr int kWavesPerSimd = MTPW == 1 ? 2 : 1;
-
-#ifndef PA_FP8_STAGED_WAVES
-#define PA_FP8_STAGED_WAVES 3  // waves per SIMD the LDS-staged layout is compiled for
-#endif
-template <int MTPW, int NS>
-constexpr int kWavesFor = NS == 0 ? PA_FP8_STAGED_WAVES : kWavesPerSimd<MTPW>;
-
-// Query rows of one wave: MTPW groups of 16 rows (r = qi*g + gi), the QK B
-// operands and the keys each row may see.  Lane (qrow l16, kg) holds dims
-// 32kg..32kg+31 of its row; keys visible to a row are [lo_n, hi_n) (causal bound
-// ctx+1-ql+qi, window start ctx-ql-sw+qi); lo_max / hi_min bound them over the
-// wave's live rows (wave-uniform).
-template <int MTPW>
-struct RowSet {
-    static constexpr bool kFp8 = false;
-    bf16x8 qop[MTPW][4];
-    int lo_n[MTPW], hi_n[MTPW];
-    int lo_max, hi_min;
-};
-
-// Query rows as a two-term fp8 split for the fp8 QK products: x = q * inv (inv =
-// 448 / amax of the row), hi = e4m3(x), lo = e4m3(x - hi), so q ~ (hi + lo) / inv
-// to about 8 significant bits (bf16's precision); dq = 1 / inv restores the logit.
-template <int MTPW>
-struct RowSetF8 {
-    static constexpr bool kFp8 = true;
-    i32x8 qh[MTPW], ql[MTPW];
-    float dq[MTPW];
-    int lo_n[MTPW], hi_n[MTPW];
-    int lo_max, hi_min;
-};
-
-// fp8 two-term split of one lane's 32 query values (dims 32kg .. 32kg+31 of its
-// row); the row's amax is reduced over its 4 lanes (kg = lane / 16).
-template <int MTPW>
-__device__ __forceinline__ void split_q_fp8(RowSetF8<MTPW> &rw, int mg, const bf16x8 (&q)[4], bool live) {
-    float x[32];
-    float amax = 0.0f;
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            x[8 * s + i] = (float)q[s][i];
-            amax = fmaxf(amax, fabsf(x[8 * s + i]));
-        }
-    amax = fmaxf(amax, shfl_xor_f(amax, 16));
-    amax = fmaxf(amax, shfl_xor_f(amax, 32));
-    const float inv = (live && amax > 0.0f) ? 448.0f / amax : 1.0f;
-    rw.dq[mg] = 1.0f / inv;
-#pragma unroll
-    for (int w = 0; w < 8; ++w) {
-        float v[4], r[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = x[4 * w + i] * inv;
-        int hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
-        hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], hi, true);
-        const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-        const f32x2 h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-        r[0] = v[0] - h01[0];
-        r[1] = v[1] - h01[1];
-        r[2] = v[2] - h23[0];
-        r[3] = v[3] - h23[1];
-        int lo = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
-        lo = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], lo, true);
-        rw.qh[mg][w] = hi;
-        rw.ql[mg][w] = lo;
-    }
-}
-
-template <class RW>
-__device__ __forceinline__ void setup_rows(RW &rw, const DecodeParams &p, int b, int h, int ctx, int tok_lo,
-                                           int tok_hi, int row_group0, int l16, int kg) {
-    constexpr int MTPW = sizeof(rw.lo_n) / sizeof(int);
-    rw.lo_max = tok_lo;
-    rw.hi_min = tok_hi;
-#pragma unroll
-    for (int mg = 0; mg < MTPW; ++mg) {
-        const int n = (row_group0 + mg) * 16 + l16;
-        if (n < p.eqgs) {
-            const int qi = n / p.g;
-            const int gi = n - qi * p.g;
-            const uint16_t *qrow =
-                p.query + (int64_t)(b * p.ql + qi) * p.s_q_seq + (int64_t)(h * p.g + gi) * p.s_q_head + 32 * kg;
-            bf16x8 q[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) q[s] = load_q8(qrow + 8 * s, p.q_f16 != 0);
-            if constexpr (RW::kFp8) {
-                split_q_fp8<MTPW>(rw, mg, q, true);
-            } else {
-#pragma unroll
-                for (int s = 0; s < 4; ++s) rw.qop[mg][s] = q[s];
-            }
-            rw.hi_n[mg] = min(tok_hi, ctx + 1 - p.ql + qi);
-            rw.lo_n[mg] = p.sw > 0 ? max(tok_lo, ctx - p.ql - p.sw + qi) : tok_lo;
-        } else {
-            bf16x8 q[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) q[s] = bf16x8{};
-            if constexpr (RW::kFp8) {
-                split_q_fp8<MTPW>(rw, mg, q, false);
-            } else {
-#pragma unroll
-                for (int s = 0; s < 4; ++s) rw.qop[mg][s] = q[s];
-            }
-            rw.hi_n[mg] = tok_hi;  // padded rows: any finite value, never stored
-            rw.lo_n[mg] = tok_lo;
-        }
-        rw.lo_max = max(rw.lo_max, rw.lo_n[mg]);
-        rw.hi_min = min(rw.hi_min, rw.hi_n[mg]);
-    }
-    // the min / max over the 16 rows of a group: rows differ only through qi
-    for (int sh = 1; sh < 16; sh <<= 1) {
-        rw.lo_max = max(rw.lo_max, __shfl_xor(rw.lo_max, sh, 64));
-        rw.hi_min = min(rw.hi_min, __shfl_xor(rw.hi_min, sh, 64));
-    }
-    rw.lo_max = __builtin_amdgcn_readfirstlane(rw.lo_max);
-    rw.hi_min = __builtin_amdgcn_readfirstlane(rw.hi_min);
-}
-
-// Per-lane online-softmax state.  m_run is the reference max (log2 units) the
-// exponentials, l_run and o are taken against; it is raised only when a step's
-// max exceeds it by more than kSlack, so exp2(logit - m_run) <= 2^kSlack and o is
-// rescaled on few steps.  m_top is the true running max, used for the stats.
-template <int MTPW>
-struct SmState {
-    float m_run[MTPW], l_run[MTPW], m_top[MTPW];
-    f32x4 o[MTPW][8];
-
-    __device__ __forceinline__ void init() {
-#pragma unroll
-        for (int mg = 0; mg < MTPW; ++mg) {
-            m_run[mg] = -INFINITY;
-            m_top[mg] = -INFINITY;
-            l_run[mg] = 0.0f;
-#pragma unroll
-            for (int m = 0; m < 8; ++m) o[mg][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-};
-
-// QK and softmax of one 64-token step: kr holds the step's K ([tile][chunk], 16 fp8
-// each: lane (l16, kg) of tile jt holds token 16*(l16>>2) + 4*jt + (l16&3), dims of
-// chunks 2kg and 2kg+1).  QK tile jt, row 4*kg+i of the MFMA output is token
-// trow + 4*jt + i with trow = t0 + 16*kg, so lane (qrow, kg) ends up owning the 16
-// tokens of group kg -- exactly the tokens of its PV operand row.  Writes the
-// bf16 probabilities of every row group to pop.  After the QK products, after_qk()
-// runs (the K registers are free again).
-//
-// With the fp8 row set (RW::kFp8), QK runs on fp8 MFMAs straight from the K bytes
-// (the lane's 32 bytes of tile jt are exactly its A operand: dims 32kg .. 32kg+31),
-// two products per tile (hi and lo terms of the query), and the row's dequant
-// factor joins the logit scale; no K conversion.
-template <int MTPW, bool PER_TOKEN, class RW, class KScale, class VScale, class AfterQk>
-__device__ __forceinline__ void step_qk_softmax(SmState<MTPW> &st, const RW &rw, const uint4 (&kr)[4][2],
-                                                const KScale &ksr, const VScale &vsr, float k_fac, int t0,
-                                                int kg, bf16x8 (&pop)[MTPW][2], AfterQk &&after_qk) {
-    const int trow = t0 + 16 * kg;  // token of (tile jt, i) = trow + 4jt + i
-    const bool interior = t0 >= rw.lo_max && t0 + kStep <= rw.hi_min;
-
-    // QK: S[token][qrow] for 4 tiles of 16 tokens.  The wave runs its products and
-    // softmax here at raised issue priority (1), and its PV products in step_pv
-    // higher still (2); its loads, LDS reads and barrier waits stay at the base
-    // level.  The SIMD then keeps feeding the matrix pipe of a wave that reached
-    // its products while the other waves' VALU work fills the pipe's busy cycles.
-    f32x4 sc[MTPW][4];
-    __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-        if constexpr (RW::kFp8) {
-            const i32x8 a = {(int)kr[jt][0].x, (int)kr[jt][0].y, (int)kr[jt][0].z, (int)kr[jt][0].w,
-                             (int)kr[jt][1].x, (int)kr[jt][1].y, (int)kr[jt][1].z, (int)kr[jt][1].w};
-#pragma unroll
-            for (int mg = 0; mg < MTPW; ++mg) {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                acc = mfma_fp8_k128(a, rw.qh[mg], acc);
-                acc = mfma_fp8_k128(a, rw.ql[mg], acc);
-                sc[mg][jt] = acc;
-            }
-        } else {
-            const bf16x8 a0 = fp8x8_to_bf16x8(kr[jt][0].x, kr[jt][0].y);
-            const bf16x8 a1 = fp8x8_to_bf16x8(kr[jt][0].z, kr[jt][0].w);
-            const bf16x8 a2 = fp8x8_to_bf16x8(kr[jt][1].x, kr[jt][1].y);
-            const bf16x8 a3 = fp8x8_to_bf16x8(kr[jt][1].z, kr[jt][1].w);
-#pragma unroll
-            for (int mg = 0; mg < MTPW; ++mg) {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                acc = mfma_bf16(a0, rw.qop[mg][0], acc);
-                acc = mfma_bf16(a1, rw.qop[mg][1], acc);
-                acc = mfma_bf16(a2, rw.qop[mg][2], acc);
-                acc = mfma_bf16(a3, rw.qop[mg][3], acc);
-                sc[mg][jt] = acc;
-            }
-        }
-    }
-    after_qk();
-
-    f32x4 kf[4];
-    if constexpr (!RW::kFp8) {
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr(jt) * k_fac : f32x4{k_fac, k_fac, k_fac, k_fac};
-    }
-
-#pragma unroll
-    for (int mg = 0; mg < MTPW; ++mg) {
-        if constexpr (RW::kFp8) {
-            const float kq = k_fac * rw.dq[mg];
-#pragma unroll
-            for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr(jt) * kq : f32x4{kq, kq, kq, kq};
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-            sc[mg][jt] *= kf[jt];
-            if (!interior) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int t = trow + 4 * jt + i;
-                    sc[mg][jt][i] = (t >= rw.lo_n[mg] && t < rw.hi_n[mg]) ? sc[mg][jt][i] : -INFINITY;
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[mg][jt][i]);
-        }
-        mx = fmaxf(mx, shfl_xor_f(mx, 16));
-        mx = fmaxf(mx, shfl_xor_f(mx, 32));
-        st.m_top[mg] = fmaxf(st.m_top[mg], mx);
-        const bool raise = mx > st.m_run[mg] + kSlack;  // false while the row has seen no key
-        if (__any(raise)) {                              // wave-uniform
-            const float alpha = raise ? fast_exp2(st.m_run[mg] - mx) : 1.0f;  // 0 on a row's first keys
-            st.m_run[mg] = raise ? mx : st.m_run[mg];
-            st.l_run[mg] *= alpha;
-#pragma unroll
-            for (int m = 0; m < 8; ++m) st.o[mg][m] *= alpha;
-        }
-        const float m_use = st.m_run[mg] == -INFINITY ? 0.0f : st.m_run[mg];
-        float psum = 0.0f;
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float pv = fast_exp2(sc[mg][jt][i] - m_use);
-                psum += pv;
-                sc[mg][jt][i] = pv;
-            }
-            if constexpr (PER_TOKEN) sc[mg][jt] *= vsr(jt);
-        }
-        st.l_run[mg] += psum;
-        pop[mg][0] = pack_bf16x8(sc[mg][0], sc[mg][1]);
-        pop[mg][1] = pack_bf16x8(sc[mg][2], sc[mg][3]);
-    }
-    __builtin_amdgcn_s_setprio(0);
-}
-
-// PV of one step: O[dim][qrow] += V^T P^T over its 64 tokens; vr[m] holds the 16
-// tokens of group kg of head dim 16m + l16.
-template <int MTPW>
-__device__ __forceinline__ void step_pv(SmState<MTPW> &st, const uint4 (&vr)[8], const bf16x8 (&pop)[MTPW][2]) {
-    __builtin_amdgcn_s_setprio(2);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        const bf16x8 v0 = fp8x8_to_bf16x8(vr[m].x, vr[m].y);
-        const bf16x8 v1 = fp8x8_to_bf16x8(vr[m].z, vr[m].w);
-#pragma unroll
-        for (int mg = 0; mg < MTPW; ++mg) {
-            st.o[mg][m] = mfma_bf16(v0, pop[mg][0], st.o[mg][m]);
-            st.o[mg][m] = mfma_bf16(v1, pop[mg][1], st.o[mg][m]);
-        }
-    }
-    __builtin_amdgcn_s_setprio(0);
-}
-
-// Rows of a wave that ran every step of the range itself: sum the four kg-lane
-// partial exp sums of each row, normalise and emit.
-template <int MTPW, class Sink>
-__device__ __forceinline__ void finish_rows(SmState<MTPW> &st, const DecodeParams &p, int row_group0, int l16, int kg,
-                                            float v_fac, const Sink &sink) {
-#pragma unroll
-    for (int mg = 0; mg < MTPW; ++mg) {
-        float lt = st.l_run[mg];
-        lt += shfl_xor_f(lt, 16);
-        lt += shfl_xor_f(lt, 32);
-        const int r = (row_group0 + mg) * 16 + l16;
-        if (r < p.eqgs) {
-            const float inv = lt > 0.f ? v_fac / lt : 0.f;
-#pragma unroll
-            for (int m = 0; m < 8; ++m) {
-                const f32x4 v = st.o[mg][m] * inv;
-                const float v4[4] = {v[0], v[1], v[2], v[3]};
-                sink.row(r, 16 * m + 4 * kg, v4);
-            }
-            if (kg == 0) sink.stats(r, lt > 0.f ? lt * fast_exp2(st.m_run[mg] - st.m_top[mg]) : 0.f, st.m_top[mg]);
-        }
-    }
-}
-
-template <class Sink>
-__device__ __forceinline__ void emit_empty(const DecodeParams &p, int nthreads, const Sink &sink) {
-    // empty range (kernels/pa_decode_fp8.py:2591-2598)
-    const int tid = threadIdx.x;
-    for (int r = tid; r < p.eqgs; r += nthreads) sink.stats(r, 0.0f, -INFINITY);
-    const float zero8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int i = tid; i < p.eqgs * (kHeadDim / 8); i += nthreads)
-        sink.row(i / (kHeadDim / 8), (i % (kHeadDim / 8)) * 8, zero8);
-}
-
-// Attention of the query rows of (sequence b, kv head h) over the keys
-// [tok_lo, tok_hi) of the sequence, streaming K / V through registers; the result
-// of each row r = qi*g + gi goes to sink.row (normalised output) and sink.stats
-// (exp sum and log2-domain max).  ctx is already clamped to the page row's
-// capacity; bt_row is the sequence's page row (block-table row or kv_page_indices
-// window).  Every thread of the workgroup calls this with the same arguments (it
-// synchronises internally).
-// The workgroup has NW = RS * NS waves.  Wave w owns query-row groups
-// [rs*MTPW, (rs+1)*MTPW) (rs = w % RS, 16 rows per group) and the steps
-// ns, ns+NS, ... of the range (ns = w / RS).  Each wave loads its own steps: the
-// next step's K goes into the K registers right after the QK products, its V
-// right after the PV products.  Waves of the same rs merge their online-softmax
-// states through LDS at the end.
-template <int MTPW, int RS, int NS, bool PER_TOKEN, class Sink>
-__device__ __forceinline__ void attend_range(const DecodeParams &p, const int b, const int h, const int ctx,
-                                             const int tok_lo, const int tok_hi, const int32_t *bt_row,
-                                             const Sink &sink) {
-    constexpr int D = kHeadDim;
-    constexpr int NW = RS * NS;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rs = wave % RS;
-    const int ns = wave / RS;
-    const int l16 = lane & 15;
-    const int kg = lane >> 4;
-    const int bs = 1 << p.bs_log2;
-
-    if (tok_lo >= tok_hi) {
-        emit_empty(p, NW * 64, sink);
-        return;
-    }
-    RowSet<MTPW> rw;
-    setup_rows(rw, p, b, h, ctx, tok_lo, tok_hi, rs * MTPW, l16, kg);
-    const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
-    const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
-    SmState<MTPW> st;
-    st.init();
-
-    const int ngroups = (tok_hi - tok_lo + kGroup - 1) / kGroup;
-    const int nsteps = (ngroups + 3) / 4;
-    const int last_group = tok_lo + (ngroups - 1) * kGroup;
-    const uint8_t *kc_h = p.kc + (int64_t)h * p.s_k_head;
-    const uint8_t *vc_h = p.vc + (int64_t)h * p.s_v_head;
-    const int kchunk = bs * 16;  // bytes between 16-dim chunks of one (block, head)
-    const int k_lane_off = (l16 & 3) * 16 + (2 * kg) * kchunk;
-    const int v_lane_off = l16 * 16;
-
-    // A lane's K group (QK row owner) is l16>>2, its V / scale group is kg.  The
-    // page-table entries of a step are read one step of the wave earlier than its
-    // K / V: vector memory waits are in order, so waiting for entries read just
-    // before the step's K would also wait for the V loads still in flight.
-    auto page_of = [&](int step, int g) {
-        const int gs = min(tok_lo + step * kStep + 16 * g, last_group);
-        return bt_row[gs >> p.bs_log2];
-    };
-    auto k_ptr = [&](int step, int e) {
-        const int gs = min(tok_lo + step * kStep + 16 * (l16 >> 2), last_group);
-        const int phys = min(max(e, 0), p.num_blocks - 1);
-        return kc_h + (int64_t)phys * p.s_k_block + ((gs & (bs - 1)) >> 4) * 256 + k_lane_off;
-    };
-    auto v_loc = [&](int step, int e, int64_t &vofs, int64_t &sofs) {
-        const int gs = min(tok_lo + step * kStep + 16 * kg, last_group);
-        const int phys = min(max(e, 0), p.num_blocks - 1);
-        const int sub = (gs & (bs - 1)) >> 4;
-        vofs = (int64_t)phys * p.s_v_block + sub * (D * 16) + v_lane_off;
-        sofs = (int64_t)phys * p.s_ks_block + (int64_t)h * p.s_ks_head + sub * 16;
-    };
-
-    uint4 kr[4][2];  // K of the step: [tile][chunk], 16 fp8 each
-    uint4 vr[8];     // V of the step: [dim tile], 16 tokens of one head dim
-    f32x4 ksr[4], vsr[4];
-    auto load_k = [&](const uint8_t *kb) {
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-            kr[jt][0] = ld16(kb + jt * 64);
-            kr[jt][1] = ld16(kb + kchunk + jt * 64);
-        }
-    };
-    auto load_v = [&](int64_t vofs) {
-#pragma unroll
-        for (int m = 0; m < 8; ++m) vr[m] = ld16(vc_h + vofs + m * 256);
-    };
-    auto load_scales = [&](int64_t sofs) {
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            ksr[q4] = *reinterpret_cast<const f32x4 *>(p.ks + sofs + 4 * q4);
-            vsr[q4] = *reinterpret_cast<const f32x4 *>(p.vs + sofs + 4 * q4);
-        }
-    };
-
-    int step = ns;
-    int ek_next = 0, ev_next = 0;  // page-table entries of the wave's next step
-    if (step < nsteps) {
-        const int ek = page_of(step, l16 >> 2), ev = page_of(step, kg);
-        if (step + NS < nsteps) {
-            ek_next = page_of(step + NS, l16 >> 2);
-            ev_next = page_of(step + NS, kg);
-        }
-        int64_t vofs, sofs;
-        v_loc(step, ev, vofs, sofs);
-        load_k(k_ptr(step, ek));
-        if constexpr (PER_TOKEN) load_scales(sofs);
-        load_v(vofs);
-    }
-    while (step < nsteps) {
-        const int nxt = step + NS;
-        const bool has_nxt = nxt < nsteps;
-        int ek_after = 0, ev_after = 0;
-        if (nxt + NS < nsteps) {
-            ek_after = page_of(nxt + NS, l16 >> 2);
-            ev_after = page_of(nxt + NS, kg);
-        }
-        const uint8_t *nkb = nullptr;
-        int64_t nvofs = 0, nsofs = 0;
-        if (has_nxt) {
-            nkb = k_ptr(nxt, ek_next);
-            v_loc(nxt, ev_next, nvofs, nsofs);
-        }
-        ek_next = ek_after;
-        ev_next = ev_after;
-        f32x4 ksc[4], vsc[4];
-        if constexpr (PER_TOKEN) {
-#pragma unroll
-            for (int jt = 0; jt < 4; ++jt) {
-                ksc[jt] = ksr[jt];
-                vsc[jt] = vsr[jt];
-            }
-        }
-        bf16x8 pop[MTPW][2];
-        step_qk_softmax<MTPW, PER_TOKEN>(st, rw, kr, [&](int jt) { return ksc[jt]; }, [&](int jt) { return vsc[jt]; },
-                                         k_fac, tok_lo + step * kStep, kg, pop, [&] {
-            if (has_nxt) {
-                load_k(nkb);  // K registers are free again
-                if constexpr (PER_TOKEN) load_scales(nsofs);
-            }
-        });
-        step_pv<MTPW>(st, vr, pop);
-        if (has_nxt) load_v(nvofs);  // V registers are free again
-        step = nxt;
-    }
-
-    if constexpr (NS == 1) {
-        finish_rows<MTPW>(st, p, rs * MTPW, l16, kg, v_fac, sink);
-    } else {
-        // sum the four kg-lane partial exp sums of each query row
-#pragma unroll
-        for (int mg = 0; mg < MTPW; ++mg) {
-            float lt = st.l_run[mg];
-            lt += shfl_xor_f(lt, 16);
-            lt += shfl_xor_f(lt, 32);
-            st.l_run[mg] = lt;
-        }
-        constexpr int DP = D + 4;
-        __shared__ float s_o[NW][16][DP];
-        __shared__ float s_m[NW][16];
-        __shared__ float s_l[NW][16];
-        __shared__ float s_t[NW][16];
-        // merge: RS*16 rows x D outputs per pass, E per thread
-        constexpr int E = RS * 16 * D / (NW * 64);
-        static_assert(E >= 4 && E % 4 == 0 && E * NW * 64 == RS * 16 * D, "merge covers each row pass exactly");
-        const int flat = tid * E;
-        const int mrs = flat / (16 * D);  // row split this thread merges
-        const int n = (flat / D) % 16;
-        const int d0 = flat % D;
-#pragma unroll
-        for (int mg = 0; mg < MTPW; ++mg) {
-#pragma unroll
-            for (int m = 0; m < 8; ++m) *reinterpret_cast<f32x4 *>(&s_o[wave][l16][16 * m + 4 * kg]) = st.o[mg][m];
-            if (kg == 0) {
-                s_m[wave][l16] = st.m_run[mg];
-                s_l[wave][l16] = st.l_run[mg];
-                s_t[wave][l16] = st.m_top[mg];
-            }
-            __syncthreads();
-            float M = -INFINITY, Mt = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < NS; ++j) {
-                M = fmaxf(M, s_m[j * RS + mrs][n]);
-                Mt = fmaxf(Mt, s_t[j * RS + mrs][n]);
-            }
-            const float Ms = M == -INFINITY ? 0.0f : M;
-            float f[NS];
-            float L = 0.f;
-#pragma unroll
-            for (int j = 0; j < NS; ++j) {
-                f[j] = fast_exp2(s_m[j * RS + mrs][n] - Ms);
-                L += s_l[j * RS + mrs][n] * f[j];
-            }
-            const float inv = L > 0.f ? v_fac / L : 0.f;
-            const int r = (mrs * MTPW + mg) * 16 + n;
-            if (r < p.eqgs) {
-                constexpr int EW = E < 8 ? E : 8;  // outputs per store (E is 4 with 8 waves)
-#pragma unroll
-                for (int e0 = 0; e0 < E; e0 += EW) {
-                    float v8[EW];
-#pragma unroll
-                    for (int j2 = 0; j2 < EW; ++j2) {
-                        float a = 0.f;
-#pragma unroll
-                        for (int j = 0; j < NS; ++j) a += s_o[j * RS + mrs][n][d0 + e0 + j2] * f[j];
-                        v8[j2] = a * inv;
-                    }
-                    sink.row(r, d0 + e0, v8);
-                }
-                if (d0 == 0) sink.stats(r, L > 0.f ? L * fast_exp2(M - Mt) : 0.f, Mt);
-            }
-            __syncthreads();
-        }
-    }
-}
-
-// ------------------------------------------------------- LDS-staged K / V stream
-// For layouts where every wave of the workgroup consumes every step (NS == 1),
-// the workgroup streams the steps' K / V through an LDS ring: each step's 16 KB
-// (plus its per-token scales) is loaded once per workgroup with direct
-// global -> LDS loads (global_load_lds_dwordx4, 16 bytes per lane, lane i landing
-// at M0 + 16 i), kStages - 1 steps ahead of the step being computed.  The loads
-// are issued from inline assembly, so the compiler does not order LDS reads
-// behind them; each wave waits for its own loads of a step with an explicit
-// s_waitcnt vmcnt(n) (loads complete in issue order, and n counts only loads this
-// wave issued later, so the wait is never short) and a barrier then publishes the
-// step to every wave.  Page indices for the load addresses come from an LDS window
-// of the page row, so no vector memory load of the compiler's own sits between
-// the asynchronous ones.
-//
-// Stage layout (bytes): K [4 groups][8 chunks][16 tokens][16] with the group
-// stride padded to 2112 (the QK operand reads of lanes 0-3 and 4-7 then hit
-// different banks), V [4 groups][128 dims][16 tokens], then the per-token K and V
-// scales [4 groups][16] f32 each.
-#ifndef PA_FP8_STAGES
-#define PA_FP8_STAGES 3  // ring depth (steps in flight + 1)
-#endif
-#ifndef PA_FP8_KPAD
-#define PA_FP8_KPAD 64  // bytes of padding after each K group
-#endif
-#ifndef PA_FP8_PAGE_WINDOW
-#define PA_FP8_PAGE_WINDOW 256  // page-row entries held in LDS at a time
-#endif
-constexpr int kStages = PA_FP8_STAGES;
-constexpr int kKGroupStride = 2048 + PA_FP8_KPAD;
-constexpr int kStageV = 4 * kKGroupStride;
-constexpr int kStageS = kStageV + 4 * 2048;
-constexpr int kStageBytes = kStageS + 512;
-constexpr int kPageWin = PA_FP8_PAGE_WINDOW;
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const lds_void_t *)p;
-}
-
-// 16 bytes from gptr to LDS byte address lds_base + 16 * lane.
-__device__ __forceinline__ void dma16(const void *gptr, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory", "m0");
-}
-
-// Wait until at most N of this wave's vector memory loads are outstanding and
-// its LDS operations are done, then meet the other waves.
-template <int N>
-__device__ __forceinline__ void wait_vm_barrier() {
-    static_assert(N >= 0 && N <= 63, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
-// Loads steps of one (sequence, kv head) token range into an LDS ring for NW waves:
-// K rows, V rows and (per-token) the scale piece of step q go to stage q % STAGES;
-// each wave issues R loads per step.  issue(q) needs every wave past its last use
-// of stage q % STAGES (the caller's barrier guarantees it).
-template <int NW, int STAGES, bool PER_TOKEN>
-struct KvStager {
-    static constexpr int KROWS = 8 / NW;    // K rows (1 KB each) a wave loads per step
-    static constexpr int VROWS = 8 / NW;    // V rows
-    static constexpr int SLANES = 32 / NW;  // lanes of a wave loading 16 bytes of scales
-    static constexpr int R = KROWS + VROWS + (PER_TOKEN ? 1 : 0);
-    static_assert(KROWS == VROWS, "K and V rows of a wave share their groups");
-    static_assert(NW == 1 || NW == 2 || NW == 4, "1, 2 or 4 waves");
-    static_assert((STAGES - 2) * R <= 63, "vmcnt range");
-
-    const DecodeParams &p;
-    uint8_t *ring;
-    int32_t *pages;
-    const int32_t *bt_row;
-    const uint8_t *kc_h, *vc_h;
-    int64_t kchunk;
-    uint32_t ring_addr;
-    int h, row_len, tok_lo, last_group, last_page, nsteps, wbase, bs, tid, lane, wave;
-
-    __device__ __forceinline__ void load_window(int base) {  // every wave is past its last use of the window
-        wbase = base;
-        const int n = min(kPageWin, last_page - base + 1);
-        for (int i = tid; i < n; i += NW * 64) pages[i] = base + i < row_len ? bt_row[base + i] : 0;
-        __syncthreads();
-    }
-    // physical block and 16-token sub-row of group g of step q
-    __device__ __forceinline__ void group_loc(int q, int g, int &phys, int &sub) const {
-        const int gs = min(tok_lo + q * kStep + 16 * g, last_group);
-        const int e = pages[(gs >> p.bs_log2) - wbase];
-        phys = min(max(e, 0), p.num_blocks - 1);
-        sub = (gs & (bs - 1)) >> 4;
-    }
-    __device__ __forceinline__ void issue(int q) {
-        const int lastg_page = min(tok_lo + q * kStep + 48, last_group) >> p.bs_log2;
-        if (lastg_page - wbase >= kPageWin) load_window((tok_lo + q * kStep) >> p.bs_log2);
-        const uint32_t sb = ring_addr + (uint32_t)((q % STAGES) * kStageBytes);
-        // every page-window read first, then the loads: each load's inline asm is a
-        // memory barrier to the compiler, so a window read placed between two loads
-        // would be waited for on its own
-        int phys[KROWS], sub[KROWS];
-#pragma unroll
-        for (int j = 0; j < KROWS; ++j) group_loc(q, (wave + NW * j) >> 1, phys[j], sub[j]);
-        const int piece = wave * SLANES + min(lane, SLANES - 1);
-        int sphys = 0, ssub = 0;
-        if constexpr (PER_TOKEN) group_loc(q, (piece & 15) >> 2, sphys, ssub);
-#pragma unroll
-        for (int j = 0; j < KROWS; ++j) {  // K rows: (group g, chunks 4*half .. 4*half+3)
-            const int r = wave + NW * j;
-            const int g = r >> 1, half = r & 1;
-            const uint8_t *src = kc_h + (int64_t)phys[j] * p.s_k_block + (4 * half + (lane >> 4)) * kchunk +
-                                 sub[j] * 256 + (lane & 15) * 16;
-            dma16(src, __builtin_amdgcn_readfirstlane(sb + g * kKGroupStride + half * 1024));
-        }
-#pragma unroll
-        for (int j = 0; j < VROWS; ++j) {  // V rows: (group g, dims 64*half .. 64*half+63), the K rows' groups
-            const int r = wave + NW * j;
-            const int g = r >> 1, half = r & 1;
-            const uint8_t *src =
-                vc_h + (int64_t)phys[j] * p.s_v_block + sub[j] * (kHeadDim * 16) + (64 * half + lane) * 16;
-            dma16(src, __builtin_amdgcn_readfirstlane(sb + kStageV + g * 2048 + half * 1024));
-        }
-        if constexpr (PER_TOKEN) {  // 32 pieces of 16 bytes: K scales of groups 0-3, then V scales
-            if (lane < SLANES) {
-                const float *src = (piece < 16 ? p.ks : p.vs) + (int64_t)sphys * p.s_ks_block +
-                                   (int64_t)h * p.s_ks_head + ssub * 16 + 4 * (piece & 3);
-                dma16(src, __builtin_amdgcn_readfirstlane(sb + kStageS + wave * SLANES * 16));
-            }
-        }
-    }
-    __device__ __forceinline__ void prologue() {
-#pragma unroll
-        for (int q = 0; q < STAGES - 1; ++q)
-            if (q < nsteps) issue(q);
-    }
-    template <int L>
-    __device__ __forceinline__ void wait_later(int later) {
-        if constexpr (L > 0) {
-            if (later >= L) {
-                wait_vm_barrier<L * R>();
-                return;
-            }
-            wait_later<L - 1>(later);
-        } else {
-            wait_vm_barrier<0>();
-        }
-    }
-    // Step n is in LDS for every wave, and every wave is done with step n-1, after
-    // this wave's loads of step n landed (at most (later steps issued) * R of its
-    // loads remain outstanding) and the barrier.
-    __device__ __forceinline__ void wait_step(int n) { wait_later<STAGES - 2>(min(STAGES - 2, nsteps - 1 - n)); }
-    __device__ __forceinline__ const uint8_t *stage(int n) const { return ring + (n % STAGES) * kStageBytes; }
-};
-
-template <int NW, int STAGES, bool PER_TOKEN>
-__device__ __forceinline__ void init_stager(KvStager<NW, STAGES, PER_TOKEN> &sg, uint8_t *ring, int32_t *pages,
-                                            const DecodeParams &p, int h, int tok_lo, int tok_hi,
-                                            const int32_t *bt_row, int row_len) {
-    sg.ring = ring;
-    sg.pages = pages;
-    sg.ring_addr = lds_addr(ring);
-    sg.bt_row = bt_row;
-    sg.row_len = row_len;
-    sg.h = h;
-    sg.kc_h = p.kc + (int64_t)h * p.s_k_head;
-    sg.vc_h = p.vc + (int64_t)h * p.s_v_head;
-    sg.bs = 1 << p.bs_log2;
-    sg.kchunk = (int64_t)sg.bs * 16;
-    sg.tok_lo = tok_lo;
-    const int ngroups = (tok_hi - tok_lo + kGroup - 1) / kGroup;
-    sg.nsteps = (ngroups + 3) / 4;
-    sg.last_group = tok_lo + (ngroups - 1) * kGroup;
-    sg.last_page = sg.last_group >> p.bs_log2;
-    sg.tid = threadIdx.x;
-    sg.lane = threadIdx.x & 63;
-    sg.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    sg.load_window(tok_lo >> p.bs_log2);
-}
-
-// Row-split LDS-staged layout: RS waves each own MTPW row groups and all take
-// every 64-token step from the ring.
-template <int MTPW, int RS, bool PER_TOKEN, class Sink>
-__device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const int b, const int h, const int ctx,
-                                                    const int tok_lo, const int tok_hi, const int32_t *bt_row,
-                                                    const int row_len, const Sink &sink) {
-    constexpr int NW = RS;
-    __shared__ __attribute__((aligned(16))) uint8_t s_ring[kStages * kStageBytes];
-    __shared__ int32_t s_pages[kPageWin];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int l16 = lane & 15;
-    const int kg = lane >> 4;
-
-    // every wave is done with the ring and the page window of an earlier range
-    wait_vm_barrier<0>();
-    if (tok_lo >= tok_hi) {
-        emit_empty(p, NW * 64, sink);
-        return;
-    }
-    RowSetF8<MTPW> rw;
-    setup_rows(rw, p, b, h, ctx, tok_lo, tok_hi, wave * MTPW, l16, kg);
-    const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
-    const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
-    SmState<MTPW> st;
-    st.init();
-    KvStager<NW, kStages, PER_TOKEN> sg{p};
-    init_stager(sg, s_ring, s_pages, p, h, tok_lo, tok_hi, bt_row, row_len);
-    sg.prologue();
-    for (int n = 0; n < sg.nsteps; ++n) {
-        sg.wait_step(n);
-        // the ring loads go out ahead of the other waves' products on the SIMD
-        __builtin_amdgcn_s_setprio(3);
-        if (n + kStages - 1 < sg.nsteps) sg.issue(n + kStages - 1);
-        __builtin_amdgcn_s_setprio(0);
-        const uint8_t *sk = sg.stage(n);
-        uint4 kr[4][2];
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-            const uint8_t *kp = sk + (l16 >> 2) * kKGroupStride + (2 * kg) * 256 + (4 * jt + (l16 & 3)) * 16;
-            kr[jt][0] = *reinterpret_cast<const uint4 *>(kp);
-            kr[jt][1] = *reinterpret_cast<const uint4 *>(kp + 256);
-        }
-        // the scales and V are read from the stage where they are used, which keeps
-        // them out of registers during the QK products and the softmax
-        const uint8_t *ss = sk + kStageS + kg * 64;
-        auto ks_at = [&](int jt) { return *reinterpret_cast<const f32x4 *>(ss + 16 * jt); };
-        auto vs_at = [&](int jt) { return *reinterpret_cast<const f32x4 *>(ss + 256 + 16 * jt); };
-        bf16x8 pop[MTPW][2];
-        step_qk_softmax<MTPW, PER_TOKEN>(st, rw, kr, ks_at, vs_at, k_fac, tok_lo + n * kStep, kg, pop, [] {});
-        uint4 vr[8];
-#pragma unroll
-        for (int m = 0; m < 8; ++m)
-            vr[m] = *reinterpret_cast<const uint4 *>(sk + kStageV + kg * 2048 + (16 * m + l16) * 16);
-        step_pv<MTPW>(st, vr, pop);
-    }
-    finish_rows<MTPW>(st, p, wave * MTPW, l16, kg, v_fac, sink);
-}
-
-// Layout <MTPW, RS, NS>: NS >= 1 streams K / V through registers (attend_range);
-// NS == 0 stages them through LDS for RS waves that all take every step
-// (attend_range_staged).
-template <int RS, int NS>
-constexpr int kThreads = RS * (NS > 0 ? NS : 1) * 64;
-
-template <int MTPW, int RS, int NS, bool PER_TOKEN, class Sink>
-__device__ __forceinline__ void attend(const DecodeParams &p, int b, int h, int ctx, int tok_lo, int tok_hi,
-                                       const int32_t *bt_row, int row_len, const Sink &sink) {
-    if constexpr (NS == 0)
-        attend_range_staged<MTPW, RS, PER_TOKEN>(p, b, h, ctx, tok_lo, tok_hi, bt_row, row_len, sink);
-    else
-        attend_range<MTPW, RS, NS, PER_TOKEN>(p, b, h, ctx, tok_lo, tok_hi, bt_row, sink);
-}
-
-template <int MTPW, int RS, int NS, bool PER_TOKEN>
-__global__ __launch_bounds__((kThreads<RS, NS>), (kWavesFor<MTPW, NS>)) void pa_decode_partition_kernel(const DecodeParams p) {
-    const int b = blockIdx.x;
-    const int h = blockIdx.y;
-    const int z = blockIdx.z;
-
-    // ---- slot -> token range (integer planner, bit-exact with the oracle)
-    int64_t ctx64 = p.ctx[b];
-    const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
-    ctx64 = ctx64 < 0 ? 0 : (ctx64 > cap ? cap : ctx64);
-    const int ctx = (int)ctx64;
-    const int T = (ctx + kPartition - 1) / kPartition;
-    int seq_start = 0;
-    if (p.sw > 0) seq_start = max(ctx - p.ql - p.sw, 0);
-    const int first_tile = seq_start / kPartition;
-    const int vis = T - first_tile;
-    const int pps = vis > 0 ? (vis + p.max_parts - 1) / p.max_parts : 0;
-    const int plo = first_tile + z * pps;
-    const int phi = min(plo + pps, T);
-    int tok_lo = plo * kPartition;
-    const int tok_hi = min(phi * kPartition, ctx);
-    if (tok_lo < seq_start) tok_lo = seq_start & ~(kGroup - 1);
-
-    const SlotSink sink{p,
-                        p.tmp_out + b * p.s_to_seq + h * p.s_to_head + z * p.s_to_part,
-                        p.exp_sums + b * p.s_es_seq + h * p.s_es_head + z * p.s_es_part,
-                        p.max_logits + b * p.s_es_seq + h * p.s_es_head + z * p.s_es_part,
-                        b,
-                        h};
-    attend<MTPW, RS, NS, PER_TOKEN>(p, b, h, ctx, tok_lo, tok_hi, p.bt + (int64_t)b * p.s_bt_seq, p.max_blocks, sink);
-}
-
-// ---------------------------------------------------------------- worklist path
-struct WorklistParams {
-    DecodeParams kv;  // caches, query, scales, shape; bt / max_blocks / partials unused
-    const int32_t *work_indptr;
-    const int32_t *work_info;
-    const int32_t *kv_page_indices;
-    const int32_t *kv_indptr;
-    const int32_t *partition_indptr;
-    float *po;
-    float *pl;
-    void *out;
-    int64_t s_out_seq, s_out_head;
-    int64_t s_po_row, s_pl_row;
-    int32_t batch, num_kv_heads, num_pages, max_work, partial_rows, output_rows, out_dtype;
-    int32_t bin_groups;  // > 1: bin group a runs on the workgroups of dispatch round a
-};
-
-// Where a work's rows go: output[qo_start + qi, qhead] when the work holds its
-// whole sequence (pidx < 0), else the f32 partial row pidx + ql + qi plus its
-// log-sum-exp (kernels/pa_decode_fp8.py:1612-1643).
-struct WorkSink {
-    const WorklistParams &w;
-    int h, qo_start, pidx;
-
-    template <int N>
-    __device__ __forceinline__ void row(int r, int d0, const float (&v)[N]) const {
-        const int g = w.kv.g;
-        const int qi = r / g, qhead = h * g + (r - qi * g);
-        if (pidx < 0) {
-            store_out<N>(w.out, w.out_dtype, (int64_t)(qo_start + qi) * w.s_out_seq + qhead * w.s_out_head + d0, v);
-            return;
-        }
-        float *dst = w.po + (int64_t)(pidx + w.kv.ql + qi) * w.s_po_row + qhead * kHeadDim + d0;
-#pragma unroll
-        for (int j = 0; j < N; j += 4) *reinterpret_cast<float4 *>(dst + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
-    }
-    __device__ __forceinline__ void stats(int r, float L, float m2) const {
-        if (pidx < 0) return;
-        const int g = w.kv.g;
-        const int qi = r / g, qhead = h * g + (r - qi * g);
-        w.pl[(int64_t)(pidx + w.kv.ql + qi) * w.s_pl_row + qhead] = L > 0.f ? m2 * kLn2 + __logf(L) : -INFINITY;
-    }
-};
-
-// Persistent decode over the get_pa_metadata_v1 worklist: workgroup c runs the
-// works [work_indptr[c], work_indptr[c+1]) of its bin one after another
-// (kernels/pa_decode_fp8.py:941-1721).  With bin_groups = G the device takes the
-// workgroups in G rounds of gridDim/G (one per CU each), and workgroup c of round
-// a = c / (gridDim/G) runs a bin of group a of some head: a schedule weighted by
-// group then gives the workgroups dispatched first, which issue ahead of the later
-// ones on their CU, the larger quotas.  Every field read from the worklist is
-// range-checked, so a malformed or overflowed worklist skips work instead of
-// touching memory outside the tensors.
-template <int MTPW, int RS, int NS, bool PER_TOKEN>
-__global__ __launch_bounds__((kThreads<RS, NS>), (kWavesFor<MTPW, NS>)) void pa_decode_worklist_kernel(const WorklistParams w) {
-    const DecodeParams &p = w.kv;
-    int c = blockIdx.x;
-    if (w.bin_groups > 1) {
-        const int per_round = gridDim.x / w.bin_groups;  // workgroups per dispatch round
-        const int per_group = per_round / w.num_kv_heads;  // bins of one head in one group
-        const int a = c / per_round, u = c - a * per_round;
-        const int k = u / per_group, j = u - k * per_group;
-        c = k * (per_round * w.bin_groups / w.num_kv_heads) + a * per_group + j;
-    }
-    const int wbeg = max(__builtin_amdgcn_readfirstlane(w.work_indptr[c]), 0);
-    const int wend = min(__builtin_amdgcn_readfirstlane(w.work_indptr[c + 1]), w.max_work);
-    for (int wi = wbeg; wi < wend; ++wi) {
-        const int32_t *info = w.work_info + (int64_t)wi * 8;
-        const int b = __builtin_amdgcn_readfirstlane(info[0]);
-        const int pidx = __builtin_amdgcn_readfirstlane(info[1]);
-        const int qo_start = __builtin_amdgcn_readfirstlane(info[2]);
-        const int kv_start = __builtin_amdgcn_readfirstlane(info[4]);
-        const int kv_end = __builtin_amdgcn_readfirstlane(info[5]);
-        const int qh_start = __builtin_amdgcn_readfirstlane(info[7]) & 0xffff;
-        const int h = qh_start / p.g;
-        if (b < 0 || b >= w.batch || h >= w.num_kv_heads) continue;
-        if (pidx < 0 ? (qo_start < 0 || qo_start > w.output_rows - p.ql)
-                     : (pidx > w.partial_rows - 2 * p.ql))
-            continue;
-        const int page0 = __builtin_amdgcn_readfirstlane(w.kv_indptr[b]);
-        const int page1 = __builtin_amdgcn_readfirstlane(w.kv_indptr[b + 1]);
-        if (page0 < 0 || page1 < page0 || page1 > w.num_pages) continue;
-        int64_t ctx64 = p.ctx[b];
-        const int64_t cap = (int64_t)(page1 - page0) << p.bs_log2;
-        ctx64 = ctx64 < 0 ? 0 : (ctx64 > cap ? cap : ctx64);
-        const int ctx = (int)ctx64;
-        const int pbase = __builtin_amdgcn_readfirstlane(w.partition_indptr[b]);
-        const int64_t lp0 = max((int64_t)kv_start - pbase, (int64_t)0);
-        const int64_t lp1 = (int64_t)kv_end - pbase;
-        const int tok_lo = (int)min(lp0 * kPartition, (int64_t)ctx);
-        const int tok_hi = (int)max(min(lp1 * kPartition, (int64_t)ctx), (int64_t)tok_lo);
-        const WorkSink sink{w, h, qo_start, pidx};
-        attend<MTPW, RS, NS, PER_TOKEN>(p, b, h, ctx, tok_lo, tok_hi, w.kv_page_indices + page0, page1 - page0, sink);
-    }
-}
 
 struct ReduceV1Params {
     void *out;
@@ -1049,15 +32,26 @@ struct ReduceV1Params {
     const int32_t *final_map;
     const int32_t *partial_map;
     int64_t s_po_row, s_po_head, s_pl_row, s_pl_head, s_out_row, s_out_head, s_lse_row, s_lse_head;
-    int32_t num_groups, num_heads, max_qlen, partial_rows, output_rows, partial_map_len, out_dtype;
+    int32_t num_groups, num_heads, max_qlen, partial_rows, output_rows, partial_map_len, out_dtype, head_dim;
 };
 
+__device__ __forceinline__ void store2(void *out, int out_dtype, int64_t off, float a0, float a1) {
+    if (out_dtype == PA_FP8_F32) {
+        *reinterpret_cast<float2 *>(reinterpret_cast<float *>(out) + off) = make_float2(a0, a1);
+    } else {
+        const uint32_t pk = out_dtype == PA_FP8_F16
+                                ? uint32_t(f32_to_f16_bits(a0)) | (uint32_t(f32_to_f16_bits(a1)) << 16)
+                                : uint32_t(f32_to_bf16_bits(a0)) | (uint32_t(f32_to_bf16_bits(a1)) << 16);
+        *reinterpret_cast<uint32_t *>(reinterpret_cast<uint16_t *>(out) + off) = pk;
+    }
+}
+
 // Merge of the partials of one (reduce group, query row, head) per wave, four
-// waves per workgroup; lane owns head dims 2*lane and 2*lane+1.  Lane j first
-// loads the log-sum-exp of partial j (all partials in parallel), the wave forms
-// LSE = log sum_j exp(lse_j) and the weights exp(lse_j - LSE), and the partial
-// rows are then summed four at a time with the weights and row indices broadcast
-// from the lanes that hold them.
+// waves per workgroup; lane owns head dims 2*lane, 2*lane+1 (+128 for the second
+// block of a head dim above 128).  Lane j first loads the log-sum-exp of partial j
+// (all partials in parallel), the wave forms LSE = log sum_j exp(lse_j) and the
+// weights exp(lse_j - LSE), and the partial rows are then summed four at a time
+// with the weights and row indices broadcast from the lanes that hold them.
 __global__ __launch_bounds__(256) void pa_reduce_v1_kernel(const ReduceV1Params p) {
     const int lane = threadIdx.x & 63;
     const int grp = blockIdx.x;
@@ -1089,59 +83,59 @@ __global__ __launch_bounds__(256) void pa_reduce_v1_kernel(const ReduceV1Params 
     for (int sh = 32; sh >= 1; sh >>= 1) wl += shfl_xor_f(wl, sh);
     const float inv = wl > 0.f ? 1.0f / wl : 0.0f;
 
-    // pass 2: weighted sum of the partial rows, 64 partials per round
-    float a0 = 0.f, a1 = 0.f;
-    for (int c0 = 0; c0 < np; c0 += 64) {
-        const int j = c0 + lane;
-        int r = -1;
-        float w = 0.f;
-        if (j < np) {
-            r = p.partial_map[j0 + j] + qi;
-            if (r >= 0 && r < p.partial_rows) w = fast_exp2((p.pl[r * p.s_pl_row + hd * p.s_pl_head] - Ms) * kLog2e) * inv;
-            else r = -1;
-        }
-        const int n = min(64, np - c0);
-        for (int k = 0; k < n; k += 4) {
-            float2 v[4];
-            float wk[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int src = min(k + u, n - 1);
-                wk[u] = k + u < n ? __shfl(w, src, 64) : 0.f;
-                const int rk = __shfl(r, src, 64);
-                v[u] = (wk[u] != 0.f && rk >= 0)
-                           ? *reinterpret_cast<const float2 *>(p.po + rk * p.s_po_row + hd * p.s_po_head + 2 * lane)
-                           : make_float2(0.f, 0.f);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                a0 += wk[u] * v[u].x;
-                a1 += wk[u] * v[u].y;
-            }
-        }
-    }
+    // pass 2: weighted sum of the partial rows, 64 partials per round, per block of
+    // 128 head dims
     const int64_t orow = qo_start + qi;
-    const int64_t off = orow * p.s_out_row + hd * p.s_out_head + 2 * lane;
-    if (p.out_dtype == PA_FP8_F32) {
-        *reinterpret_cast<float2 *>(reinterpret_cast<float *>(p.out) + off) = make_float2(a0, a1);
-    } else {
-        const uint32_t pk = p.out_dtype == PA_FP8_F16
-                                ? uint32_t(f32_to_f16_bits(a0)) | (uint32_t(f32_to_f16_bits(a1)) << 16)
-                                : uint32_t(f32_to_bf16_bits(a0)) | (uint32_t(f32_to_bf16_bits(a1)) << 16);
-        *reinterpret_cast<uint32_t *>(reinterpret_cast<uint16_t *>(p.out) + off) = pk;
+    for (int db = 0; db < p.head_dim; db += 128) {
+        const int d = db + 2 * lane;
+        const bool live_d = d < p.head_dim;
+        float a0 = 0.f, a1 = 0.f;
+        for (int c0 = 0; c0 < np; c0 += 64) {
+            const int j = c0 + lane;
+            int r = -1;
+            float w = 0.f;
+            if (j < np) {
+                r = p.partial_map[j0 + j] + qi;
+                if (r >= 0 && r < p.partial_rows)
+                    w = fast_exp2((p.pl[r * p.s_pl_row + hd * p.s_pl_head] - Ms) * kLog2e) * inv;
+                else
+                    r = -1;
+            }
+            const int n = min(64, np - c0);
+            for (int k = 0; k < n; k += 4) {
+                float2 v[4];
+                float wk[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int src = min(k + u, n - 1);
+                    wk[u] = k + u < n ? __shfl(w, src, 64) : 0.f;
+                    const int rk = __shfl(r, src, 64);
+                    v[u] = (wk[u] != 0.f && rk >= 0 && live_d)
+                               ? *reinterpret_cast<const float2 *>(p.po + rk * p.s_po_row + hd * p.s_po_head + d)
+                               : make_float2(0.f, 0.f);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    a0 += wk[u] * v[u].x;
+                    a1 += wk[u] * v[u].y;
+                }
+            }
+        }
+        if (live_d) store2(p.out, p.out_dtype, orow * p.s_out_row + hd * p.s_out_head + d, a0, a1);
     }
     if (p.final_lse != nullptr && lane == 0)
         p.final_lse[orow * p.s_lse_row + hd * p.s_lse_head] = wl > 0.f ? Ms + __logf(wl) : -INFINITY;
 }
 
 // The same merge with 16-byte accesses: one workgroup per (reduce group, query
-// row, 8 heads), thread t owning dims 4*(t%32) .. +3 of head 8*blockIdx.z + t/32.
-// The partial rows of a group are a uniform list (scalar loads); each thread then
-// issues its log-sum-exp loads and row loads together, so a group costs two
-// dependent memory round trips.  Partials are merged kRedBatch at a time when a
-// group has more.
+// row, 8 heads), thread t owning dims 4*(t%32) .. +3 (and 128 above them for the
+// second of NB 128-dim blocks) of head 8*blockIdx.z + t/32.  The partial rows of a
+// group are a uniform list (scalar loads); each thread then issues its
+// log-sum-exp loads and row loads together, so a group costs two dependent memory
+// round trips.  Partials are merged kRedBatch at a time when a group has more.
 constexpr int kRedBatch = 8;
 
+template <int NB>
 __global__ __launch_bounds__(256) void pa_reduce_v1_rows_kernel(const ReduceV1Params p) {
     const int grp = blockIdx.x, qi = blockIdx.y;
     const int hd = blockIdx.z * 8 + (threadIdx.x >> 5);
@@ -1153,18 +147,25 @@ __global__ __launch_bounds__(256) void pa_reduce_v1_rows_kernel(const ReduceV1Pa
     const int qo_end = p.final_map[2 * grp + 1];
     if (qi >= qo_end - qo_start || qo_start < 0 || qo_start + qi >= p.output_rows) return;
     const int np = j1 - j0;
+    bool live[NB];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) live[k] = d0 + 128 * k < p.head_dim;
+    auto row_at = [&](int r, int k) {
+        return live[k] ? *reinterpret_cast<const float4 *>(p.po + r * p.s_po_row + hd * p.s_po_head + d0 + 128 * k)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
 
     // first batch of rows and every log-sum-exp, issued before any is used
     float lse[kRedBatch];
-    float4 v[kRedBatch];
+    float4 v[kRedBatch][NB];
     int rr[kRedBatch];
 #pragma unroll
     for (int j = 0; j < kRedBatch; ++j) {
         const int r = j < np ? p.partial_map[j0 + j] + qi : -1;
         rr[j] = (r >= 0 && r < p.partial_rows) ? r : -1;
         lse[j] = rr[j] >= 0 ? p.pl[rr[j] * p.s_pl_row + hd * p.s_pl_head] : -INFINITY;
-        v[j] = rr[j] >= 0 ? *reinterpret_cast<const float4 *>(p.po + rr[j] * p.s_po_row + hd * p.s_po_head + d0)
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int k = 0; k < NB; ++k) v[j][k] = rr[j] >= 0 ? row_at(rr[j], k) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float mloc = -INFINITY;
 #pragma unroll
@@ -1185,51 +186,55 @@ __global__ __launch_bounds__(256) void pa_reduce_v1_rows_kernel(const ReduceV1Pa
         if (r >= 0 && r < p.partial_rows) wl += fast_exp2((p.pl[r * p.s_pl_row + hd * p.s_pl_head] - Ms) * kLog2e);
     }
     const float inv = wl > 0.f ? 1.0f / wl : 0.0f;
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 a[NB];
 #pragma unroll
-    for (int j = 0; j < kRedBatch; ++j) {
-        const float w = lse[j] * inv;
-        a.x += w * v[j].x;
-        a.y += w * v[j].y;
-        a.z += w * v[j].z;
-        a.w += w * v[j].w;
-    }
+    for (int k = 0; k < NB; ++k) a[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto accumulate = [&](float w, const float4 (&vj)[NB]) {
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            a[k].x += w * vj[k].x;
+            a[k].y += w * vj[k].y;
+            a[k].z += w * vj[k].z;
+            a[k].w += w * vj[k].w;
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < kRedBatch; ++j) accumulate(lse[j] * inv, v[j]);
     for (int jb = kRedBatch; jb < np; jb += kRedBatch) {
 #pragma unroll
         for (int j = 0; j < kRedBatch; ++j) {
             const int r = jb + j < np ? p.partial_map[j0 + jb + j] + qi : -1;
             rr[j] = (r >= 0 && r < p.partial_rows) ? r : -1;
             lse[j] = rr[j] >= 0 ? p.pl[rr[j] * p.s_pl_row + hd * p.s_pl_head] : -INFINITY;
-            v[j] = rr[j] >= 0 ? *reinterpret_cast<const float4 *>(p.po + rr[j] * p.s_po_row + hd * p.s_po_head + d0)
-                              : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int k = 0; k < NB; ++k) v[j][k] = rr[j] >= 0 ? row_at(rr[j], k) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
-        for (int j = 0; j < kRedBatch; ++j) {
-            const float w = rr[j] >= 0 ? fast_exp2((lse[j] - Ms) * kLog2e) * inv : 0.f;
-            a.x += w * v[j].x;
-            a.y += w * v[j].y;
-            a.z += w * v[j].z;
-            a.w += w * v[j].w;
-        }
+        for (int j = 0; j < kRedBatch; ++j) accumulate(rr[j] >= 0 ? fast_exp2((lse[j] - Ms) * kLog2e) * inv : 0.f, v[j]);
     }
     const int64_t orow = qo_start + qi;
-    const int64_t off = orow * p.s_out_row + hd * p.s_out_head + d0;
-    if (p.out_dtype == PA_FP8_F32) {
-        *reinterpret_cast<float4 *>(reinterpret_cast<float *>(p.out) + off) = a;
-    } else {
-        const bool f16 = p.out_dtype == PA_FP8_F16;
-        const uint32_t lo = f16 ? uint32_t(f32_to_f16_bits(a.x)) | (uint32_t(f32_to_f16_bits(a.y)) << 16)
-                                : uint32_t(f32_to_bf16_bits(a.x)) | (uint32_t(f32_to_bf16_bits(a.y)) << 16);
-        const uint32_t hi = f16 ? uint32_t(f32_to_f16_bits(a.z)) | (uint32_t(f32_to_f16_bits(a.w)) << 16)
-                                : uint32_t(f32_to_bf16_bits(a.z)) | (uint32_t(f32_to_bf16_bits(a.w)) << 16);
-        *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.out) + off) = make_uint2(lo, hi);
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+        if (!live[k]) continue;
+        const int64_t off = orow * p.s_out_row + hd * p.s_out_head + d0 + 128 * k;
+        if (p.out_dtype == PA_FP8_F32) {
+            *reinterpret_cast<float4 *>(reinterpret_cast<float *>(p.out) + off) = a[k];
+        } else {
+            const bool f16 = p.out_dtype == PA_FP8_F16;
+            const uint32_t lo = f16 ? uint32_t(f32_to_f16_bits(a[k].x)) | (uint32_t(f32_to_f16_bits(a[k].y)) << 16)
+                                    : uint32_t(f32_to_bf16_bits(a[k].x)) | (uint32_t(f32_to_bf16_bits(a[k].y)) << 16);
+            const uint32_t hi = f16 ? uint32_t(f32_to_f16_bits(a[k].z)) | (uint32_t(f32_to_f16_bits(a[k].w)) << 16)
+                                    : uint32_t(f32_to_bf16_bits(a[k].z)) | (uint32_t(f32_to_bf16_bits(a[k].w)) << 16);
+            *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.out) + off) = make_uint2(lo, hi);
+        }
     }
     if (p.final_lse != nullptr && d0 == 0)
         p.final_lse[orow * p.s_lse_row + hd * p.s_lse_head] = wl > 0.f ? Ms + __logf(wl) : -INFINITY;
 }
 
 // Log-sum-exp merge of the P partials of one (sequence, kv head, query row):
-// one wave, lane owns head dims 2*lane and 2*lane+1 (kernels/pa_decode_swa.py:954-1130).
+// one wave, lane owns head dims 2*lane and 2*lane+1 of each 128-dim block
+// (kernels/pa_decode_swa.py:954-1130).
 template <int OUT>
 __global__ __launch_bounds__(64) void pa_lse_reduce_kernel(const ReduceParams p) {
     const int lane = threadIdx.x;
@@ -1253,69 +258,41 @@ __global__ __launch_bounds__(64) void pa_lse_reduce_kernel(const ReduceParams p)
     for (int sh = 32; sh >= 1; sh >>= 1) wl += shfl_xor_f(wl, sh);
     const float inv = wl > 0.f ? 1.0f / wl : 0.0f;
 
-    float a0 = 0.f, a1 = 0.f;
+    constexpr int NB = kMaxHeadDim / 128;
+    bool live[NB];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) live[k] = 2 * lane + 128 * k < p.head_dim;
+    float a0[NB], a1[NB];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) a0[k] = a1[k] = 0.f;
     for (int z = 0; z < P; ++z) {
         const float w = es[z * p.s_es_part] * fast_exp2((ml[z * p.s_es_part] - Ms) * kLog2e) * inv;
         if (w != 0.f) {
-            const uint32_t two = *reinterpret_cast<const uint32_t *>(to + z * p.s_to_part);
-            a0 += w * bf16_bits_to_f32(uint16_t(two & 0xffffu));
-            a1 += w * bf16_bits_to_f32(uint16_t(two >> 16));
+#pragma unroll
+            for (int k = 0; k < NB; ++k) {
+                if (!live[k]) continue;
+                const uint32_t two = *reinterpret_cast<const uint32_t *>(to + z * p.s_to_part + 128 * k);
+                a0[k] += w * bf16_bits_to_f32(uint16_t(two & 0xffffu));
+                a1[k] += w * bf16_bits_to_f32(uint16_t(two >> 16));
+            }
         }
     }
     const int qi = r / p.g, gi = r - (r / p.g) * p.g;
     const int64_t off = b * p.s_o_seq + qi * p.s_o_len + h * p.s_o_head + gi * p.s_o_group + 2 * lane;
-    if constexpr (OUT == PA_FP8_F32) {
-        float *o = reinterpret_cast<float *>(p.out) + off;
-        *reinterpret_cast<float2 *>(o) = make_float2(a0, a1);
-    } else if constexpr (OUT == PA_FP8_F16) {
-        uint16_t *o = reinterpret_cast<uint16_t *>(p.out) + off;
-        *reinterpret_cast<uint32_t *>(o) = uint32_t(f32_to_f16_bits(a0)) | (uint32_t(f32_to_f16_bits(a1)) << 16);
-    } else {
-        uint16_t *o = reinterpret_cast<uint16_t *>(p.out) + off;
-        *reinterpret_cast<uint32_t *>(o) = uint32_t(f32_to_bf16_bits(a0)) | (uint32_t(f32_to_bf16_bits(a1)) << 16);
-    }
-}
-
-template <int MTPW, int RS, int NS, bool PT>
-hipError_t launch_decode(const DecodeParams &p, dim3 grid, hipStream_t s) {
-    hipLaunchKernelGGL((pa_decode_partition_kernel<MTPW, RS, NS, PT>), grid, dim3((kThreads<RS, NS>)), 0, s, p);
-    return hipGetLastError();
-}
-
-// Wave layout per number of 16-row query groups (ql * group_size / 16, rounded up):
-//   one group    -> <1,1,4>: four waves split the steps;
-//   two groups   -> <2,1,4>: every wave holds both groups, four waves split the steps;
-//   3 / 4 groups -> <1,4,0>: one wave per group, the workgroup's steps staged through
-//                   an LDS ring that every wave reads.
-// The waves of the one-group layout come with the launch (waves_per_slot).
-
-template <bool PT>
-hipError_t dispatch_decode(const DecodeParams &p, int mtp, int waves, dim3 grid, hipStream_t s) {
-    switch (mtp) {
-    case 1:
-        switch (waves) {
-        case 1: return launch_decode<1, 1, 1, PT>(p, grid, s);
-        case 2: return launch_decode<1, 1, 2, PT>(p, grid, s);
-        case 8: return launch_decode<1, 1, 8, PT>(p, grid, s);
-        default: return launch_decode<1, 1, 4, PT>(p, grid, s);
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+        if (!live[k]) continue;
+        if constexpr (OUT == PA_FP8_F32) {
+            float *o = reinterpret_cast<float *>(p.out) + off + 128 * k;
+            *reinterpret_cast<float2 *>(o) = make_float2(a0[k], a1[k]);
+        } else if constexpr (OUT == PA_FP8_F16) {
+            uint16_t *o = reinterpret_cast<uint16_t *>(p.out) + off + 128 * k;
+            *reinterpret_cast<uint32_t *>(o) = uint32_t(f32_to_f16_bits(a0[k])) | (uint32_t(f32_to_f16_bits(a1[k])) << 16);
+        } else {
+            uint16_t *o = reinterpret_cast<uint16_t *>(p.out) + off + 128 * k;
+            *reinterpret_cast<uint32_t *>(o) =
+                uint32_t(f32_to_bf16_bits(a0[k])) | (uint32_t(f32_to_bf16_bits(a1[k])) << 16);
         }
-    case 2: return launch_decode<2, 1, 4, PT>(p, grid, s);
-    default: return launch_decode<1, 4, 0, PT>(p, grid, s);
-    }
-}
-
-template <int MTPW, int RS, int NS, bool PT>
-hipError_t launch_worklist(const WorklistParams &w, dim3 grid, hipStream_t s) {
-    hipLaunchKernelGGL((pa_decode_worklist_kernel<MTPW, RS, NS, PT>), grid, dim3((kThreads<RS, NS>)), 0, s, w);
-    return hipGetLastError();
-}
-
-template <bool PT>
-hipError_t dispatch_worklist(const WorklistParams &w, int mtp, dim3 grid, hipStream_t s) {
-    switch (mtp) {
-    case 1: return launch_worklist<1, 1, 4, PT>(w, grid, s);
-    case 2: return launch_worklist<2, 1, 4, PT>(w, grid, s);
-    default: return launch_worklist<1, 4, 0, PT>(w, grid, s);
     }
 }
 
@@ -1328,6 +305,27 @@ int log2_pow2(int v) {
     return l;
 }
 
+bool decode_head_dim(int d) { return d == 64 || d == 128 || d == 192 || d == 256; }
+
+hipError_t run_partition(int d, const DecodeParams &p, bool pt, bool v4, int mtp, int waves, dim3 grid,
+                         hipStream_t s) {
+    switch (d) {
+    case 64: return dispatch_partition<64>(p, pt, v4, mtp, waves, grid, s);
+    case 192: return dispatch_partition<192>(p, pt, v4, mtp, waves, grid, s);
+    case 256: return dispatch_partition<256>(p, pt, v4, mtp, waves, grid, s);
+    default: return dispatch_partition<128>(p, pt, v4, mtp, waves, grid, s);
+    }
+}
+
+hipError_t run_worklist(int d, const WorklistParams &w, bool pt, bool v4, int mtp, dim3 grid, hipStream_t s) {
+    switch (d) {
+    case 64: return dispatch_worklist<64>(w, pt, v4, mtp, grid, s);
+    case 192: return dispatch_worklist<192>(w, pt, v4, mtp, grid, s);
+    case 256: return dispatch_worklist<256>(w, pt, v4, mtp, grid, s);
+    default: return dispatch_worklist<128>(w, pt, v4, mtp, grid, s);
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -1338,9 +336,10 @@ const char *pa_fp8_status_string(int status) {
     switch (status) {
     case PA_FP8_OK: return "ok";
     case PA_FP8_ERR_NULL_POINTER: return "a required pointer is NULL";
-    case PA_FP8_ERR_HEAD_DIM: return "unsupported head_dim (decode: 128; KV-cache writer: a multiple of 16 up to 1024)";
+    case PA_FP8_ERR_HEAD_DIM:
+        return "unsupported head_dim (decode: 64, 128, 192 or 256; KV-cache writer: a multiple of 16 up to 1024)";
     case PA_FP8_ERR_BLOCK_SIZE: return "block_size must be a power of two >= 16";
-    case PA_FP8_ERR_GROUP: return "query_length * query_group_size must be in 1..64";
+    case PA_FP8_ERR_GROUP: return "query_length * query_group_size must be in 1..65535";
     case PA_FP8_ERR_SHAPE: return "a size, stride or alignment is out of range";
     case PA_FP8_ERR_DTYPE: return "unsupported dtype";
     case PA_FP8_ERR_PARTITIONS: return "max_context_partition_num must be in 1..65535";
@@ -1356,14 +355,16 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
     if (!a) return PA_FP8_ERR_NULL_POINTER;
     if (a->batch_size < 0 || a->num_kv_heads <= 0 || a->query_group_size <= 0 || a->query_length <= 0)
         return PA_FP8_ERR_SHAPE;
-    if (a->head_dim != kHeadDim) return PA_FP8_ERR_HEAD_DIM;
+    if (!decode_head_dim(a->head_dim)) return PA_FP8_ERR_HEAD_DIM;
     const int bs_log2 = log2_pow2(a->block_size);
     if (bs_log2 < 4) return PA_FP8_ERR_BLOCK_SIZE;
-    const int eqgs = a->query_length * a->query_group_size;
-    if (eqgs < 1 || eqgs > 64) return PA_FP8_ERR_GROUP;
+    const int64_t eqgs64 = (int64_t)a->query_length * a->query_group_size;
+    if (eqgs64 < 1 || eqgs64 > 65535) return PA_FP8_ERR_GROUP;
+    const int eqgs = (int)eqgs64;
     if (a->max_context_partition_num < 1 || a->max_context_partition_num > 65535) return PA_FP8_ERR_PARTITIONS;
     if (a->query_dtype != PA_FP8_BF16 && a->query_dtype != PA_FP8_F16) return PA_FP8_ERR_DTYPE;
     if (a->num_kv_heads > 65535 || a->sliding_window < 0) return PA_FP8_ERR_SHAPE;
+    if (a->value_layout != PA_FP8_V_TRANS && a->value_layout != PA_FP8_V_4D) return PA_FP8_ERR_LAYOUT;
     if (a->waves_per_slot != 0 && a->waves_per_slot != 1 && a->waves_per_slot != 2 && a->waves_per_slot != 4 &&
         a->waves_per_slot != 8)
         return PA_FP8_ERR_SHAPE;
@@ -1372,6 +373,8 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
         if (a->out_dtype != PA_FP8_BF16 && a->out_dtype != PA_FP8_F16 && a->out_dtype != PA_FP8_F32)
             return PA_FP8_ERR_DTYPE;
     }
+    const int chunks = (eqgs + kRowChunk - 1) / kRowChunk;
+    if ((int64_t)a->batch_size * chunks > 0x7fffffff) return PA_FP8_ERR_SHAPE;
     if (a->batch_size == 0) return PA_FP8_OK;
     if (!a->query || !a->key_cache || !a->value_cache || !a->block_tables || !a->context_lengths || !a->key_scale ||
         !a->value_scale)
@@ -1434,6 +437,7 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
     p.max_parts = a->max_context_partition_num;
     p.sw = a->sliding_window;
     p.q_f16 = a->query_dtype == PA_FP8_F16;
+    p.chunks = chunks;
     p.qk_scale = a->softmax_scale * kLog2e;
     p.direct = a->direct_output ? 1 : 0;
     p.out = a->output;
@@ -1443,12 +447,11 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
     p.s_o_group = a->stride_o_group;
     p.out_dtype = a->out_dtype;
 
-    const dim3 grid(a->batch_size, a->num_kv_heads, a->max_context_partition_num);
+    const dim3 grid(a->batch_size * chunks, a->num_kv_heads, a->max_context_partition_num);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const int mtp = (eqgs + 15) / 16;
-    const int waves = a->waves_per_slot;
-    const hipError_t err =
-        a->per_token_kv ? dispatch_decode<true>(p, mtp, waves, grid, s) : dispatch_decode<false>(p, mtp, waves, grid, s);
+    const int mtp = (min(eqgs, kRowChunk) + 15) / 16;
+    const hipError_t err = run_partition(a->head_dim, p, a->per_token_kv != 0, a->value_layout == PA_FP8_V_4D, mtp,
+                                         a->waves_per_slot, grid, s);
     return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
 }
 
@@ -1456,9 +459,9 @@ int pa_fp8_lse_reduce(const pa_fp8_reduce_args *a, void *stream) {
     if (!a) return PA_FP8_ERR_NULL_POINTER;
     if (a->batch_size < 0 || a->num_kv_heads <= 0 || a->query_group_size <= 0 || a->query_length <= 0)
         return PA_FP8_ERR_SHAPE;
-    if (a->head_dim != kHeadDim) return PA_FP8_ERR_HEAD_DIM;
+    if (a->head_dim <= 0 || a->head_dim > kMaxHeadDim || (a->head_dim & 1)) return PA_FP8_ERR_HEAD_DIM;
     if (a->max_context_partition_num < 1) return PA_FP8_ERR_PARTITIONS;
-    const int eqgs = a->query_length * a->query_group_size;
+    const int64_t eqgs = (int64_t)a->query_length * a->query_group_size;
     if (eqgs > 65535 || a->num_kv_heads > 65535) return PA_FP8_ERR_SHAPE;
     if (a->out_dtype != PA_FP8_BF16 && a->out_dtype != PA_FP8_F16 && a->out_dtype != PA_FP8_F32)
         return PA_FP8_ERR_DTYPE;
@@ -1488,7 +491,8 @@ int pa_fp8_lse_reduce(const pa_fp8_reduce_args *a, void *stream) {
     p.s_to_group = a->stride_to_group;
     p.g = a->query_group_size;
     p.max_parts = a->max_context_partition_num;
-    const dim3 grid(a->batch_size, a->num_kv_heads, eqgs);
+    p.head_dim = a->head_dim;
+    const dim3 grid(a->batch_size, a->num_kv_heads, (unsigned)eqgs);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     switch (a->out_dtype) {
     case PA_FP8_F32: hipLaunchKernelGGL(pa_lse_reduce_kernel<PA_FP8_F32>, grid, dim3(64), 0, s, p); break;
@@ -1503,15 +507,19 @@ int pa_fp8_decode_worklist(const pa_fp8_worklist_args *a, void *stream) {
     if (!a) return PA_FP8_ERR_NULL_POINTER;
     if (a->batch_size < 0 || a->num_kv_heads <= 0 || a->query_group_size <= 0 || a->query_length <= 0)
         return PA_FP8_ERR_SHAPE;
-    if (a->head_dim != kHeadDim) return PA_FP8_ERR_HEAD_DIM;
+    if (!decode_head_dim(a->head_dim)) return PA_FP8_ERR_HEAD_DIM;
     const int bs_log2 = log2_pow2(a->block_size);
     if (bs_log2 < 4) return PA_FP8_ERR_BLOCK_SIZE;
-    const int eqgs = a->query_length * a->query_group_size;
-    if (eqgs < 1 || eqgs > 64) return PA_FP8_ERR_GROUP;
+    const int64_t eqgs64 = (int64_t)a->query_length * a->query_group_size;
+    if (eqgs64 < 1 || eqgs64 > 65535) return PA_FP8_ERR_GROUP;
+    const int eqgs = (int)eqgs64;
     if (a->query_dtype != PA_FP8_BF16 && a->query_dtype != PA_FP8_F16) return PA_FP8_ERR_DTYPE;
     if (a->out_dtype != PA_FP8_BF16 && a->out_dtype != PA_FP8_F16 && a->out_dtype != PA_FP8_F32) return PA_FP8_ERR_DTYPE;
+    if (a->value_layout != PA_FP8_V_TRANS && a->value_layout != PA_FP8_V_4D) return PA_FP8_ERR_LAYOUT;
     if (a->num_cu < 0 || a->max_work < 0 || a->partial_rows < 0 || a->output_rows < 0 || a->num_pages < 0)
         return PA_FP8_ERR_SHAPE;
+    const int chunks = (eqgs + kRowChunk - 1) / kRowChunk;
+    if ((int64_t)a->num_cu * chunks > 0x7fffffff) return PA_FP8_ERR_SHAPE;
     if (a->batch_size == 0 || a->num_cu == 0) return PA_FP8_OK;
     if (!a->output || !a->query || !a->key_cache || !a->value_cache || !a->context_lengths || !a->key_scale ||
         !a->value_scale || !a->work_indptr || !a->work_info || !a->kv_indptr || !a->partition_indptr)
@@ -1555,6 +563,7 @@ int pa_fp8_decode_worklist(const pa_fp8_worklist_args *a, void *stream) {
     p.max_parts = 1;
     p.sw = 0;
     p.q_f16 = a->query_dtype == PA_FP8_F16;
+    p.chunks = chunks;
     p.qk_scale = a->softmax_scale * kLog2e;
     w.work_indptr = a->work_indptr;
     w.work_info = a->work_info;
@@ -1575,21 +584,24 @@ int pa_fp8_decode_worklist(const pa_fp8_worklist_args *a, void *stream) {
     w.partial_rows = a->partial_rows;
     w.output_rows = a->output_rows;
     w.out_dtype = a->out_dtype;
-    w.bin_groups = a->bin_groups > 1 && a->bin_groups <= 4 && a->num_cu % (a->bin_groups * a->num_kv_heads) == 0
+    w.head_dim = a->head_dim;
+    w.num_bins = a->num_cu;
+    w.bin_groups = chunks == 1 && a->bin_groups > 1 && a->bin_groups <= 4 &&
+                           a->num_cu % (a->bin_groups * a->num_kv_heads) == 0
                        ? a->bin_groups
                        : 1;
 
-    const dim3 grid(a->num_cu);
+    const dim3 grid(a->num_cu * chunks);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const int mtp = (eqgs + 15) / 16;
-    const hipError_t err =
-        a->per_token_kv ? dispatch_worklist<true>(w, mtp, grid, s) : dispatch_worklist<false>(w, mtp, grid, s);
+    const int mtp = (min(eqgs, kRowChunk) + 15) / 16;
+    const hipError_t err = run_worklist(a->head_dim, w, a->per_token_kv != 0, a->value_layout == PA_FP8_V_4D, mtp,
+                                        grid, s);
     return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
 }
 
 int pa_fp8_reduce_v1(const pa_fp8_reduce_v1_args *a, void *stream) {
     if (!a) return PA_FP8_ERR_NULL_POINTER;
-    if (a->head_dim != kHeadDim) return PA_FP8_ERR_HEAD_DIM;
+    if (a->head_dim <= 0 || a->head_dim > kMaxHeadDim || (a->head_dim & 1)) return PA_FP8_ERR_HEAD_DIM;
     if (a->num_groups < 0 || a->num_heads <= 0 || a->num_heads > 65535 || a->max_qlen <= 0 || a->max_qlen > 65535 ||
         a->partial_rows < 0 || a->output_rows < 0 || a->partial_map_len < 0)
         return PA_FP8_ERR_SHAPE;
@@ -1628,19 +640,24 @@ int pa_fp8_reduce_v1(const pa_fp8_reduce_v1_args *a, void *stream) {
     p.output_rows = a->output_rows;
     p.partial_map_len = a->partial_map_len;
     p.out_dtype = a->out_dtype;
-    // 16-byte path: 16-byte aligned partial rows and heads, 4-element aligned output heads
+    p.head_dim = a->head_dim;
+    // 16-byte path: 16-byte aligned partial rows and heads, 4-element aligned output
+    // heads, whole 4-dim pieces
     const bool vec = (reinterpret_cast<uintptr_t>(a->partial_output) & 15) == 0 &&
                      ((a->stride_po_row | a->stride_po_head) & 3) == 0 &&
                      (reinterpret_cast<uintptr_t>(a->output) & (4 * esz - 1)) == 0 &&
-                     ((a->stride_out_row | a->stride_out_head) & 3) == 0;
+                     ((a->stride_out_row | a->stride_out_head) & 3) == 0 && (a->head_dim & 3) == 0;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (vec) {
-        hipLaunchKernelGGL(pa_reduce_v1_rows_kernel, dim3(a->num_groups, a->max_qlen, (a->num_heads + 7) / 8), dim3(256),
-                           0, reinterpret_cast<hipStream_t>(stream), p);
+        const dim3 grid(a->num_groups, a->max_qlen, (a->num_heads + 7) / 8);
+        if (a->head_dim > 128)
+            hipLaunchKernelGGL(pa_reduce_v1_rows_kernel<2>, grid, dim3(256), 0, s, p);
+        else
+            hipLaunchKernelGGL(pa_reduce_v1_rows_kernel<1>, grid, dim3(256), 0, s, p);
     } else {
         const int64_t rows = (int64_t)a->num_heads * a->max_qlen;  // (qi, head) rows of a group, four per workgroup
         if ((rows + 3) / 4 > 65535) return PA_FP8_ERR_SHAPE;
-        hipLaunchKernelGGL(pa_reduce_v1_kernel, dim3(a->num_groups, (rows + 3) / 4), dim3(256), 0,
-                           reinterpret_cast<hipStream_t>(stream), p);
+        hipLaunchKernelGGL(pa_reduce_v1_kernel, dim3(a->num_groups, (rows + 3) / 4), dim3(256), 0, s, p);
     }
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;

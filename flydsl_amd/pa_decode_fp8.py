@@ -43,10 +43,22 @@ _REFERENCE_BINS_PER_CU = 3  # the reference's _PA_METADATA_GRID_OVERSUB (kernels
 _BIN_WEIGHTS = {2: (105, 100), 3: (130, 114, 100)}
 
 
-def _metadata_bins_per_cu(query_length: int, query_group_size: int) -> int:
-    return _PA_METADATA_GRID_OVERSUB_STAGED if query_length * query_group_size > 32 else _PA_METADATA_GRID_OVERSUB
+def _metadata_bins_per_cu(query_length: int, query_group_size: int, head_dim: int = 128) -> int:
+    """Worklist workgroups that fit a CU: at head_dim 128 and below two of the
+    register-streaming kernel and three of the LDS-staged one; at 192 one and two
+    (one wave per SIMD, a 76 KiB ring); at 256 one of either."""
+    staged = query_length * query_group_size > 32
+    if head_dim <= 128:
+        return _PA_METADATA_GRID_OVERSUB_STAGED if staged else _PA_METADATA_GRID_OVERSUB
+    if head_dim <= 192:
+        return 2 if staged else 1
+    return 1
 _PA_DECODE_PS_SMALL_BLOCK_SIZES = (16, 64)  # kernels/pa_decode_fp8.py:1955
 HEAD_DIM = 128
+# Head dims the decode kernels are built for: the multiples of 64 up to 256 (the
+# reference accepts every multiple of 64, kernels/pa_decode_fp8.py:969-970, :2084-2085).
+HEAD_DIMS = (64, 128, 192, 256)
+_MAX_QUERY_ROWS = 65535  # query_length * group size per kv head (the merge's grid)
 
 _PACKED_FP8_QUERY_DTYPES = tuple(
     dt
@@ -149,7 +161,10 @@ def _check_int32(name: str, t: torch.Tensor, ndim: int) -> None:
         raise ValueError(f"`{name}` must be a {ndim}-D int32 tensor, got {tuple(t.shape)} {t.dtype}")
 
 
-def _check_cache_layouts(key_cache: torch.Tensor, value_cache: torch.Tensor, head_size: int) -> int:
+def _check_cache_layouts(key_cache: torch.Tensor, value_cache: torch.Tensor, head_size: int):
+    """(block_size, trans_v) of the caches: K [nb, Hkv, D/16, bs, 16] and V either
+    trans_v [nb, Hkv, bs/16, D, 16] or 4-D [nb, Hkv, D, bs] (trans_v = V.ndim == 5,
+    kernels/pa_decode_fp8.py:2841), each contiguous within a (block, kv head) tile."""
     if key_cache.dim() != 5:
         raise ValueError(f"key_cache must be [num_blocks, kv_heads, head_dim/16, block_size, 16], got {tuple(key_cache.shape)}")
     if key_cache.element_size() != 1 or value_cache.element_size() != 1:
@@ -157,15 +172,20 @@ def _check_cache_layouts(key_cache: torch.Tensor, value_cache: torch.Tensor, hea
     nb, hkv, dc, bs, x = key_cache.shape
     if x != 16 or dc * 16 != head_size:
         raise ValueError(f"key_cache inner dims {tuple(key_cache.shape[2:])} do not match head_dim {head_size}")
-    if value_cache.dim() != 5:
-        raise NotImplementedError("pa_decode_ps_launch: trans_v=False (4-D value_cache) not yet supported.")
-    if tuple(value_cache.shape) != (nb, hkv, bs // 16, head_size, 16):
-        raise ValueError(f"value_cache {tuple(value_cache.shape)} is not the trans_v layout of key_cache")
     if key_cache.stride()[2:] != (bs * 16, 16, 1):
         raise ValueError("key_cache must be contiguous within each (block, kv head) tile")
-    if value_cache.stride()[2:] != (head_size * 16, 16, 1):
-        raise ValueError("value_cache must be contiguous within each (block, kv head) tile")
-    return bs
+    trans_v = value_cache.dim() == 5
+    if trans_v:
+        if tuple(value_cache.shape) != (nb, hkv, bs // 16, head_size, 16):
+            raise ValueError(f"value_cache {tuple(value_cache.shape)} is not the trans_v layout of key_cache")
+        if value_cache.stride()[2:] != (head_size * 16, 16, 1):
+            raise ValueError("value_cache must be contiguous within each (block, kv head) tile")
+    else:
+        if tuple(value_cache.shape) != (nb, hkv, head_size, bs):
+            raise ValueError(f"value_cache {tuple(value_cache.shape)} is not [num_blocks, kv_heads, head_dim, block_size]")
+        if value_cache.stride()[2:] != (bs, 1):
+            raise ValueError("value_cache must be contiguous within each (block, kv head) tile")
+    return bs, trans_v
 
 
 def _u8(t: torch.Tensor) -> torch.Tensor:
@@ -225,6 +245,7 @@ def _decode_args(
     a.per_token_kv = 1 if per_token_kv else 0
     a.query_dtype = _lib.PA_FP8_F16 if query.dtype == torch.float16 else _lib.PA_FP8_BF16
     a.softmax_scale = float(softmax_scale)
+    a.value_layout = _lib.PA_FP8_V_TRANS if value_cache.dim() == 5 else _lib.PA_FP8_V_4D
     return a
 
 
@@ -292,26 +313,29 @@ _TARGET_WORKGROUPS_PER_CU = 2
 _MAX_SLOT_TOKENS = 8192
 
 
-def _auto_partitions(dev, batch_size, num_kv_heads, max_tokens, sliding_window, query_length):
-    return _auto_layout(dev, batch_size, num_kv_heads, max_tokens, sliding_window, query_length)[0]
+def _auto_partitions(dev, batch_size, num_kv_heads, max_tokens, sliding_window, query_length, head_dim=HEAD_DIM):
+    return _auto_layout(dev, batch_size, num_kv_heads, max_tokens, sliding_window, query_length, head_dim)[0]
 
 
-def _auto_layout(dev, batch_size, num_kv_heads, max_tokens, sliding_window, query_length):
-    """(partition slots, waves per slot) for the launcher's default."""
+def _auto_layout(dev, batch_size, num_kv_heads, max_tokens, sliding_window, query_length, head_dim=HEAD_DIM):
+    """(partition slots, waves per slot) for the launcher's default.  Eight-wave
+    slots exist for head_dim 128 only; other head dims size the grid for four."""
     cus = _device_cu_count(dev)
     pairs = max(1, batch_size * num_kv_heads)
     span = min(max_tokens, sliding_window + query_length) if sliding_window > 0 else max_tokens
     tiles = max(1, _cdiv(span, KV_COMPUTE_BLOCK) + (1 if sliding_window > 0 else 0))
     least = _cdiv(span, _MAX_SLOT_TOKENS)
     p8 = max(1, min(max(_cdiv(cus, pairs), least), tiles))
-    if pairs * p8 <= cus:
+    if pairs * p8 <= cus and head_dim == HEAD_DIM:
         return p8, 8
     fill = _cdiv(cus * _TARGET_WORKGROUPS_PER_CU, pairs)
     return max(1, min(max(fill, least), tiles)), 4
 
 
-def _waves_per_slot(dev, batch_size, num_kv_heads, max_parts):
-    """Eight waves per slot when the grid fits one workgroup per CU, else four."""
+def _waves_per_slot(dev, batch_size, num_kv_heads, max_parts, head_dim=HEAD_DIM):
+    """Eight waves per slot when the grid fits one workgroup per CU (head_dim 128), else four."""
+    if head_dim != HEAD_DIM:
+        return 4
     return 8 if batch_size * num_kv_heads * max_parts <= _device_cu_count(dev) else 4
 
 
@@ -397,7 +421,7 @@ def _partitioned_plan(
         softmax_scale=softmax_scale,
     )
     out_dtype = _get_output_dtype_str(output)
-    dargs.waves_per_slot = _waves_per_slot(dev, batch_size, num_kv_heads, max_parts)
+    dargs.waves_per_slot = _waves_per_slot(dev, batch_size, num_kv_heads, max_parts, head_size)
     if direct:
         dargs.direct_output = 1
         dargs.out_dtype = {"bf16": _lib.PA_FP8_BF16, "f16": _lib.PA_FP8_F16, "f32": _lib.PA_FP8_F32}[out_dtype]
@@ -524,6 +548,7 @@ def _worklist_plan(
     w.query_dtype = _lib.PA_FP8_F16 if query.dtype == torch.float16 else _lib.PA_FP8_BF16
     w.out_dtype = {"bf16": _lib.PA_FP8_BF16, "f16": _lib.PA_FP8_F16, "f32": _lib.PA_FP8_F32}[out_dtype]
     w.softmax_scale = float(softmax_scale)
+    w.value_layout = _lib.PA_FP8_V_TRANS if value_cache.dim() == 5 else _lib.PA_FP8_V_4D
     # no partial rows past the first query_length: nothing was split, so there is nothing to merge
     v = None
     if po.shape[0] > query_length:
@@ -682,8 +707,8 @@ def _build_plan_checked(
             "bf16/f16 query inputs with kernel-internal query scale computation."
         )
     head_size = query.shape[-1]
-    if head_size != HEAD_DIM:
-        raise ValueError(f"Unsupported head_dim={head_size}; this build supports {HEAD_DIM}.")
+    if head_size not in HEAD_DIMS:
+        raise ValueError(f"Unsupported head_dim={head_size}; this build supports {', '.join(map(str, HEAD_DIMS))}.")
     if num_query_heads % num_kv_heads != 0:
         raise ValueError("Query heads must be divisible by KV heads")
     _check_int32("context_lengths", context_lengths, 1)
@@ -695,7 +720,7 @@ def _build_plan_checked(
     _get_output_dtype_str(output)
     if query.stride(2) != 1 or not output.is_contiguous():
         raise ValueError("query needs a unit last stride and output must be contiguous")
-    block_size = _check_cache_layouts(key_cache, value_cache, head_size)
+    block_size, trans_v = _check_cache_layouts(key_cache, value_cache, head_size)
     if block_size < 16 or block_size & (block_size - 1):
         raise ValueError(f"pa_decode_ps_launch: unsupported block_size={block_size}; expected a power of two >= 16.")
     per_token_kv = key_scale.ndim > 1
@@ -705,8 +730,8 @@ def _build_plan_checked(
         raise ValueError("key_scale and value_scale must both be per-tensor or both per-token")
     query_length = query.shape[0] // batch_size
     query_group_size = num_query_heads // num_kv_heads
-    if query_length * query_group_size > 64:
-        raise ValueError("query_length * (num_query_heads // num_kv_heads) must be <= 64")
+    if query_length * query_group_size > _MAX_QUERY_ROWS:
+        raise ValueError(f"query_length * (num_query_heads // num_kv_heads) must be <= {_MAX_QUERY_ROWS}")
     for name, t in (("query", query), ("key_cache", key_cache), ("value_cache", value_cache), ("output", output),
                     ("context_lengths", context_lengths), ("key_scale", key_scale), ("value_scale", value_scale)):
         if t.device != dev:
@@ -722,6 +747,9 @@ def _build_plan_checked(
     # not touched (they are scratch of the split-context kernels).
     balanced_worklist = (metadata is not None and kv_page_indices is not None and kv_indptr is not None
                          and not metadata.get("uniform_context", False))
+    if small and sliding_window <= 0 and not trans_v:
+        # the reference's small-block kernel reads trans_v only (kernels/pa_decode_fp8.py:2082-2083)
+        raise NotImplementedError("compile_pa_decode_ps: trans_v=False not yet supported.")
     if sliding_window <= 0 and (not small or balanced_worklist):
         if small:
             if is_graph_capturing and (exp_sums is None or max_logits is None or temporary_output is None):
@@ -751,7 +779,8 @@ def _build_plan_checked(
             max_context_partition_num = exp_sums.shape[2] if exp_sums.dim() == 4 else 0
         else:
             max_context_partition_num = _auto_partitions(
-                dev, batch_size, num_kv_heads, block_tables.shape[1] * block_size, sliding_window, query_length
+                dev, batch_size, num_kv_heads, block_tables.shape[1] * block_size, sliding_window, query_length,
+                head_size,
             )
     if max_context_partition_num < 1 or max_context_partition_num > 65535:
         raise ValueError(f"max_context_partition_num={max_context_partition_num} out of range [1, 65535]")
@@ -867,7 +896,7 @@ def get_pa_metadata(
         )
     schedules = [(num_sm, 0)]
     if tuned:
-        bins_per_cu = _metadata_bins_per_cu(query_length, gqa)
+        bins_per_cu = _metadata_bins_per_cu(query_length, gqa, head_size)
         t_sm = (cus * bins_per_cu // num_kv_heads) * num_kv_heads
         # quotas weighted by dispatch round, when every round holds whole groups of bins
         # and the parallel scheduler runs (the serial one, past 4096 batches, splits evenly)

@@ -2,16 +2,18 @@
 
 Builds seeded inputs in the tensor formats ``pa_decode_ps_launch`` consumes:
 
-* query        bf16 N(0,1)  [B*ql, Hq, 128]
-* key_cache    fp8 e4m3fn   [nb, Hkv, 8, bs, 16]      (uint8 storage)
-* value_cache  fp8 e4m3fn   [nb, Hkv, bs/16, 128, 16] (trans_v, uint8 storage)
+* query        bf16 N(0,1)  [B*ql, Hq, D] (D = 128 unless a config says otherwise)
+* key_cache    fp8 e4m3fn   [nb, Hkv, D/16, bs, 16]   (uint8 storage)
+* value_cache  fp8 e4m3fn   [nb, Hkv, bs/16, D, 16]   (trans_v, uint8 storage), or
+                            [nb, Hkv, D, bs]          (4-D, trans_v False)
 * key/value scales: per-tensor [1] (amax/448) or per-token [nb, Hkv, bs, 1]
 * block_tables int32 [B, max_blocks]: a random permutation of the physical
-  blocks, handed to the sequences in order; context_lengths int32 [B]
+  blocks, handed to the sequences in order (or, with bt_replace, entries drawn
+  with replacement, so pages are shared); context_lengths int32 [B]
 * kv_page_indices / kv_indptr int32: the same pages as one flat list
   (tests/kernels/test_pa.py:545-559), read by the persistent path
 
-K and V are drawn N(0,1) in float32 and quantised with scale = amax/448 and
+K and V are drawn N(0,1) (or U(-1,1)) in float32 and quantised with scale = amax/448 and
 ``(x / scale).to(torch.float8_e4m3fn)`` -- the quantisers of
 tests/kernels/test_pa.py:334-416 and tests/utils.py:29-73.  Generation runs
 on any torch device (chunked, so large caches fit).
@@ -46,6 +48,13 @@ class DecodeConfig:
     lognormal_sigma: float = 1.0
     num_physical_blocks: Optional[int] = None  # None: exactly the blocks the sequences use
     blocks_per_seq_stride: Optional[int] = None  # sequence b takes perm[b*stride : ...]
+    head_dim: int = HEAD_DIM
+    trans_v: bool = True  # value cache [nb, Hkv, bs/16, D, 16]; False: [nb, Hkv, D, bs]
+    # block-table entries drawn with replacement from num_physical_blocks (default:
+    # the blocks the sequences use), so pages repeat within and across sequences
+    # (tests/kernels/test_pa.py:713-716)
+    bt_replace: bool = False
+    dist: str = "normal"  # query / K / V draws: "normal" N(0,1) or "uniform" U(-1,1) (test_pa.py:62)
     description: str = field(default="", compare=False)
 
     @property
@@ -105,6 +114,11 @@ def block_tables_for(cfg: DecodeConfig, ctx: List[int], seed: int = 123):
             bt[b, : nblk[b]] = perm[b * stride : b * stride + nblk[b]]
         return bt, total
     total = sum(nblk) if cfg.num_physical_blocks is None else cfg.num_physical_blocks
+    if cfg.bt_replace:
+        bt = np.zeros((cfg.batch, max_blocks), dtype=np.int64)
+        for b in range(cfg.batch):
+            bt[b, : nblk[b]] = rng.integers(0, total, size=nblk[b])
+        return bt, total
     perm = rng.permutation(total)
     bt = np.zeros((cfg.batch, max_blocks), dtype=np.int64)
     off = 0
@@ -123,6 +137,12 @@ def _chunks(n: int, chunk: int):
         yield s, min(n, s + chunk)
 
 
+def _draw(shape, gen, dev, dist: str) -> torch.Tensor:
+    if dist == "uniform":
+        return torch.rand(shape, generator=gen, device=dev, dtype=torch.float32) * 2.0 - 1.0
+    return torch.randn(shape, generator=gen, device=dev, dtype=torch.float32)
+
+
 def build_kv_cache(
     num_blocks: int,
     num_kv_heads: int,
@@ -131,15 +151,24 @@ def build_kv_cache(
     device,
     seed: int = 123,
     chunk_blocks: int = 4096,
+    head_dim: int = HEAD_DIM,
+    trans_v: bool = True,
+    dist: str = "normal",
 ):
-    """Quantised caches (key_x, value_trans, key_scale, value_scale) on ``device``.
+    """Quantised caches (key_x, value, key_scale, value_scale) on ``device``; the
+    value cache is trans_v [nb, Hkv, bs/16, D, 16] or, with ``trans_v`` False,
+    4-D [nb, Hkv, D, bs].
 
-    K/V values are N(0,1) draws from a per-chunk seeded generator, token-major
-    [blocks, Hkv, bs, D] before packing.
+    K/V values are N(0,1) (or U(-1,1)) draws from a per-chunk seeded generator,
+    token-major [blocks, Hkv, bs, D] before packing.
     """
     dev = torch.device(device)
-    kx = torch.empty((num_blocks, num_kv_heads, HEAD_DIM // 16, block_size, 16), dtype=torch.uint8, device=dev)
-    vt = torch.empty((num_blocks, num_kv_heads, block_size // 16, HEAD_DIM, 16), dtype=torch.uint8, device=dev)
+    D = head_dim
+    kx = torch.empty((num_blocks, num_kv_heads, D // 16, block_size, 16), dtype=torch.uint8, device=dev)
+    if trans_v:
+        vt = torch.empty((num_blocks, num_kv_heads, block_size // 16, D, 16), dtype=torch.uint8, device=dev)
+    else:
+        vt = torch.empty((num_blocks, num_kv_heads, D, block_size), dtype=torch.uint8, device=dev)
     if per_token:
         ks = torch.empty((num_blocks, num_kv_heads, block_size, 1), dtype=torch.float32, device=dev)
         vs = torch.empty_like(ks)
@@ -147,7 +176,7 @@ def build_kv_cache(
 
     def draw(lo, hi, which):
         gen.manual_seed(seed * 1000003 + lo * 2 + which)
-        return torch.randn((hi - lo, num_kv_heads, block_size, HEAD_DIM), generator=gen, device=dev, dtype=torch.float32)
+        return _draw((hi - lo, num_kv_heads, block_size, D), gen, dev, dist)
 
     if not per_token:
         amax = [torch.zeros((), device=dev), torch.zeros((), device=dev)]
@@ -173,8 +202,11 @@ def build_kv_cache(
             kq = _quant_per_tensor(k, ks)
             vq = _quant_per_tensor(v, vs)
         n = hi - lo
-        kx[lo:hi] = kq.view(n, num_kv_heads, block_size, HEAD_DIM // 16, 16).permute(0, 1, 3, 2, 4)
-        vt[lo:hi] = vq.view(n, num_kv_heads, block_size // 16, 16, HEAD_DIM).permute(0, 1, 2, 4, 3)
+        kx[lo:hi] = kq.view(n, num_kv_heads, block_size, D // 16, 16).permute(0, 1, 3, 2, 4)
+        if trans_v:
+            vt[lo:hi] = vq.view(n, num_kv_heads, block_size // 16, 16, D).permute(0, 1, 2, 4, 3)
+        else:
+            vt[lo:hi] = vq.permute(0, 1, 3, 2)
         del k, v, kq, vq
     return kx, vt, ks, vs
 
@@ -186,9 +218,9 @@ def build_workload(cfg: DecodeConfig, device, seed: int = 123, context_lengths: 
     bt, nphys = block_tables_for(cfg, ctx, seed)
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    q = torch.randn((cfg.batch * cfg.query_length, cfg.num_q_heads, HEAD_DIM), generator=gen, device=dev,
-                    dtype=torch.float32).to(torch.bfloat16)
-    kx, vt, ks, vs = build_kv_cache(nphys, cfg.num_kv_heads, cfg.block_size, cfg.per_token, dev, seed)
+    q = _draw((cfg.batch * cfg.query_length, cfg.num_q_heads, cfg.head_dim), gen, dev, cfg.dist).to(torch.bfloat16)
+    kx, vt, ks, vs = build_kv_cache(nphys, cfg.num_kv_heads, cfg.block_size, cfg.per_token, dev, seed,
+                                    head_dim=cfg.head_dim, trans_v=cfg.trans_v, dist=cfg.dist)
     # flat page list of the persistent path (tests/kernels/test_pa.py:545-559)
     pages = [(c + cfg.block_size - 1) // cfg.block_size for c in ctx]
     kv_indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
@@ -242,7 +274,7 @@ def attended_tokens(ctx: List[int], query_length: int, sliding_window: int) -> L
 
 def kv_bytes(cfg: DecodeConfig, ctx: List[int]) -> int:
     """Algorithmic fp8 K+V bytes of one decode step: sum_b sum_h attended_b * 2 * D."""
-    return sum(attended_tokens(ctx, cfg.query_length, cfg.sliding_window)) * cfg.num_kv_heads * 2 * HEAD_DIM
+    return sum(attended_tokens(ctx, cfg.query_length, cfg.sliding_window)) * cfg.num_kv_heads * 2 * cfg.head_dim
 
 
 def algorithmic_bytes(cfg: DecodeConfig, ctx: List[int]) -> int:
@@ -250,7 +282,7 @@ def algorithmic_bytes(cfg: DecodeConfig, ctx: List[int]) -> int:
     att = attended_tokens(ctx, cfg.query_length, cfg.sliding_window)
     total = kv_bytes(cfg, ctx)
     total += sum(att) * cfg.num_kv_heads * 8 if cfg.per_token else 8
-    qo = cfg.batch * cfg.query_length * cfg.num_q_heads * HEAD_DIM * 2
+    qo = cfg.batch * cfg.query_length * cfg.num_q_heads * cfg.head_dim * 2
     total += 2 * qo
     total += sum((a + cfg.block_size - 1) // cfg.block_size for a in att) * 4
     total += 4 * cfg.batch

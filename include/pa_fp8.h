@@ -29,7 +29,7 @@ enum pa_fp8_status {
     PA_FP8_ERR_NULL_POINTER = 1,     /* a required pointer is NULL            */
     PA_FP8_ERR_HEAD_DIM = 2,         /* head_dim unsupported by the entry     */
     PA_FP8_ERR_BLOCK_SIZE = 3,       /* block_size not a power of two >= 16   */
-    PA_FP8_ERR_GROUP = 4,            /* query_length * group_size not in 1..64 */
+    PA_FP8_ERR_GROUP = 4,            /* query_length * group_size not in 1..65535 */
     PA_FP8_ERR_SHAPE = 5,            /* a size or stride out of range         */
     PA_FP8_ERR_DTYPE = 6,            /* unsupported query / output dtype      */
     PA_FP8_ERR_PARTITIONS = 7,       /* max_context_partition_num out of range */
@@ -40,6 +40,12 @@ enum pa_fp8_status {
 
 /* element types of query / output tensors */
 enum pa_fp8_dtype { PA_FP8_BF16 = 0, PA_FP8_F16 = 1, PA_FP8_F32 = 2 };
+
+/* value-cache layouts the decode reads (kernels/pa_decode_fp8.py:2841, trans_v = V.ndim == 5) */
+enum pa_fp8_value_layout {
+    PA_FP8_V_TRANS = 0,  /* [nb, Hkv, bs/16, D, 16]: 16 consecutive tokens of a head dim in 16 bytes */
+    PA_FP8_V_4D = 1      /* [nb, Hkv, D, bs]: every token of a head dim contiguous                    */
+};
 
 /*
  * Split-context decode: one workgroup per (sequence, kv head, partition slot).
@@ -52,12 +58,16 @@ enum pa_fp8_dtype { PA_FP8_BF16 = 0, PA_FP8_F16 = 1, PA_FP8_F32 = 2 };
  * the partitions start at tile max(ctx-ql-sw, 0)/256 (kernels/pa_decode_swa.py:1359-1368).
  *
  * Inputs:
- *   query          [B*ql, Hq, D] bf16 or f16 (query_dtype)
+ *   query          [B*ql, Hq, D] bf16 or f16 (query_dtype), D = head_dim in {64, 128, 192, 256}
  *   key_cache      [nb, Hkv, D/16, bs, 16] fp8 e4m3fn
- *   value_cache    [nb, Hkv, bs/16, D, 16] fp8 e4m3fn (trans_v layout)
+ *   value_cache    [nb, Hkv, bs/16, D, 16] (value_layout PA_FP8_V_TRANS) or
+ *                  [nb, Hkv, D, bs] (PA_FP8_V_4D) fp8 e4m3fn
  *   block_tables   [B, max_blocks] int32; context_lengths [B] int32
  *   key_scale / value_scale: per-tensor [1] f32, or per-token [nb, Hkv, bs, 1] f32
  *   (per_token_kv = 1, element = blk*stride_ks_block + h*stride_ks_head + slot)
+ *
+ * A workgroup holds up to 64 of the ql*g query rows of a (sequence, kv head); more
+ * rows (e.g. GQA 16 x ql 8) run as chunks of 64 in adjacent workgroups.
  *
  * Replaces the launcher of `compile_pa_decode_ps` (kernels/pa_decode_fp8.py:2739-2803,
  * called at :3061-3093) and of `compile_pa_decode_sw` (kernels/pa_decode_swa.py:1195-1724,
@@ -103,9 +113,10 @@ typedef struct pa_fp8_decode_args {
     void *output;
     int64_t stride_o_seq, stride_o_len, stride_o_head, stride_o_group;
     /* waves per workgroup when ql * query_group_size <= 16 (the waves split a slot's
-     * steps): 0 = 4, or 1, 2, 4, 8.  Eight suits grids of at most one workgroup per CU. */
+     * steps): 0 = 4, or 1, 2, 4, 8.  Eight suits grids of at most one workgroup per CU.
+     * Head dims other than 128 and 256 always run four. */
     int32_t waves_per_slot;
-    int32_t reserved;
+    int32_t value_layout;        /* pa_fp8_value_layout */
 } pa_fp8_decode_args;
 
 int pa_fp8_decode_partitions(const pa_fp8_decode_args *args, void *hip_stream);
@@ -115,7 +126,7 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *args, void *hip_stream);
  *   out[b, qi, h, gi, d] = sum_z w_z * tmp_out[b, h, z, qi*g+gi, d],
  *   w_z = s_z e^(m_z - M) / sum_z s_z e^(m_z - M),  M = max_z m_z
  * Output dtype bf16 / f16 / f32 (out_dtype); strides describe the 5-D view
- * [B, ql, Hkv, g, D] of the [B*ql, Hq, D] output.
+ * [B, ql, Hkv, g, D] of the [B*ql, Hq, D] output; head_dim even, at most 256.
  *
  * Replaces the launcher of `compile_pa_decode_sw_reduce`
  * (kernels/pa_decode_swa.py:1132-1183, called at kernels/pa_decode_fp8.py:3094-3120).
@@ -156,8 +167,9 @@ int pa_fp8_lse_reduce(const pa_fp8_reduce_args *args, void *hip_stream);
  *                        and the row's log-sum-exp (natural log; -inf when nothing is
  *                        visible) to partial_lse[(partial_qo_loc + ql + qi) * stride_pl_row + qhead].
  * Works whose batch, head or partial row fall outside the given sizes are skipped.
- * Q rows are batch * ql + qi.  Caches, scales and query as for
- * pa_fp8_decode_partitions (trans_v V layout, any power-of-two block size >= 16).
+ * Q rows are batch * ql + qi.  Caches, scales, query, head dims, value layouts
+ * and row chunks as for pa_fp8_decode_partitions (any power-of-two block size >= 16);
+ * with more than 64 rows the grid is num_cu * chunks.
  *
  * Replaces the launcher of `compile_pa_decode_metadata`
  * (kernels/pa_decode_fp8.py:941-1721, called at :3155-3187).
@@ -205,8 +217,9 @@ typedef struct pa_fp8_worklist_args {
      * device takes num_cu/G workgroups per round) and c % (num_cu/G) = k*(nspk/G) + j,
      * nspk = num_cu / num_kv_heads.  So bin group a of every head (see
      * pa_fp8_metadata_args.bin_weight) runs on the workgroups of round a.  Any
-     * permutation of the bins gives the same outputs. */
+     * permutation of the bins gives the same outputs.  Not applied with row chunks. */
     int32_t bin_groups;
+    int32_t value_layout;        /* pa_fp8_value_layout */
 } pa_fp8_worklist_args;
 
 int pa_fp8_decode_worklist(const pa_fp8_worklist_args *args, void *hip_stream);
@@ -222,7 +235,7 @@ int pa_fp8_decode_worklist(const pa_fp8_worklist_args *args, void *hip_stream);
  *   final_lse[qo_start + qi, h] = LSE (when final_lse is not NULL)
  * A row whose partials are all -inf gets 0 (and LSE -inf).  partial_output /
  * partial_lse point at the row the map's 0 refers to (the launcher passes
- * partial_output[query_length:]).
+ * partial_output[query_length:]).  head_dim even, at most 256.
  */
 typedef struct pa_fp8_reduce_v1_args {
     void *output;

@@ -62,7 +62,8 @@ def launch(w: Dict, max_parts: int = 0, out_dtype=torch.bfloat16, query=None, wi
         partials = {
             "exp_sums": torch.full(shape, float("nan"), device=q.device),
             "max_logits": torch.full(shape, float("nan"), device=q.device),
-            "temporary_output": torch.full(shape + (128,), float("nan"), device=q.device, dtype=torch.bfloat16),
+            "temporary_output": torch.full(shape + (cfg.head_dim,), float("nan"), device=q.device,
+                                           dtype=torch.bfloat16),
         }
     tag = pa_decode_ps_launch(
         out,
@@ -72,7 +73,7 @@ def launch(w: Dict, max_parts: int = 0, out_dtype=torch.bfloat16, query=None, wi
         w["context_lengths"],
         w["kv_page_indices"],
         w["kv_indptr"],
-        1.0 / math.sqrt(128),
+        1.0 / math.sqrt(q.shape[-1]),
         w["key_scale"],
         w["value_scale"],
         sliding_window=cfg.sliding_window,
@@ -118,7 +119,7 @@ def check_partials(w: Dict, partials: Dict, max_parts: int, batches: Iterable[in
     es = partials["exp_sums"].cpu().numpy()
     ml = partials["max_logits"].cpu().numpy()
     to = partials["temporary_output"].float().cpu().numpy()
-    scale = 1.0 / math.sqrt(128)
+    scale = 1.0 / math.sqrt(cfg.head_dim)
     for b in batches:
         ctx = int(w["context_list"][b])
         q, kf, vf = sequence_inputs(w, b)
@@ -161,7 +162,7 @@ def metadata_with_bins(w: Dict, num_cu: int) -> Dict:
     return {
         "work_indptr": wi, "work_info_flat": winfo.reshape(-1).contiguous(), "partition_indptr": pind,
         "reduce_indptr": ri, "reduce_final_map": rfm, "reduce_partial_map": rpm, "num_sm": num_cu,
-        "partial_output": torch.full(((nparts + 1) * ql, 1, hq, 128), float("nan"), device=dev),
+        "partial_output": torch.full(((nparts + 1) * ql, 1, hq, cfg.head_dim), float("nan"), device=dev),
         "partial_lse": torch.full(((nparts + 1) * ql, 1, hq, 1), float("nan"), device=dev),
     }
 
@@ -193,7 +194,7 @@ def check_worklist_partials(w: Dict, md: Dict) -> int:
     po_gpu = md["partial_output"].cpu().numpy()[:, 0]
     pl_gpu = md["partial_lse"].cpu().numpy()[:, 0, :, 0]
     _, po, pl = oatt.worklist_decode(
-        w["query"].float().cpu().numpy(), seq_kv, w["context_list"], ql, g, 1.0 / math.sqrt(128),
+        w["query"].float().cpu().numpy(), seq_kv, w["context_list"], ql, g, 1.0 / math.sqrt(cfg.head_dim),
         md["work_indptr"].cpu().numpy(), md["work_info_flat"].cpu().numpy(), md["partition_indptr"].cpu().numpy(),
         po_gpu.shape[0],
     )

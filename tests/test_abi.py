@@ -103,11 +103,19 @@ def _decode_args(lib, **over):
     "over,status",
     [
         ({}, 0),  # an empty batch is a no-op
-        ({"head_dim": 64}, 2),
+        ({"head_dim": 64}, 0),
+        ({"head_dim": 192}, 0),
+        ({"head_dim": 256}, 0),
+        ({"head_dim": 96}, 2),
+        ({"head_dim": 320}, 2),
         ({"block_size": 8}, 3),
         ({"block_size": 48}, 3),
-        ({"query_group_size": 65}, 4),
-        ({"query_length": 5, "query_group_size": 16}, 4),
+        ({"query_group_size": 65}, 0),  # more than 64 rows run as row chunks
+        ({"query_length": 8, "query_group_size": 16}, 0),
+        ({"query_group_size": 65536}, 4),
+        ({"query_length": 300, "query_group_size": 256}, 4),
+        ({"value_layout": 1}, 0),
+        ({"value_layout": 2}, 9),
         ({"max_context_partition_num": 0}, 7),
         ({"query_dtype": 2}, 6),
         ({"num_kv_heads": 0}, 5),
@@ -140,6 +148,8 @@ def test_reduce_and_metadata_validation(lib):
     assert lib.LIB.pa_fp8_lse_reduce(ctypes.byref(r), None) == 0
     r.out_dtype = 7
     assert lib.LIB.pa_fp8_lse_reduce(ctypes.byref(r), None) == 6
+    r.out_dtype, r.head_dim = 0, 320
+    assert lib.LIB.pa_fp8_lse_reduce(ctypes.byref(r), None) == 2
     m = lib.MetadataArgs()
     m.num_batches, m.gqa, m.num_heads_k, m.num_cu, m.kv_granularity, m.query_length = 4, 4, 8, 12, 256, 1
     assert lib.LIB.pa_fp8_metadata_v1(ctypes.byref(m), None) == 5  # 12 bins not a multiple of 8 heads
@@ -164,8 +174,12 @@ def _worklist_args(lib, **over):
         ({}, 0),  # an empty batch is a no-op
         ({"batch_size": 2, "num_cu": 0}, 0),  # no workgroups: nothing to launch
         ({"head_dim": 96}, 2),
+        ({"head_dim": 256}, 0),
         ({"block_size": 1000}, 3),
-        ({"query_length": 5, "query_group_size": 16}, 4),
+        ({"query_length": 5, "query_group_size": 16}, 0),  # row chunks
+        ({"query_length": 5, "query_group_size": 16384}, 4),
+        ({"value_layout": 1}, 0),
+        ({"value_layout": 5}, 9),
         ({"query_dtype": 2}, 6),
         ({"out_dtype": 5}, 6),
         ({"num_cu": -1}, 5),
@@ -181,6 +195,8 @@ def test_reduce_v1_validation(lib):
     r.num_groups, r.num_heads, r.head_dim, r.max_qlen, r.partial_map_len = 0, 8, 128, 1, 4
     assert lib.LIB.pa_fp8_reduce_v1(ctypes.byref(r), None) == 0  # no groups: no-op
     r.head_dim = 64
+    assert lib.LIB.pa_fp8_reduce_v1(ctypes.byref(r), None) == 0
+    r.head_dim = 258
     assert lib.LIB.pa_fp8_reduce_v1(ctypes.byref(r), None) == 2
     r.head_dim, r.num_groups, r.out_dtype = 128, 3, 9
     assert lib.LIB.pa_fp8_reduce_v1(ctypes.byref(r), None) == 6

@@ -64,7 +64,47 @@ def test_baseline_configs_with_metadata(name):
     md["uniform_context"] = False  # run the worklist kernel on every config, c2 included
     out, tag, _ = launch(w, metadata=md)
     assert tag == "ps_small_block"
-    compare_outputs(w, out, _spread(cfg.batch, 6))
+    # every sequence the schedule splits (its rows come from the merge) plus a spread
+    split = split_sequences(schedule_of(md))
+    print(f"[worklist] {name}: {len(split)} split sequences", flush=True)
+    compare_outputs(w, out, sorted(set(_spread(cfg.batch, 6)) | split))
+
+
+def split_sequences(sched):
+    """Batches with a work that writes partials (partial_qo_loc >= 0)."""
+    nw = int(sched["work_indptr"][-1])
+    info = sched["work_info_flat"][: 8 * nw].view(nw, 8).cpu().numpy()
+    return {int(b) for b, p in zip(info[:, 0], info[:, 1]) if p >= 0}
+
+
+# The reference's second case set (tests/kernels/test_pa.py:1207-1233, named
+# sliding_window_accuracy; its window option is 0): 16- and 1024-token pages,
+# heads (8,1) / (16,1), ql 1-4, per-token scales, context lengths U[ql, 8192],
+# batch 128, uniform(-1, 1) draws, block tables drawn with replacement
+# (:713-716).  Called as the reference's harness calls the launcher: the
+# metadata of get_pa_metadata, max_context_partition_num 8 (:852-856) and the
+# flat page list; 16-token pages also without metadata (the reference's
+# small-block kernel ignores it).
+@pytest.mark.parametrize("bs", [16, 1024])
+@pytest.mark.parametrize("heads", [(8, 1), (16, 1)])
+@pytest.mark.parametrize("ql", [1, 2, 3, 4])
+def test_reference_sliding_window_accuracy_cases(bs, heads, ql):
+    from flydsl_amd import get_pa_metadata
+
+    hq, hkv = heads
+    cfg = scaled(CONFIGS["c3"], name="sliding_window_accuracy", batch=128, num_q_heads=hq, num_kv_heads=hkv,
+                 block_size=bs, query_length=ql, per_token=True, ctx_kind="uniform", ctx_a=ql, ctx_b=8192,
+                 dist="uniform", bt_replace=True, num_physical_blocks=128 * ((16384 + bs - 1) // bs))
+    print(f"[worklist] sliding_window_accuracy bs {bs} heads {heads} ql {ql}", flush=True)
+    w = build_workload(cfg, "cuda", seed=123)
+    md = get_pa_metadata(w["query"], w["key_cache"], w["context_lengths"], w["kv_indptr"], hq, hkv)
+    out, tag, _ = launch(w, max_parts=8, metadata=md)
+    assert tag == ("ps_small_block" if bs == 16 else "ps_split_reduce")
+    check = sorted(set(_spread(cfg.batch, 12)) | set(sorted(split_sequences(schedule_of(md)))[:12]))
+    compare_outputs(w, out, check)
+    if bs == 16:
+        out2, _, _ = launch(w, max_parts=8)  # the partition kernel, as the reference's small-block route
+        compare_outputs(w, out2, _spread(cfg.batch, 12))
 
 
 @pytest.mark.parametrize("name", ["c3", "c5"])

@@ -211,9 +211,67 @@ def test_validation_errors(over, exc, match):
         plan(make(), max_parts=4, **over)
 
 
-def test_eqgs_limit():
-    with pytest.raises(ValueError, match="<= 64"):
-        plan(make(batch=1, hq=40, hkv=2, ql=4), max_parts=2)
+def test_query_rows_past_64_run_as_chunks():
+    """ql * g above 64 (here 80 and GQA 16 x ql 8 = 128) is planned like any other
+    shape (the kernels split the rows into chunks of 64); only the merge's grid
+    limit of 65535 rows per kv head is refused."""
+    p = plan(make(batch=1, hq=40, hkv=2, ql=4), max_parts=2)
+    assert p.dargs.query_length * p.dargs.query_group_size == 80 and p.rargs.query_group_size == 20
+    t = make_paged(bs=1024, hq=16, hkv=1, ql=8, batch=3, ctx=(1027, 300, 700))
+    assert plan(t, max_parts=0).wargs.query_length == 8
+    with pytest.raises(ValueError, match="65535"):
+        plan(make(batch=1, hq=4096, hkv=1, ql=16, max_blocks=2), max_parts=2)
+
+
+def make_4d(t):
+    """The same caches with the 4-D value layout [nb, Hkv, D, bs]."""
+    nb, hkv, _, bs, _ = t["key_cache"].shape
+    return {**t, "value_cache": torch.zeros(nb, hkv, 128, bs, dtype=torch.uint8)}
+
+
+def test_4d_value_cache_routing():
+    """The 4-D value layout (trans_v False) runs on the sliding-window and
+    persistent paths, as in the reference (kernels/pa_decode_swa.py:183-186,
+    kernels/pa_decode_fp8.py:283-286); the small-block kernel refuses it like the
+    reference's (:2082-2083), also when metadata would route it to the worklist."""
+    t = make_4d(make())
+    p = plan(t, sliding_window=300, max_parts=3)
+    assert p.tag == "ps_sw_partitioned" and p.dargs.value_layout == _lib.PA_FP8_V_4D
+    assert p.dargs.stride_v_block == 2 * 128 * 16 and p.dargs.stride_v_head == 128 * 16
+    assert plan(make(), sliding_window=300, max_parts=3).dargs.value_layout == _lib.PA_FP8_V_TRANS
+    tp = make_paged(bs=1024)
+    tp4 = make_4d(tp)
+    p = plan(tp4, max_parts=0)
+    assert p.tag == "ps_split_reduce" and p.wargs.value_layout == _lib.PA_FP8_V_4D
+    assert plan(tp, max_parts=0).wargs.value_layout == _lib.PA_FP8_V_TRANS
+    with pytest.raises(NotImplementedError, match="trans_v=False"):
+        plan(t, max_parts=4)
+    with pytest.raises(NotImplementedError, match="trans_v=False"):
+        plan(make_4d(make_paged(bs=16, ctx=(1027, 300, 2000), num_cu=3)), max_parts=4)
+    with pytest.raises(ValueError, match="head_dim, block_size"):
+        plan(t, sliding_window=300, max_parts=3, value_cache=torch.zeros(20, 2, 16, 128, dtype=torch.uint8))
+
+
+@pytest.mark.parametrize("d", [64, 192, 256])
+def test_other_head_dims(d):
+    """Head dims 64, 192 and 256 plan like 128 (the reference accepts multiples of 64,
+    kernels/pa_decode_fp8.py:2084-2085); eight-wave slots are for 128 only."""
+    t = make(max_blocks=2)
+    t = {**t, "query": torch.zeros(3, 8, d, dtype=torch.bfloat16), "output": torch.empty(3, 8, d, dtype=torch.bfloat16),
+         "key_cache": torch.zeros(20, 2, d // 16, 16, 16, dtype=torch.uint8),
+         "value_cache": torch.zeros(20, 2, 1, d, 16, dtype=torch.uint8)}
+    p = plan(t, max_parts=2)
+    assert p.dargs.head_dim == d and p.dargs.waves_per_slot == 4
+    assert tuple(p.keepalive[2].shape) == (3, 2, 2, 4, d)
+    assert pdf._auto_layout(None, 4, 8, 32768, 0, 1, d)[1] == 4
+
+
+def test_unsupported_head_dims():
+    t = make()
+    for d in (96, 320):
+        bad = {"query": torch.zeros(3, 8, d, dtype=torch.bfloat16), "output": torch.empty(3, 8, d, dtype=torch.bfloat16)}
+        with pytest.raises(ValueError, match="Unsupported head_dim"):
+            plan(t, max_parts=2, **bad)
 
 
 def test_graph_capture_requires_preallocated_partials():
