@@ -18,6 +18,8 @@ PA_FP8_BF16, PA_FP8_F16, PA_FP8_F32 = 0, 1, 2
 PA_FP8_CACHE_ELEM, PA_FP8_CACHE_FP8_TENSOR, PA_FP8_CACHE_FP8_TOKEN = 0, 1, 2
 PA_FP8_KV_FLASH, PA_FP8_KV_X_PACKED, PA_FP8_KV_X_TRANS = 0, 1, 2
 PA_FP8_V_TRANS, PA_FP8_V_4D = 0, 1
+PA_FP8_ERR_SCRATCH = 10
+PA_FP8_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -262,6 +264,7 @@ class RopeCacheArgs(ctypes.Structure):
 
 EXPORTED_SYMBOLS = (
     "pa_fp8_decode_partitions",
+    "pa_fp8_decode_partitions_noalloc",
     "pa_fp8_lse_reduce",
     "pa_fp8_decode_worklist",
     "pa_fp8_reduce_v1",
@@ -295,6 +298,8 @@ def _load() -> ctypes.CDLL:
         raise ImportError(f"libpa_fp8.so ABI version {ver} != expected {PA_FP8_ABI_VERSION}; rebuild the library")
     lib.pa_fp8_decode_partitions.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     lib.pa_fp8_decode_partitions.restype = ctypes.c_int
+    lib.pa_fp8_decode_partitions_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
+    lib.pa_fp8_decode_partitions_noalloc.restype = ctypes.c_int
     lib.pa_fp8_lse_reduce.argtypes = [ctypes.POINTER(ReduceArgs), _vp]
     lib.pa_fp8_lse_reduce.restype = ctypes.c_int
     lib.pa_fp8_decode_worklist.argtypes = [ctypes.POINTER(WorklistArgs), _vp]
@@ -322,6 +327,10 @@ def check(func: str, status: int) -> None:
 
 def decode_partitions(args: DecodeArgs, stream: int) -> None:
     check("pa_fp8_decode_partitions", LIB.pa_fp8_decode_partitions(ctypes.byref(args), _vp(stream)))
+
+
+def decode_partitions_noalloc(args: DecodeArgs, stream: int) -> None:
+    check("pa_fp8_decode_partitions_noalloc", LIB.pa_fp8_decode_partitions_noalloc(ctypes.byref(args), _vp(stream)))
 
 
 def lse_reduce(args: ReduceArgs, stream: int) -> None:

@@ -3,12 +3,51 @@
 // (pa_lse_reduce_kernel) and the merge of split worklist partials
 // (pa_reduce_v1_*_kernel, the role of aiter's pa_reduce_v1).  The decode kernels
 // themselves are in pa_decode_kernels.h, built per head dim in pa_decode_hd.hip.
+#include <mutex>
+
 #include "pa_decode_params.h"
 #include "pa_fp8.h"
 
 using namespace pa;
 
 namespace {
+
+// ---------------------------------------------------------------- static scratch
+// The partials of pa_fp8_decode_partitions_noalloc: a file-scope device array of
+// PA_FP8_NOALLOC_SCRATCH_BYTES, which every GPU the library runs on holds until
+// the process ends.  Host code must not pass `scratch` itself to a kernel (in host
+// code the name is a host-side stand-in, not a device address): its device
+// address on each device is looked up once, with that device current, and kept.
+__device__ __align__(256) uint8_t scratch[PA_FP8_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_ptr[kMaxDevices];  // device address of `scratch` on each device, nullptr until looked up
+
+// The device address of `scratch` on device dev (looked up on the first call for dev).
+int scratch_on(int dev, uint8_t **out) {
+    if (dev < 0 || dev >= kMaxDevices) return PA_FP8_ERR_SHAPE;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        int cur = -1;
+        hipError_t e = hipGetDevice(&cur);
+        if (e != hipSuccess) return PA_FP8_ERR_HIP + (int)e;
+        if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return PA_FP8_ERR_HIP + (int)e;
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (cur != dev) {
+            const hipError_t e2 = hipSetDevice(cur);
+            if (e == hipSuccess) e = e2;
+        }
+        if (e != hipSuccess) return PA_FP8_ERR_HIP + (int)e;
+        if (!ptr) return PA_FP8_ERR_NULL_POINTER;
+        g_scratch_ptr[dev] = static_cast<uint8_t *>(ptr);
+    }
+    *out = g_scratch_ptr[dev];
+    return PA_FP8_OK;
+}
+
+constexpr int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
 
 constexpr int kMaxHeadDim = 256;
 
@@ -345,6 +384,9 @@ const char *pa_fp8_status_string(int status) {
     case PA_FP8_ERR_PARTITIONS: return "max_context_partition_num must be in 1..65535";
     case PA_FP8_ERR_WORKLIST: return "worklist buffers too small for the schedule";
     case PA_FP8_ERR_LAYOUT: return "KV-cache layout or format not valid for these sizes";
+    case PA_FP8_ERR_SCRATCH:
+        return "partials exceed the static scratch of pa_fp8_decode_partitions_noalloc (32 MiB); "
+               "use pa_fp8_decode_partitions with caller-allocated partials";
     default: break;
     }
     if (status >= PA_FP8_ERR_HIP) return hipGetErrorString((hipError_t)(status - PA_FP8_ERR_HIP));
@@ -453,6 +495,74 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
     const hipError_t err = run_partition(a->head_dim, p, a->per_token_kv != 0, a->value_layout == PA_FP8_V_4D, mtp,
                                          a->waves_per_slot, grid, s);
     return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
+}
+
+int pa_fp8_decode_partitions_noalloc(const pa_fp8_decode_args *a, void *stream) {
+    if (!a) return PA_FP8_ERR_NULL_POINTER;
+    if (a->out_dtype != PA_FP8_BF16 && a->out_dtype != PA_FP8_F16 && a->out_dtype != PA_FP8_F32)
+        return PA_FP8_ERR_DTYPE;
+    pa_fp8_decode_args d = *a;
+    if (a->max_context_partition_num == 1) {  // one slot per sequence: the kernel writes the output itself
+        d.direct_output = 1;
+        d.exp_sums = d.max_logits = nullptr;
+        d.tmp_out = nullptr;
+        return pa_fp8_decode_partitions(&d, stream);
+    }
+    if (a->batch_size < 0 || a->num_kv_heads <= 0 || a->query_group_size <= 0 || a->query_length <= 0 ||
+        a->max_context_partition_num < 1 || !decode_head_dim(a->head_dim))
+        return pa_fp8_decode_partitions(&d, stream);  // its own status for these
+    const int64_t eqgs = (int64_t)a->query_length * a->query_group_size;
+    const int64_t n = (int64_t)a->batch_size * a->num_kv_heads * a->max_context_partition_num * eqgs;
+    const int64_t es_bytes = align256(n * 4);
+    const int64_t to_bytes = align256(n * a->head_dim * 2);
+    if (2 * es_bytes + to_bytes > PA_FP8_NOALLOC_SCRATCH_BYTES) return PA_FP8_ERR_SCRATCH;
+    if (a->batch_size == 0) return PA_FP8_OK;
+    if (!a->output) return PA_FP8_ERR_NULL_POINTER;
+    int dev = -1;
+    hipError_t e = stream ? hipStreamGetDevice(reinterpret_cast<hipStream_t>(stream), &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) return PA_FP8_ERR_HIP + (int)e;
+    uint8_t *base = nullptr;
+    const int st = scratch_on(dev, &base);
+    if (st != PA_FP8_OK) return st;
+    // partials in the scratch: exp_sums, max_logits [B, Hkv, P, eqgs] f32, tmp_out [B, Hkv, P, eqgs, D] bf16
+    const int64_t P = a->max_context_partition_num, D = a->head_dim;
+    d.direct_output = 0;
+    d.exp_sums = reinterpret_cast<float *>(base);
+    d.max_logits = reinterpret_cast<float *>(base + es_bytes);
+    d.tmp_out = base + 2 * es_bytes;
+    d.stride_es_seq = a->num_kv_heads * P * eqgs;
+    d.stride_es_head = P * eqgs;
+    d.stride_es_part = eqgs;
+    d.stride_to_seq = a->num_kv_heads * P * eqgs * D;
+    d.stride_to_head = P * eqgs * D;
+    d.stride_to_part = eqgs * D;
+    d.stride_to_group = D;
+    int status = pa_fp8_decode_partitions(&d, stream);
+    if (status != PA_FP8_OK) return status;
+    pa_fp8_reduce_args r = {};
+    r.output = a->output;
+    r.exp_sums = d.exp_sums;
+    r.max_logits = d.max_logits;
+    r.tmp_out = d.tmp_out;
+    r.stride_o_seq = a->stride_o_seq;
+    r.stride_o_len = a->stride_o_len;
+    r.stride_o_head = a->stride_o_head;
+    r.stride_o_group = a->stride_o_group;
+    r.stride_es_seq = d.stride_es_seq;
+    r.stride_es_head = d.stride_es_head;
+    r.stride_es_part = d.stride_es_part;
+    r.stride_to_seq = d.stride_to_seq;
+    r.stride_to_head = d.stride_to_head;
+    r.stride_to_part = d.stride_to_part;
+    r.stride_to_group = d.stride_to_group;
+    r.batch_size = a->batch_size;
+    r.num_kv_heads = a->num_kv_heads;
+    r.query_group_size = a->query_group_size;
+    r.query_length = a->query_length;
+    r.head_dim = a->head_dim;
+    r.max_context_partition_num = a->max_context_partition_num;
+    r.out_dtype = a->out_dtype;
+    return pa_fp8_lse_reduce(&r, stream);
 }
 
 int pa_fp8_lse_reduce(const pa_fp8_reduce_args *a, void *stream) {

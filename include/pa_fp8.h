@@ -35,6 +35,7 @@ enum pa_fp8_status {
     PA_FP8_ERR_PARTITIONS = 7,       /* max_context_partition_num out of range */
     PA_FP8_ERR_WORKLIST = 8,         /* metadata buffer too small             */
     PA_FP8_ERR_LAYOUT = 9,           /* cache layout / format not valid here  */
+    PA_FP8_ERR_SCRATCH = 10,         /* partials exceed the static scratch    */
     PA_FP8_ERR_HIP = 1000            /* 1000 + hipError_t of a failed launch  */
 };
 
@@ -120,6 +121,30 @@ typedef struct pa_fp8_decode_args {
 } pa_fp8_decode_args;
 
 int pa_fp8_decode_partitions(const pa_fp8_decode_args *args, void *hip_stream);
+
+/* Bytes of the static device scratch pa_fp8_decode_partitions_noalloc keeps its
+ * partials in (32 MiB on every GPU the library runs on, held until the process ends). */
+#define PA_FP8_NOALLOC_SCRATCH_BYTES (32 << 20)
+
+/*
+ * The split-context decode and its log-sum-exp reduce in one call that allocates
+ * nothing: pa_fp8_decode_partitions followed by pa_fp8_lse_reduce into `output`
+ * (out_dtype, stride_o_*), with the partials (exp_sums, max_logits, tmp_out) in a
+ * static device array of PA_FP8_NOALLOC_SCRATCH_BYTES instead of caller buffers;
+ * args->exp_sums / max_logits / tmp_out and their strides are ignored.  With
+ * max_context_partition_num == 1 it is the direct-output decode (no scratch).
+ * The partials need B * Hkv * P * ql*g * (8 + 2 * head_dim) bytes (each piece
+ * rounded up to 256); more returns PA_FP8_ERR_SCRATCH.  Outputs are bit-identical
+ * to the two-call path.  The scratch is looked up (hipGetSymbolAddress) on the
+ * first call on each device and never allocated or freed.  Every call on a GPU
+ * shares that GPU's one scratch: calls that overlap on one GPU (several streams,
+ * or host threads, at once) race; calls ordered on one stream do not.
+ *
+ * No counterpart in the reference.  It is for callers that cannot allocate:
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.
+ */
+int pa_fp8_decode_partitions_noalloc(const pa_fp8_decode_args *args, void *hip_stream);
 
 /*
  * Log-sum-exp reduce of the partials into the final output

@@ -37,7 +37,7 @@ def declared_functions():
 
 def test_header_declares_the_expected_api():
     assert declared_functions() == sorted(
-        ["pa_fp8_decode_partitions", "pa_fp8_lse_reduce", "pa_fp8_decode_worklist", "pa_fp8_reduce_v1",
+        ["pa_fp8_decode_partitions", "pa_fp8_decode_partitions_noalloc", "pa_fp8_lse_reduce", "pa_fp8_decode_worklist", "pa_fp8_reduce_v1",
          "pa_fp8_metadata_v1", "pa_fp8_metadata_multi", "pa_fp8_rope_cache", "pa_fp8_status_string",
          "pa_fp8_abi_version"]
     )
@@ -135,10 +135,24 @@ def test_null_args_and_status_strings(lib):
     assert lib.LIB.pa_fp8_decode_worklist(None, None) == 1
     assert lib.LIB.pa_fp8_reduce_v1(None, None) == 1
     assert lib.LIB.pa_fp8_rope_cache(None, None) == 1
-    for code in range(0, 10):
+    for code in range(0, 11):
         assert lib.LIB.pa_fp8_status_string(code)
+    assert b"scratch" in lib.LIB.pa_fp8_status_string(lib.PA_FP8_ERR_SCRATCH)
     with pytest.raises(lib.PaFp8Error, match="status 2"):
         lib.check("pa_fp8_decode_partitions", 2)
+
+
+def test_noalloc_validation_codes(lib):
+    """The allocation-free decode returns before any device work on these."""
+    assert lib.LIB.pa_fp8_decode_partitions_noalloc(None, None) == 1
+    a = _decode_args(lib)  # empty batch
+    assert lib.LIB.pa_fp8_decode_partitions_noalloc(ctypes.byref(a), None) == 0
+    a.out_dtype = 3
+    assert lib.LIB.pa_fp8_decode_partitions_noalloc(ctypes.byref(a), None) == 6
+    # 4096 x 8 heads x 8 slots x 4 rows of partials need 69 MB: more than the scratch
+    big = _decode_args(lib, batch_size=4096)
+    assert lib.LIB.pa_fp8_decode_partitions_noalloc(ctypes.byref(big), None) == lib.PA_FP8_ERR_SCRATCH
+    assert lib.LIB.pa_fp8_decode_partitions_noalloc(ctypes.byref(_decode_args(lib, head_dim=96)), None) == 2
 
 
 def test_reduce_and_metadata_validation(lib):

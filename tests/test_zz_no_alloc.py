@@ -1,0 +1,77 @@
+"""pa_fp8_decode_partitions_noalloc (the allocation-free decode, partials in the
+library's static device scratch) against the existing entry points with
+caller-allocated partials (pa_fp8_decode_partitions + pa_fp8_lse_reduce, as
+pa_decode_ps_launch calls them): bit-identical outputs, on two calls in a row
+(the second smaller, so stale scratch contents from the first would show), and
+the direct one-slot case; an oversized request is refused."""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import pytest
+import torch
+
+from flydsl_amd.workloads import CONFIGS, build_workload, scaled
+from tests.pa_testlib import compare_outputs, launch
+
+pytestmark = pytest.mark.gpu
+
+
+def _noalloc(w, parts, out_dtype=torch.bfloat16):
+    """One call of the allocation-free entry through the C ABI."""
+    from flydsl_amd import _lib
+    from flydsl_amd import pa_decode_fp8 as pdf
+
+    cfg = w["config"]
+    q = w["query"]
+    out = torch.full(q.shape, float("nan"), dtype=out_dtype, device=q.device)
+    a = pdf._decode_args(
+        query=q, key_cache=w["key_cache"], value_cache=w["value_cache"], block_tables=w["block_tables"],
+        context_lengths=w["context_lengths"], key_scale=w["key_scale"], value_scale=w["value_scale"],
+        per_token_kv=cfg.per_token, exp_sums=None, max_logits=None, temporary_output=None,
+        query_length=cfg.query_length, query_group_size=cfg.group_size, max_parts=parts,
+        sliding_window=cfg.sliding_window, softmax_scale=1.0 / math.sqrt(q.shape[-1]),
+    )
+    o5 = out.view(cfg.batch, cfg.query_length, cfg.num_kv_heads, cfg.group_size, q.shape[-1])
+    a.output = o5.data_ptr()
+    a.stride_o_seq, a.stride_o_len, a.stride_o_head, a.stride_o_group = (o5.stride(i) for i in range(4))
+    a.out_dtype = {torch.bfloat16: _lib.PA_FP8_BF16, torch.float16: _lib.PA_FP8_F16,
+                   torch.float32: _lib.PA_FP8_F32}[out_dtype]
+    # the launcher's wave count, so both paths accumulate in the same order
+    a.waves_per_slot = pdf._waves_per_slot(q.device, cfg.batch, cfg.num_kv_heads, parts, q.shape[-1])
+    stream = torch.cuda.current_stream().cuda_stream
+    status = _lib.LIB.pa_fp8_decode_partitions_noalloc(ctypes.byref(a), ctypes.c_void_p(stream))
+    torch.cuda.synchronize()
+    return status, out
+
+
+def test_noalloc_matches_the_two_call_path():
+    big = scaled(CONFIGS["c2"], name="noalloc_big", batch=64, ctx_kind="uniform", ctx_a=1, ctx_b=4096)
+    small = scaled(CONFIGS["c3"], name="noalloc_small", batch=5, num_q_heads=16, num_kv_heads=2, query_length=2,
+                   ctx_kind="uniform", ctx_a=2, ctx_b=3000)
+    for cfg, parts, seed in ((big, 8, 61), (small, 3, 62)):
+        print(f"[noalloc] {cfg.name} P {parts}", flush=True)
+        w = build_workload(cfg, "cuda", seed=seed)
+        ref, tag, _ = launch(w, max_parts=parts, with_partials=True)  # caller-allocated partials
+        assert tag == "ps_small_block"
+        status, got = _noalloc(w, parts)
+        assert status == 0
+        assert torch.equal(got, ref), f"{cfg.name}: differs from the two-call path"
+        compare_outputs(w, got, range(0, cfg.batch, max(1, cfg.batch // 6)))
+    # one slot: the direct-output decode, no scratch
+    w = build_workload(small, "cuda", seed=63)
+    ref, _, _ = launch(w, max_parts=1)
+    status, got = _noalloc(w, 1)
+    assert status == 0 and torch.equal(got, ref)
+
+
+def test_noalloc_refuses_more_partials_than_the_scratch():
+    from flydsl_amd import _lib
+
+    cfg = scaled(CONFIGS["c2"], name="noalloc_over", batch=64, ctx_kind="fixed", ctx_a=512, ctx_b=512)
+    w = build_workload(cfg, "cuda", seed=64)
+    # 64 x 8 x 128 slots x 4 rows x (8 + 256) bytes = 69 MB > 32 MiB
+    status, _ = _noalloc(w, 128)
+    assert status == _lib.PA_FP8_ERR_SCRATCH
