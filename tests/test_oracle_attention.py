@@ -167,3 +167,39 @@ def test_torch_mha_extend_matches_direct_attention():
         vv = np.stack([vd[p, :, s] for p, s in toks])
         exp = oatt.reference_masked_attention(q[b * ql : (b + 1) * ql], kk, vv, 1 / math.sqrt(d), True, 0)
         np.testing.assert_array_equal(out[b * ql : (b + 1) * ql], ofp8.bf16_round(exp))
+
+
+def test_torch_restatement_matches_numpy_oracle():
+    """oracle/attention_torch.py (the baseline's torch CPU path) computes what the
+    numpy oracle computes, on the golden fixtures (per-tensor c1; per-token, ql 3,
+    window 100, bs 32) with the trans_v and the 4-D value layouts: to float32
+    rounding before the bf16 cast, and the same bf16 values after it except at
+    rare ties on a bf16 boundary."""
+    import json
+    from pathlib import Path
+
+    import torch
+
+    from oracle import attention_torch as oat
+
+    golden = Path(__file__).resolve().parent / "golden"
+    for name in ("c1", "mtp_tok_sw"):
+        z = np.load(golden / f"{name}.npz", allow_pickle=False)
+        meta = json.loads(str(z["meta"]))
+        q = ofp8.bf16_bits_to_f32(z["query_bf16"])
+        ql, sw = int(meta.get("query_length", 1)), int(meta.get("sliding_window", 0))
+        ctx = [int(c) for c in z["context_lengths"]]
+        for v in (z["value_cache"], oq.v_trans_to_4d(z["value_cache"])):
+            ref = np.concatenate([
+                oatt.reference_masked_attention(
+                    q[b * ql:(b + 1) * ql],
+                    *oatt.gather_sequence(z["key_cache"], v, z["block_tables"][b], ctx[b], z["key_scale"],
+                                          z["value_scale"]),
+                    1 / math.sqrt(q.shape[-1]), True, sw)
+                for b in range(len(ctx))])
+            got = oat.torch_mha_extend(torch.from_numpy(q), torch.from_numpy(z["key_cache"]), torch.from_numpy(v),
+                                       torch.from_numpy(z["block_tables"]), ctx, ql,
+                                       torch.from_numpy(z["key_scale"]), torch.from_numpy(z["value_scale"]), sw,
+                                       round_bf16=False).numpy()
+            np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6, err_msg=name)
+            assert np.mean(ofp8.bf16_round(got) == ofp8.bf16_round(ref)) > 0.999, name
