@@ -722,9 +722,14 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const lds_void_t *)p;
 }
 
-// 16 bytes from gptr to LDS byte address lds_base + 16 * lane.
+// 16 bytes from gptr to LDS byte address lds_base + 16 * lane (with the
+// non-temporal hint by default: each K / V byte is read once).
 __device__ __forceinline__ void dma16(const void *gptr, uint32_t lds_base) {
+#if PA_FP8_NT_KV
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(gptr), "s"(lds_base) : "memory", "m0");
+#else
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory", "m0");
+#endif
 }
 
 // Wait until at most N of this wave's vector memory loads are outstanding and

@@ -7,6 +7,8 @@ exact (see pa_testlib.check_partials).
 
 from __future__ import annotations
 
+import math
+
 import pytest
 import torch
 
@@ -103,3 +105,40 @@ def test_f16_query():
     w = build_workload(cfg, "cuda", seed=5)
     out, _, _ = launch(w, query=w["query"].to(torch.float16))
     compare_outputs(w, out, range(cfg.batch))
+
+
+@pytest.mark.parametrize("name", ["c3", "c4"])
+def test_reference_call_pattern_with_recommended_partials(name):
+    """The reference harness's call: max_context_partition_num=0 with exp_sums /
+    max_logits / temporary_output preallocated for get_recommended_splits' count
+    (kernels/pa_decode_fp8.py:3024-3049; 8 for c3, 17 for the c4 window).  The
+    launcher takes the count from the buffers and fills every slot; each slot's
+    partial is checked against the oracle's token range."""
+    import torch
+
+    from flydsl_amd import get_recommended_splits, pa_decode_ps_launch
+
+    cfg = CONFIGS[name]
+    print(f"[parity] {name}: reference call pattern", flush=True)
+    w = build_workload(cfg, "cuda")
+    if cfg.sliding_window:
+        parts = get_recommended_splits(cfg.batch, cfg.num_kv_heads, sliding_window=cfg.sliding_window,
+                                       query_length=cfg.query_length)
+    else:
+        parts = get_recommended_splits(cfg.batch, cfg.num_kv_heads, split_kv_blocks=256 // cfg.block_size)
+    assert parts == (17 if cfg.sliding_window else 8)
+    eqgs = cfg.query_length * cfg.group_size
+    shape = (cfg.batch, cfg.num_kv_heads, parts, eqgs)
+    partials = {"exp_sums": torch.full(shape, float("nan"), device="cuda"),
+                "max_logits": torch.full(shape, float("nan"), device="cuda"),
+                "temporary_output": torch.full(shape + (128,), float("nan"), dtype=torch.bfloat16, device="cuda")}
+    out = torch.empty_like(w["query"])
+    tag = pa_decode_ps_launch(out, w["query"], w["key_cache"], w["value_cache"], w["context_lengths"],
+                              w["kv_page_indices"], w["kv_indptr"], 1.0 / math.sqrt(128), w["key_scale"],
+                              w["value_scale"], sliding_window=cfg.sliding_window, block_tables=w["block_tables"],
+                              max_context_partition_num=0, **partials)
+    torch.cuda.synchronize()
+    assert tag == ("ps_sw_partitioned" if cfg.sliding_window else "ps_small_block")
+    batches = _spread(cfg.batch, 5)
+    compare_outputs(w, out, batches)
+    check_partials(w, partials, parts, batches)
