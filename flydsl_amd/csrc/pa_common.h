@@ -43,12 +43,18 @@ __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
-// C[16x16] += A[16x128] B[128x16], fp8 e4m3fn operands, f32 accumulation
-// (v_mfma_scale_f32_16x16x128_f8f6f4 with both block scales 2^0).  Lane l holds
-// row / column l % 16 and k = 32 * (l / 16) + byte j of its 32 bytes (checked on
-// the GPU against a host product).
-__device__ __forceinline__ f32x4 mfma_fp8_k128(i32x8 a, i32x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+// C[16x16] += A[16x128] B[128x16] 2^(sb - 127): fp8 e4m3fn operands, f32
+// accumulation, B's E8M0 block scale from byte 0 of sb, A's 2^0
+// (v_mfma_scale_f32_16x16x128_f8f6f4).  Lane l holds row / column l % 16; its
+// bytes j < 16 are k = 16 (l / 16) + j and its bytes j >= 16 are
+// k = 64 + 16 (l / 16) + j - 16.  The scale of column c, k block q
+// (k in [32 q, 32 q + 32)) comes from lane c + 16 q, so it covers bytes of two
+// lanes, and only a scale that varies with the column alone (the same in lanes
+// c, c + 16, c + 32, c + 48) is exact.  Any placement of k that A and B share
+// gives the same product, so the operands only keep A and B alike.  (Layout and
+// scale lanes measured on the GPU against host products.)
+__device__ __forceinline__ f32x4 mfma_fp8_k128(i32x8 a, i32x8 b, f32x4 c, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, sb);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -141,18 +141,20 @@ struct RowSet {
     int lo_max, hi_min;
 };
 
-// Query rows as a two-term fp8 split for the fp8 QK products: x = q * inv (inv =
-// 448 / amax of the row), hi = e4m3(x), lo = e4m3(x - hi), so q ~ (hi + lo) / inv
-// to about 8 significant bits (bf16's precision); dq = 1 / inv restores the logit.
-// A lane's D/4 values fill NF 32-byte operands (the last one zero-padded when
-// D/4 is not a multiple of 32).
+// Query rows as a two-term fp8 split for the fp8 QK products: x = q * k_fac * 2^k
+// (k_fac the logit scale, 2^k the largest power of two with amax(x) <= 448),
+// hi = e4m3(x), lo = e4m3(x - hi), so q k_fac ~ (hi + lo) 2^-k to about 8
+// significant bits (bf16's precision).  2^-k is the E8M0 block scale qsb = 127 - k
+// of the row's B operand, so the products come out as finished logits.  A lane's
+// D/4 values fill NF 32-byte operands (the last one zero-padded when D/4 is not a
+// multiple of 32).
 template <int MTPW, int D>
 struct RowSetF8 {
     static constexpr bool kFp8 = true;
     static constexpr int kMtpw = MTPW, kD = D;
     static constexpr int NF = (D / 4 + 31) / 32;
     i32x8 qh[MTPW][NF], ql[MTPW][NF];
-    float dq[MTPW];
+    int qsb[MTPW];
     int lo_n[MTPW], hi_n[MTPW];
     int lo_max, hi_min;
 };
@@ -160,7 +162,8 @@ struct RowSetF8 {
 // fp8 two-term split of one lane's D/4 query values (dims D/4 kg .. D/4 kg + D/4 - 1
 // of its row); the row's amax is reduced over its 4 lanes (kg = lane / 16).
 template <int MTPW, int D>
-__device__ __forceinline__ void split_q_fp8(RowSetF8<MTPW, D> &rw, int mg, const bf16x8 (&q)[D / 32], bool live) {
+__device__ __forceinline__ void split_q_fp8(RowSetF8<MTPW, D> &rw, int mg, const bf16x8 (&q)[D / 32], bool live,
+                                            float k_fac) {
     constexpr int DL = D / 4;
     constexpr int NF = RowSetF8<MTPW, D>::NF;
     float x[DL];
@@ -174,8 +177,12 @@ __device__ __forceinline__ void split_q_fp8(RowSetF8<MTPW, D> &rw, int mg, const
         }
     amax = fmaxf(amax, shfl_xor_f(amax, 16));
     amax = fmaxf(amax, shfl_xor_f(amax, 32));
-    const float inv = (live && amax > 0.0f) ? 448.0f / amax : 1.0f;
-    rw.dq[mg] = 1.0f / inv;
+    amax *= k_fac;
+    // 448 / amax in [2^(e-1), 2^e): k = e - 1, clamped to the E8M0 range
+    int k = 0;
+    if (live && amax > 0.0f) k = min(max(__builtin_amdgcn_frexp_expf(448.0f / amax) - 1, -126), 126);
+    rw.qsb[mg] = 127 - k;
+    const float inv = __builtin_amdgcn_ldexpf(k_fac, k);
 #pragma unroll
     for (int u = 0; u < NF; ++u)
 #pragma unroll
@@ -204,7 +211,7 @@ __device__ __forceinline__ void split_q_fp8(RowSetF8<MTPW, D> &rw, int mg, const
 // Query rows (row_group0 + mg) * 16 + l16 of (sequence b, kv head h).
 template <class RW>
 __device__ __forceinline__ void setup_rows(RW &rw, const DecodeParams &p, int b, int h, int ctx, int tok_lo,
-                                           int tok_hi, int row_group0, int l16, int kg) {
+                                           int tok_hi, int row_group0, int l16, int kg, float k_fac) {
     constexpr int MTPW = RW::kMtpw;
     constexpr int D = RW::kD;
     rw.lo_max = tok_lo;
@@ -221,7 +228,7 @@ __device__ __forceinline__ void setup_rows(RW &rw, const DecodeParams &p, int b,
 #pragma unroll
             for (int s = 0; s < D / 32; ++s) q[s] = load_q8(qrow + 8 * s, p.q_f16 != 0);
             if constexpr (RW::kFp8) {
-                split_q_fp8<MTPW, D>(rw, mg, q, true);
+                split_q_fp8<MTPW, D>(rw, mg, q, true, k_fac);
             } else {
 #pragma unroll
                 for (int s = 0; s < D / 32; ++s) rw.qop[mg][s] = q[s];
@@ -233,7 +240,7 @@ __device__ __forceinline__ void setup_rows(RW &rw, const DecodeParams &p, int b,
 #pragma unroll
             for (int s = 0; s < D / 32; ++s) q[s] = bf16x8{};
             if constexpr (RW::kFp8) {
-                split_q_fp8<MTPW, D>(rw, mg, q, false);
+                split_q_fp8<MTPW, D>(rw, mg, q, false, k_fac);
             } else {
 #pragma unroll
                 for (int s = 0; s < D / 32; ++s) rw.qop[mg][s] = q[s];
@@ -285,7 +292,8 @@ struct SmState {
 // With the fp8 row set (RW::kFp8), QK runs on fp8 MFMAs straight from the K bytes
 // (two consecutive 16-byte chunks of tile jt are one 32-byte A operand, matching
 // the query's operand u), two products per operand (hi and lo terms of the query),
-// and the row's dequant factor joins the logit scale; no K conversion.
+// and the row's block scale makes them finished logits (per-tensor) or logits
+// before the token's K scale (per-token); no K conversion.
 // 16-byte K chunks a lane holds per tile: D/64, rounded up to even (the padding
 // chunk, zero, completes the last 32-byte fp8 operand when D/64 is odd).
 template <int D>
@@ -323,8 +331,8 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW, D> &st, const RW &
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int u = 0; u < NF; ++u) {
-                    acc = mfma_fp8_k128(a[u], rw.qh[mg][u], acc);
-                    acc = mfma_fp8_k128(a[u], rw.ql[mg][u], acc);
+                    acc = mfma_fp8_k128(a[u], rw.qh[mg][u], acc, rw.qsb[mg]);
+                    acc = mfma_fp8_k128(a[u], rw.ql[mg][u], acc, rw.qsb[mg]);
                 }
                 sc[mg][jt] = acc;
             }
@@ -346,23 +354,23 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW, D> &st, const RW &
     }
     after_qk();
 
+    // logit factors of the 16 tokens: none where the products already hold them
+    constexpr bool kScaleLogits = !RW::kFp8 || PER_TOKEN;
     f32x4 kf[4];
-    if constexpr (!RW::kFp8) {
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr(jt) * k_fac : f32x4{k_fac, k_fac, k_fac, k_fac};
+    for (int jt = 0; jt < 4; ++jt) {
+        if constexpr (!RW::kFp8)
+            kf[jt] = PER_TOKEN ? ksr(jt) * k_fac : f32x4{k_fac, k_fac, k_fac, k_fac};
+        else if constexpr (PER_TOKEN)
+            kf[jt] = ksr(jt);
     }
 
 #pragma unroll
     for (int mg = 0; mg < MTPW; ++mg) {
-        if constexpr (RW::kFp8) {
-            const float kq = k_fac * rw.dq[mg];
-#pragma unroll
-            for (int jt = 0; jt < 4; ++jt) kf[jt] = PER_TOKEN ? ksr(jt) * kq : f32x4{kq, kq, kq, kq};
-        }
         float mx = -INFINITY;
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
-            sc[mg][jt] *= kf[jt];
+            if constexpr (kScaleLogits) sc[mg][jt] *= kf[jt];
             if (!interior) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -489,9 +497,9 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
         emit_empty<D>(NW * 64, row0, min(p.eqgs, row0 + kRowChunk), sink);
         return;
     }
-    RowSet<MTPW, D> rw;
-    setup_rows(rw, p, b, h, ctx, tok_lo, tok_hi, row_group0, l16, kg);
     const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
+    RowSet<MTPW, D> rw;
+    setup_rows(rw, p, b, h, ctx, tok_lo, tok_hi, row_group0, l16, kg, k_fac);
     const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
     SmState<MTPW, D> st;
     st.init();
@@ -887,9 +895,9 @@ __device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const
         emit_empty<D>(NW * 64, row0, min(p.eqgs, row0 + kRowChunk), sink);
         return;
     }
-    RowSetF8<MTPW, D> rw;
-    setup_rows(rw, p, b, h, ctx, tok_lo, tok_hi, row_group0, l16, kg);
     const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
+    RowSetF8<MTPW, D> rw;
+    setup_rows(rw, p, b, h, ctx, tok_lo, tok_hi, row_group0, l16, kg, k_fac);
     const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
     SmState<MTPW, D> st;
     st.init();
