@@ -61,6 +61,24 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// Lane J of each quad of lanes (4q .. 4q+3) to the whole quad: a DPP quad_perm
+// broadcast (a VALU move, no LDS).
+template <int J>
+__device__ __forceinline__ float quad_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), J * 0x55, 0xf, 0xf, true));
+}
+
+// out[j] = piece of quad lane j, for j = 0..3.
+__device__ __forceinline__ void quad_gather(const f32x4 &piece, f32x4 (&out)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        out[0][i] = quad_bcast<0>(piece[i]);
+        out[1][i] = quad_bcast<1>(piece[i]);
+        out[2][i] = quad_bcast<2>(piece[i]);
+        out[3][i] = quad_bcast<3>(piece[i]);
+    }
+}
+
 // 16 bytes with the non-temporal hint (data read once).
 __device__ __forceinline__ u32x4 ld16_nt(const void *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
