@@ -1047,29 +1047,50 @@ __global__ __launch_bounds__((kThreads<RS, NS>), (kWavesFor<MTPW, NS, D>)) void 
     }
     const int wbeg = max(__builtin_amdgcn_readfirstlane(w.work_indptr[c]), 0);
     const int wend = min(__builtin_amdgcn_readfirstlane(w.work_indptr[c + 1]), w.max_work);
+    // A work's fields, and its sequence's page range, context length and partition
+    // base, are read with scalar loads (the constant address space: the worklist is
+    // read-only here) one work ahead, so the next work's set-up does not start with
+    // two dependent memory round trips, and no vector memory wait covers them:
+    // c3 kernel 156.3 -> 152.2 us.
+    typedef __attribute__((address_space(4))) const int32_t cint;
+    struct Fields {
+        int b, pidx, qo_start, kv_start, kv_end, qh_start, page0, page1, ctx, pbase;
+    };
+    auto fields = [&](int wi) {
+        Fields r;
+        const cint *info = (const cint *)(w.work_info + (int64_t)wi * 8);
+        r.b = info[0];
+        r.pidx = info[1];
+        r.qo_start = info[2];
+        r.kv_start = info[4];
+        r.kv_end = info[5];
+        r.qh_start = info[7] & 0xffff;
+        const int bb = min(max(r.b, 0), w.batch - 1);  // batch >= 1 here; out-of-range works are skipped below
+        r.page0 = ((const cint *)w.kv_indptr)[bb];
+        r.page1 = ((const cint *)w.kv_indptr)[bb + 1];
+        r.ctx = ((const cint *)p.ctx)[bb];
+        r.pbase = ((const cint *)w.partition_indptr)[bb];
+        return r;
+    };
+    Fields nxt{};
+    if (wbeg < wend) nxt = fields(wbeg);
     for (int wi = wbeg; wi < wend; ++wi) {
-        const int32_t *info = w.work_info + (int64_t)wi * 8;
-        const int b = __builtin_amdgcn_readfirstlane(info[0]);
-        const int pidx = __builtin_amdgcn_readfirstlane(info[1]);
-        const int qo_start = __builtin_amdgcn_readfirstlane(info[2]);
-        const int kv_start = __builtin_amdgcn_readfirstlane(info[4]);
-        const int kv_end = __builtin_amdgcn_readfirstlane(info[5]);
-        const int qh_start = __builtin_amdgcn_readfirstlane(info[7]) & 0xffff;
-        const int h = qh_start / p.g;
+        const Fields f = nxt;
+        if (wi + 1 < wend) nxt = fields(wi + 1);
+        const int b = f.b, pidx = f.pidx, qo_start = f.qo_start;
+        const int h = f.qh_start / p.g;
         if (b < 0 || b >= w.batch || h >= w.num_kv_heads) continue;
         if (pidx < 0 ? (qo_start < 0 || qo_start > w.output_rows - p.ql)
                      : (pidx > w.partial_rows - 2 * p.ql))
             continue;
-        const int page0 = __builtin_amdgcn_readfirstlane(w.kv_indptr[b]);
-        const int page1 = __builtin_amdgcn_readfirstlane(w.kv_indptr[b + 1]);
+        const int page0 = f.page0, page1 = f.page1;
         if (page0 < 0 || page1 < page0 || page1 > w.num_pages) continue;
-        int64_t ctx64 = p.ctx[b];
+        int64_t ctx64 = f.ctx;
         const int64_t cap = (int64_t)(page1 - page0) << p.bs_log2;
         ctx64 = ctx64 < 0 ? 0 : (ctx64 > cap ? cap : ctx64);
         const int ctx = (int)ctx64;
-        const int pbase = __builtin_amdgcn_readfirstlane(w.partition_indptr[b]);
-        const int64_t lp0 = max((int64_t)kv_start - pbase, (int64_t)0);
-        const int64_t lp1 = (int64_t)kv_end - pbase;
+        const int64_t lp0 = max((int64_t)f.kv_start - f.pbase, (int64_t)0);
+        const int64_t lp1 = (int64_t)f.kv_end - f.pbase;
         const int tok_lo = (int)min(lp0 * kPartition, (int64_t)ctx);
         const int tok_hi = (int)max(min(lp1 * kPartition, (int64_t)ctx), (int64_t)tok_lo);
         const WorkSink sink{w, h, qo_start, pidx};
