@@ -141,13 +141,14 @@ struct RowSet {
     int lo_max, hi_min;
 };
 
-// Query rows as a two-term fp8 split for the fp8 QK products: x = q * k_fac * 2^k
-// (k_fac the logit scale, 2^k the largest power of two with amax(x) <= 448),
-// hi = e4m3(x), lo = e4m3(x - hi), so q k_fac ~ (hi + lo) 2^-k to about 8
-// significant bits (bf16's precision).  2^-k is the E8M0 block scale qsb = 127 - k
-// of the row's B operand, so the products come out as finished logits.  A lane's
-// D/4 values fill NF 32-byte operands (the last one zero-padded when D/4 is not a
-// multiple of 32).
+// Query rows as a two-term fp8 split for the fp8 QK products: x = q * 2^k (2^k the
+// largest power of two with amax(x) <= 448), hi = e4m3(x), lo = e4m3(x - hi).  A
+// bf16 value has 8 significant bits and hi keeps the top 4 (rounded), so the
+// residual is a multiple of the bf16 ulp below 2^-4 |x| and lo holds it exactly
+// (while it stays above e4m3's subnormal step 2^-9): hi + lo = x.  2^-k is the E8M0
+// block scale qsb = 127 - k of the row's B operand, so the products are q . k exactly
+// (f32 accumulation), as on the bf16 path.  A lane's D/4 values fill NF 32-byte
+// operands (the last one zero-padded when D/4 is not a multiple of 32).
 template <int MTPW, int D>
 struct RowSetF8 {
     static constexpr bool kFp8 = true;
@@ -162,8 +163,7 @@ struct RowSetF8 {
 // fp8 two-term split of one lane's D/4 query values (dims D/4 kg .. D/4 kg + D/4 - 1
 // of its row); the row's amax is reduced over its 4 lanes (kg = lane / 16).
 template <int MTPW, int D>
-__device__ __forceinline__ void split_q_fp8(RowSetF8<MTPW, D> &rw, int mg, const bf16x8 (&q)[D / 32], bool live,
-                                            float k_fac) {
+__device__ __forceinline__ void split_q_fp8(RowSetF8<MTPW, D> &rw, int mg, const bf16x8 (&q)[D / 32], bool live) {
     constexpr int DL = D / 4;
     constexpr int NF = RowSetF8<MTPW, D>::NF;
     float x[DL];
@@ -177,12 +177,11 @@ __device__ __forceinline__ void split_q_fp8(RowSetF8<MTPW, D> &rw, int mg, const
         }
     amax = fmaxf(amax, shfl_xor_f(amax, 16));
     amax = fmaxf(amax, shfl_xor_f(amax, 32));
-    amax *= k_fac;
     // 448 / amax in [2^(e-1), 2^e): k = e - 1, clamped to the E8M0 range
     int k = 0;
     if (live && amax > 0.0f) k = min(max(__builtin_amdgcn_frexp_expf(448.0f / amax) - 1, -126), 126);
     rw.qsb[mg] = 127 - k;
-    const float inv = __builtin_amdgcn_ldexpf(k_fac, k);
+    const float inv = __builtin_amdgcn_ldexpf(1.0f, k);
 #pragma unroll
     for (int u = 0; u < NF; ++u)
 #pragma unroll
@@ -208,10 +207,22 @@ __device__ __forceinline__ void split_q_fp8(RowSetF8<MTPW, D> &rw, int mg, const
         }
 }
 
-// Query rows (row_group0 + mg) * 16 + l16 of (sequence b, kv head h).
+// bf16 negation (sign bits) of eight values.
+__device__ __forceinline__ bf16x8 neg_bf16x8(bf16x8 v) {
+    u32x4 u = __builtin_bit_cast(u32x4, v);
+    u ^= u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+    return __builtin_bit_cast(bf16x8, u);
+}
+
+// |k_fac| kept positive (a zero scale, as from an all-zero K, becomes the smallest
+// normal float: every visible logit then scales to about 0, masked ones stay -inf).
+__device__ __forceinline__ float logit_scale(float k_fac) { return fmaxf(fabsf(k_fac), 1.17549435e-38f); }
+
+// Query rows (row_group0 + mg) * 16 + l16 of (sequence b, kv head h), negated when
+// the logit scale is negative (the softmax then takes |scale|).
 template <class RW>
 __device__ __forceinline__ void setup_rows(RW &rw, const DecodeParams &p, int b, int h, int ctx, int tok_lo,
-                                           int tok_hi, int row_group0, int l16, int kg, float k_fac) {
+                                           int tok_hi, int row_group0, int l16, int kg, bool negate) {
     constexpr int MTPW = RW::kMtpw;
     constexpr int D = RW::kD;
     rw.lo_max = tok_lo;
@@ -227,8 +238,12 @@ __device__ __forceinline__ void setup_rows(RW &rw, const DecodeParams &p, int b,
             bf16x8 q[D / 32];
 #pragma unroll
             for (int s = 0; s < D / 32; ++s) q[s] = load_q8(qrow + 8 * s, p.q_f16 != 0);
+            if (negate) {
+#pragma unroll
+                for (int s = 0; s < D / 32; ++s) q[s] = neg_bf16x8(q[s]);
+            }
             if constexpr (RW::kFp8) {
-                split_q_fp8<MTPW, D>(rw, mg, q, true, k_fac);
+                split_q_fp8<MTPW, D>(rw, mg, q, true);
             } else {
 #pragma unroll
                 for (int s = 0; s < D / 32; ++s) rw.qop[mg][s] = q[s];
@@ -240,7 +255,7 @@ __device__ __forceinline__ void setup_rows(RW &rw, const DecodeParams &p, int b,
 #pragma unroll
             for (int s = 0; s < D / 32; ++s) q[s] = bf16x8{};
             if constexpr (RW::kFp8) {
-                split_q_fp8<MTPW, D>(rw, mg, q, false, k_fac);
+                split_q_fp8<MTPW, D>(rw, mg, q, false);
             } else {
 #pragma unroll
                 for (int s = 0; s < D / 32; ++s) rw.qop[mg][s] = q[s];
@@ -292,8 +307,12 @@ struct SmState {
 // With the fp8 row set (RW::kFp8), QK runs on fp8 MFMAs straight from the K bytes
 // (two consecutive 16-byte chunks of tile jt are one 32-byte A operand, matching
 // the query's operand u), two products per operand (hi and lo terms of the query),
-// and the row's block scale makes them finished logits (per-tensor) or logits
-// before the token's K scale (per-token); no K conversion.
+// and the row's block scale makes them the exact q . k; no K conversion.
+//
+// Either way the products are q . k before any scale.  The per-token K scale
+// multiplies them; the logit scale k_eff (> 0: softmax scale x log2 e x per-tensor K
+// scale, its sign moved into the query) joins the max once per row and each
+// exponent through an FMA, exp2(s k_eff - m).
 // 16-byte K chunks a lane holds per tile: D/64, rounded up to even (the padding
 // chunk, zero, completes the last 32-byte fp8 operand when D/64 is odd).
 template <int D>
@@ -301,7 +320,7 @@ constexpr int kKChunks = (D / 64 + 1) / 2 * 2;
 
 template <int MTPW, int D, bool PER_TOKEN, class RW, class KScale, class VScale, class AfterQk>
 __device__ __forceinline__ void step_qk_softmax(SmState<MTPW, D> &st, const RW &rw, const uint4 (&kr)[4][kKChunks<D>],
-                                                const KScale &ksr, const VScale &vsr, float k_fac, int t0,
+                                                const KScale &ksr, const VScale &vsr, float k_eff, int t0,
                                                 int kg, bf16x8 (&pop)[MTPW][2], AfterQk &&after_qk) {
     constexpr int CPL = D / 64;  // 16-byte K chunks per lane that hold keys
     const int trow = t0 + 16 * kg;  // token of (tile jt, i) = trow + 4jt + i
@@ -354,15 +373,10 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW, D> &st, const RW &
     }
     after_qk();
 
-    // logit factors of the 16 tokens: none where the products already hold them
-    constexpr bool kScaleLogits = !RW::kFp8 || PER_TOKEN;
-    f32x4 kf[4];
+    f32x4 kf[4];  // per-token K scales of the 16 tokens
+    if constexpr (PER_TOKEN) {
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-        if constexpr (!RW::kFp8)
-            kf[jt] = PER_TOKEN ? ksr(jt) * k_fac : f32x4{k_fac, k_fac, k_fac, k_fac};
-        else if constexpr (PER_TOKEN)
-            kf[jt] = ksr(jt);
+        for (int jt = 0; jt < 4; ++jt) kf[jt] = ksr(jt);
     }
 
 #pragma unroll
@@ -370,7 +384,7 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW, D> &st, const RW &
         float mx = -INFINITY;
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
-            if constexpr (kScaleLogits) sc[mg][jt] *= kf[jt];
+            if constexpr (PER_TOKEN) sc[mg][jt] *= kf[jt];
             if (!interior) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -383,6 +397,7 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW, D> &st, const RW &
         }
         mx = fmaxf(mx, shfl_xor_f(mx, 16));
         mx = fmaxf(mx, shfl_xor_f(mx, 32));
+        mx *= k_eff;  // k_eff > 0: the max of the scaled logits (-inf stays -inf)
         st.m_top[mg] = fmaxf(st.m_top[mg], mx);
         const bool raise = mx > st.m_run[mg] + kSlack;  // false while the row has seen no key
         if (__any(raise)) {                              // wave-uniform
@@ -398,7 +413,7 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW, D> &st, const RW &
         for (int jt = 0; jt < 4; ++jt) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float pv = fast_exp2(sc[mg][jt][i] - m_use);
+                const float pv = fast_exp2(fmaf(sc[mg][jt][i], k_eff, -m_use));
                 psum += pv;
                 sc[mg][jt][i] = pv;
             }
@@ -498,8 +513,9 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
         return;
     }
     const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
+    const float k_eff = logit_scale(k_fac);
     RowSet<MTPW, D> rw;
-    setup_rows(rw, p, b, h, ctx, tok_lo, tok_hi, row_group0, l16, kg, k_fac);
+    setup_rows(rw, p, b, h, ctx, tok_lo, tok_hi, row_group0, l16, kg, k_fac < 0.0f);
     const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
     SmState<MTPW, D> st;
     st.init();
@@ -598,7 +614,7 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
         }
         bf16x8 pop[MTPW][2];
         step_qk_softmax<MTPW, D, PER_TOKEN>(st, rw, kr, [&](int jt) { return ksc[jt]; },
-                                            [&](int jt) { return vsc[jt]; }, k_fac, tok_lo + step * kStep, kg, pop,
+                                            [&](int jt) { return vsc[jt]; }, k_eff, tok_lo + step * kStep, kg, pop,
                                             [&] {
                                                 if (has_nxt) {
                                                     load_k(nkb);  // K registers are free again
@@ -896,8 +912,9 @@ __device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const
         return;
     }
     const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
+    const float k_eff = logit_scale(k_fac);
     RowSetF8<MTPW, D> rw;
-    setup_rows(rw, p, b, h, ctx, tok_lo, tok_hi, row_group0, l16, kg, k_fac);
+    setup_rows(rw, p, b, h, ctx, tok_lo, tok_hi, row_group0, l16, kg, k_fac < 0.0f);
     const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
     SmState<MTPW, D> st;
     st.init();
@@ -925,7 +942,7 @@ __device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const
         auto ks_at = [&](int jt) { return *reinterpret_cast<const f32x4 *>(ss + 16 * jt); };
         auto vs_at = [&](int jt) { return *reinterpret_cast<const f32x4 *>(ss + 256 + 16 * jt); };
         bf16x8 pop[MTPW][2];
-        step_qk_softmax<MTPW, D, PER_TOKEN>(st, rw, kr, ks_at, vs_at, k_fac, tok_lo + n * kStep, kg, pop, [] {});
+        step_qk_softmax<MTPW, D, PER_TOKEN>(st, rw, kr, ks_at, vs_at, k_eff, tok_lo + n * kStep, kg, pop, [] {});
         uint4 vr[D / 16];
 #pragma unroll
         for (int m = 0; m < D / 16; ++m)

@@ -258,3 +258,35 @@ def test_shared_pages(path, dist):
     else:
         _run_partitions(cfg, 51, 3)
         _run_partitions(cfg, 51, 0)
+
+
+# ----------------------------------------------- query magnitudes, zero K scale
+@pytest.mark.parametrize("exp2", [-125, -60, 6])
+@pytest.mark.parametrize("case", ["g4", "mtp4_g16"])
+@pytest.mark.parametrize("quant", ["per_token", "per_tensor"])
+def test_query_magnitudes(exp2, case, quant):
+    """Queries scaled by 2^exp2, on the register-streaming (g4) and LDS-staged
+    (mtp4_g16) layouts.  At 2^-125 the staged layout's power-of-two query scale
+    saturates the E8M0 range and every row averages its visible values; at 2^6 the
+    logits are 64 times the unit-scale ones, so the softmax is nearly one-hot and a
+    logit error of 2^-8 relative would show: the products must be the exact q . k."""
+    cfg = scaled(CONFIGS["c5"], name=f"qmag{exp2}_{case}_{quant}", batch=3, block_size=16,
+                 per_token=quant == "per_token", ctx_kind="uniform", ctx_a=4, ctx_b=2000, **HEAD_DIM_CASES[case])
+    w = build_workload(cfg, "cuda", seed=61)
+    w["query"] = (w["query"].float() * 2.0**exp2).to(torch.bfloat16)
+    print(f"[shapes] query x 2^{exp2}, {case}, {quant}", flush=True)
+    out, tag, _ = launch(w)
+    compare_outputs(w, out, range(cfg.batch))
+
+
+@pytest.mark.parametrize("case", ["g4", "mtp4_g16"])
+def test_zero_key_scale(case):
+    """A per-tensor K scale of 0 (an all-zero key cache): every logit is 0 and each
+    row averages its visible values."""
+    cfg = scaled(CONFIGS["c2"], name=f"ks0_{case}", batch=3, block_size=16, ctx_kind="uniform", ctx_a=4,
+                 ctx_b=1500, **HEAD_DIM_CASES[case])
+    w = build_workload(cfg, "cuda", seed=63)
+    w["key_scale"].zero_()
+    print(f"[shapes] zero K scale, {case}", flush=True)
+    out, tag, _ = launch(w)
+    compare_outputs(w, out, range(cfg.batch))
