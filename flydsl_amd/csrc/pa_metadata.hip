@@ -518,10 +518,15 @@ int meta_params(const pa_fp8_metadata_args *a, MetaParams &p) {
         return PA_FP8_ERR_SHAPE;
     if (a->num_cu % a->num_heads_k != 0) return PA_FP8_ERR_SHAPE;
     if (a->kv_granularity <= 0 || (a->kv_granularity & (a->kv_granularity - 1)) != 0) return PA_FP8_ERR_SHAPE;
-    if (!a->seqlens_qo_indptr || !a->context_lens || !a->work_indptr || !a->work_info || !a->reduce_indptr ||
-        !a->reduce_final_map || !a->reduce_partial_map)
-        return PA_FP8_ERR_NULL_POINTER;
     if (a->max_work < 0 || a->max_split_tiles < 0) return PA_FP8_ERR_SHAPE;
+    // a buffer of no entries may be NULL (torch gives an empty tensor a NULL data
+    // pointer): one bin per kv head leaves reduce_partial_map empty, and every
+    // write to work_info, reduce_final_map and reduce_partial_map is bounded by
+    // max_work, num_batches and max_split_tiles
+    if (!a->seqlens_qo_indptr || !a->context_lens || !a->work_indptr || !a->reduce_indptr ||
+        (!a->work_info && a->max_work > 0) || (!a->reduce_final_map && a->num_batches > 0) ||
+        (!a->reduce_partial_map && a->max_split_tiles > 0))
+        return PA_FP8_ERR_NULL_POINTER;
     if (a->bin_groups > 1) {
         if (a->bin_groups > 4) return PA_FP8_ERR_SHAPE;
         for (int g = 0; g < a->bin_groups; ++g)

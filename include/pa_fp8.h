@@ -292,7 +292,8 @@ int pa_fp8_reduce_v1(const pa_fp8_reduce_v1_args *args, void *hip_stream);
  * common case and the serial machine the rest).  Writes work_indptr
  * [num_cu+1], work_info [max_work, 8], reduce_indptr [B+1],
  * reduce_final_map [B, 2], reduce_partial_map [max_split_tiles]; only the
- * valid prefixes are defined.  kv_granularity must be a power of two and
+ * valid prefixes are defined, and a buffer of no entries may be NULL (one bin
+ * per kv head gives max_split_tiles 0).  kv_granularity must be a power of two and
  * num_cu a multiple of num_heads_k.  Optional outputs (NULL: not written):
  * partition_indptr [B+1], the exclusive prefix of ceil(context_len /
  * kv_granularity), and uniform_context [1], 1 when every context length is

@@ -173,6 +173,23 @@ def test_reduce_and_metadata_validation(lib):
     assert lib.LIB.pa_fp8_metadata_v1(ctypes.byref(m), None) == 1  # null buffers
 
 
+def test_metadata_accepts_null_for_empty_buffers(lib):
+    """One bin per kv head gives get_pa_metadata_info_v1 a zero-entry
+    reduce_partial_map (min(B + cu - 1, 2 (cu - 1)) = 0), and torch gives an empty
+    tensor a NULL data pointer: the scheduler must take it (every write to it is
+    bounded by max_split_tiles).  Without a GPU the call then fails at the launch,
+    never at the argument check."""
+    m = lib.MetadataArgs()
+    m.num_batches, m.gqa, m.num_heads_k, m.num_cu, m.kv_granularity, m.query_length = 3, 4, 1, 1, 256, 1
+    buf = (ctypes.c_int32 * 64)()
+    for name in ("seqlens_qo_indptr", "context_lens", "work_indptr", "work_info", "reduce_indptr", "reduce_final_map"):
+        setattr(m, name, ctypes.cast(buf, ctypes.c_void_p).value)
+    m.max_work, m.max_split_tiles = 3, 0
+    assert lib.LIB.pa_fp8_metadata_v1(ctypes.byref(m), None) != 1
+    m.max_split_tiles = 2  # a buffer with entries must not be NULL
+    assert lib.LIB.pa_fp8_metadata_v1(ctypes.byref(m), None) == 1
+
+
 def _worklist_args(lib, **over):
     a = lib.WorklistArgs()
     a.batch_size, a.num_kv_heads, a.query_group_size, a.query_length = 0, 1, 8, 1

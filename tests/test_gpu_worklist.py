@@ -146,6 +146,11 @@ WORKLIST_CASES = {
     "bs64_long_mtp4_g16": dict(base="c5", batch=2, ctx_kind="uniform", ctx_a=16500, ctx_b=30000),
     "bs1024_long": dict(base="c2", batch=2, num_q_heads=16, num_kv_heads=2, block_size=1024, ctx_kind="uniform",
                         ctx_a=9000, ctx_b=20000),
+    # one kv head: at one bin per head get_pa_metadata_info_v1 sizes reduce_partial_map to 0 entries
+    "bs64_hkv1_mtp2_g8": dict(base="c5", batch=4, num_q_heads=8, num_kv_heads=1, query_length=2,
+                              ctx_kind="uniform", ctx_a=2, ctx_b=2500),
+    "bs256_hkv1_g1": dict(base="c2", batch=5, num_q_heads=1, num_kv_heads=1, block_size=256, ctx_kind="uniform",
+                          ctx_a=1, ctx_b=3000),
 }
 
 
