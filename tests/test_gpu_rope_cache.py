@@ -454,3 +454,31 @@ def test_divisors_that_are_not_powers_of_two(layout, bs, fmt, kind):
     else:  # consecutive slots from a 16-aligned start: the staged V writes
         slots = _runs("aligned", T, bs, nb, T)
     run_case(T, 96, 12, 3, layout=layout, fmt=fmt, bs=bs, num_blocks=nb, slots=slots)
+
+
+# ---- seeded random cases -------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_writer_case(seed):
+    """Random valid writer launches, bit-exact against the oracle: token counts 1-600,
+    head dims 16-512, GQA 1-8, every cache layout, element dtype and cache format,
+    half / full tables, i32 / i64 indices, page sizes 1-1024, strided Q/K/V views,
+    and unique random slots with some skipped (negative)."""
+    import random
+
+    rnd = random.Random(9000 + seed)
+    layout = rnd.choice(["flash", "x4", "x5"])
+    bs = rnd.choice([16, 32, 64, 256, 1024] if layout == "x5" else [1, 2, 8, 16, 64, 256, 1024])
+    D = rnd.choice([16, 32, 64, 96, 128, 128, 192, 256, 512])
+    KH = rnd.choice([1, 2, 4, 8])
+    QH = KH * rnd.choice([1, 2, 4, 8])
+    T = rnd.choice([1, 3, 16, 64, 200, 600])
+    nb = max(4, (T + bs - 1) // bs + rnd.randint(0, 4))
+    g = torch.Generator().manual_seed(9000 + seed)
+    slots = torch.randperm(nb * bs, generator=g)[:T].to(torch.int32)
+    slots[torch.rand(T, generator=g) < 0.1] = -1
+    run_case(T, D, QH, KH, layout=layout, elem=rnd.choice(["bf16", "f16"]),
+             fmt=rnd.choice(["elem", "fp8_tensor", "fp8_token"]), reuse=rnd.random() < 0.5,
+             pos_dtype=rnd.choice(["i32", "i64"]), bs=bs, num_blocks=nb, slots=slots,
+             fused_qkv=rnd.random() < 0.3, seed=9000 + seed)
