@@ -46,6 +46,8 @@ CASES = {
     "bs1024_tok_ql2": dict(base="c3", batch=5, block_size=1024, query_length=2, num_q_heads=16, num_kv_heads=2,
                            ctx_kind="uniform", ctx_a=2, ctx_b=3000),
     "bs16_pt_g4": dict(base="c2", batch=9, ctx_kind="uniform", ctx_a=1, ctx_b=2600),
+    # 64 query rows per kv head: the LDS-staged worklist kernel under capture
+    "bs64_tok_mtp4_g16": dict(base="c5", batch=4, ctx_kind="uniform", ctx_a=4, ctx_b=3000),
 }
 
 
