@@ -96,6 +96,35 @@ def test_device_scheduler_matches_oracle(seed):
         np.testing.assert_array_equal(op.metadata_valid_prefixes(got)[key], val, err_msg=key)
 
 
+@pytest.mark.parametrize("seed", range(24))
+def test_device_scheduler_random_wide(seed):
+    """Wider random draws: odd kv-head counts, one bin per head up to 256 per head,
+    batches either side of the 4096-batch closed-form limit, and contexts that are
+    all zero, all equal, partly zero or all long."""
+    rng = np.random.default_rng(5000 + seed)
+    nhk = int(rng.choice([1, 2, 3, 4, 8]))
+    num_cu = nhk * int(rng.choice([1, 2, 3, 7, 64, 100, 192, 256]))
+    b = int(rng.choice([1, 2, 7, 64, 300, 4095, 4096, 4097, 5000]))
+    dist = rng.choice(["uniform", "zeros", "mixed", "long", "equal"])
+    hi = int(rng.choice([2, 300, 5000, 33000]))
+    if dist == "zeros":
+        ctx = [0] * b
+    elif dist == "equal":
+        ctx = [hi] * b
+    elif dist == "mixed":
+        ctx = [int(x) if rng.random() > 0.3 else 0 for x in rng.integers(1, hi, size=b)]
+    elif dist == "long":
+        ctx = [int(x) for x in rng.integers(hi // 2, hi + 1, size=b)]
+    else:
+        ctx = [int(x) for x in rng.integers(1, hi, size=b)]
+    ql = int(rng.integers(1, 5))
+    gqa = int(rng.choice([1, 4, 16]))
+    gran = int(rng.choice([16, 64, 256, 1024]))
+    got, ref = run_device(ctx, ql, gqa, nhk, num_cu, gran)
+    for key, val in op.metadata_valid_prefixes(ref).items():
+        np.testing.assert_array_equal(op.metadata_valid_prefixes(got)[key], val, err_msg=key)
+
+
 def _metadata_for(name):
     from flydsl_amd import get_pa_metadata
     from flydsl_amd.workloads import CONFIGS, context_lengths_for
