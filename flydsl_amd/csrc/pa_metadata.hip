@@ -28,6 +28,7 @@ struct MetaParams {
     int32_t nb, gqa, nhk, num_cu, kv_gran, ql, max_work, max_split_tiles;
     int32_t bin_groups;      // > 1: weighted quotas over this many equal groups of each head's bins
     int32_t bin_weight[4];   // weight of group g (bins [g*nspk/G, (g+1)*nspk/G) of every head)
+    int32_t pack;            // 1: the packing schedule where it applies (pa_metadata_pack_kernel)
 };
 
 __device__ __forceinline__ int cdiv_u(int a, int b) { return (int)(((unsigned)a + (unsigned)b - 1u) / (unsigned)b); }
@@ -43,6 +44,10 @@ constexpr int kParThreads = 1024;
 constexpr int kParBatches = 4 * kParThreads;         // batches the parallel scheduler handles
 constexpr int kParBins = 4096;                       // bins per head the weighted quota table holds
 constexpr int32_t kSerialSentinel = INT32_MIN + 7;   // work_indptr[0]: "the serial scheduler runs"
+constexpr int32_t kPackDone = INT32_MIN + 9;         // work_indptr[0]: "the pack kernel wrote the schedule"
+constexpr int32_t kPackNo = INT32_MIN + 11;          // work_indptr[0]: "the packing schedule does not apply"
+constexpr int kPackBatches = 2048;                   // batches the pack kernel handles
+constexpr int kPackBins = 2048;                      // bins per head the pack kernel handles
 
 // The schedules of one launch: workgroup i of each kernel computes p[i].
 struct MetaSchedules {
@@ -71,6 +76,340 @@ __device__ __forceinline__ T block_scan_excl(T v, T *s_wave, T &total) {
     __syncthreads();  // s_wave is reused by the next scan
     total = tot;
     return before + x - v;
+}
+
+// Weighted quotas apply when every bin keeps at least one partition: S >= 4 nspk
+// and S * (least weight) >= 2 * Wt (a bin's quota is at least S w / Wt - 1), and a
+// head has at most kParBins bins.  wt gets Wt.
+__device__ __forceinline__ bool weighted_quotas(const MetaParams &p, long long S64, int nspk, long long &wt) {
+    const int ng = p.bin_groups;
+    bool weighted = ng > 1 && ng <= 4 && nspk % ng == 0 && S64 >= 4LL * nspk && nspk <= kParBins;
+    long long wmin = 1000;
+    wt = 0;
+    if (weighted) {
+        for (int g = 0; g < ng; ++g) {
+            wt += p.bin_weight[g] * (long long)(nspk / ng);
+            wmin = min(wmin, (long long)p.bin_weight[g]);
+        }
+        weighted = S64 * wmin >= 2 * wt;
+    }
+    return weighted;
+}
+
+// Qs(c) = floor(S * Wc(c) / Wt) for c in [0, nspk], Wc(c) the weights of the bins
+// before c (the threads of the workgroup share the entries).
+__device__ __forceinline__ void fill_weighted_starts(const MetaParams &p, long long S64, int nspk, long long wt,
+                                                     int32_t *s_Q) {
+    const int ng = p.bin_groups, gm = nspk / ng;
+    for (int c = threadIdx.x; c <= nspk; c += blockDim.x) {
+        long long wc = 0;
+        for (int g = 0; g < ng; ++g) wc += p.bin_weight[g] * (long long)min(max(c - g * gm, 0), gm);
+        s_Q[c] = (int)(S64 * wc / wt);
+    }
+}
+
+// Sorts n <= 2 * kParThreads 64-bit keys in LDS ascending (bitonic; n a power of two).
+__device__ void block_sort_u64(uint64_t *key, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < n / 2; i += blockDim.x) {
+                const int lo = 2 * i - (i & (stride - 1));  // first of the pair
+                const int hi = lo + stride;
+                const bool up = (lo & size) == 0;
+                const uint64_t a = key[lo], b = key[hi];
+                if ((a > b) == up) {
+                    key[lo] = b;
+                    key[hi] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Exclusive prefix of two values per thread (entries 2t, 2t+1 of v) over the
+// workgroup; total gets the sum.
+__device__ __forceinline__ int scan2(int v0, int v1, int *s_wave, int &total, int &x1) {
+    const int x0 = block_scan_excl<int>(v0 + v1, s_wave, total);
+    x1 = x0 + v0;
+    return x0;
+}
+
+// The packing schedule (get_pa_metadata's tuned schedule, when it applies): with
+// the same quotas as the sequential fill, sequences in order of (partitions
+// descending, batch) and bins in order of (quota descending, bin), rank k < min(n,
+// B) places sequence k whole in bin k; the other sequences are poured in rank
+// order into the bins' remaining room (gaps, in bin-rank order), split at gap
+// boundaries, and an empty one becomes an empty work in the last bin with a gap.
+// A bin runs its whole sequence, then its poured pieces in rank order.  Split
+// sequences form the reduce groups in batch order, their pieces taking consecutive
+// partial rows by position.  It applies when every rank k < min(n, B) fits its bin
+// (then a head has at most B + gaps - 1 works and at most 2 (gaps - 1) split
+// pieces, within the buffers' bounds), B <= kPackBatches and n <= kPackBins.
+// Writes the schedule and kPackDone to work_indptr[0], else kPackNo (the
+// sequential fill then runs).  Schedules without `pack` are left alone.
+__global__ __launch_bounds__(kParThreads) void pa_metadata_pack_kernel(const MetaSchedules sched) {
+    const MetaParams &p = sched.p[blockIdx.x];
+    if (!p.pack) return;
+    __shared__ int32_t s_P[kPackBatches + 1];    // partitions before batch b
+    __shared__ uint64_t s_key[kPackBatches];     // sort keys: sequences, then bins
+    __shared__ int32_t s_ord[kPackBatches];      // batch of rank k
+    __shared__ int32_t s_bo[kPackBins];          // bin of rank j
+    __shared__ int32_t s_Q[kPackBins + 1];       // first partition of bin c
+    __shared__ int32_t s_Y[kPackBins + 1];       // room of the bin ranks before j (the pour line)
+    __shared__ int32_t s_G[kPackBins + 1];       // bin ranks with room before j
+    __shared__ int32_t s_X[kPackBatches + 1];    // pour position of rank k (ranks >= m)
+    __shared__ int32_t s_np[kPackBatches];       // works of batch b
+    __shared__ int32_t s_PB[kPackBatches + 1];   // pieces of split batches before b
+    __shared__ int32_t s_GB[kPackBatches + 1];   // split batches before b
+    __shared__ int32_t s_cnt[kPackBins];         // works of bin c
+    __shared__ int32_t s_WI[kPackBins + 1];      // works of the bins before c (one head)
+    __shared__ int32_t s_wave[kParThreads / 64];
+    __shared__ long long s_w64[kParThreads / 64];
+    __shared__ int32_t s_flag[2];
+    const int t = threadIdx.x;
+    const int nb = p.nb, nspk = p.num_cu / p.nhk;
+    auto give_up = [&]() {
+        __syncthreads();
+        if (t == 0) p.work_indptr[0] = kPackNo;
+    };
+    if (nb < 1 || nb > kPackBatches || nspk > kPackBins) {
+        give_up();
+        return;
+    }
+    // partitions per batch and their prefix (two per thread); a negative context
+    // length is left to the sequential fill
+    long long pa[2];
+    int neg = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int b = 2 * t + i;
+        const int c = b < nb ? p.ctx[b] : 0;
+        neg |= c < 0 ? 1 : 0;
+        pa[i] = c > 0 ? cdiv_u(c, p.kv_gran) : 0;
+    }
+    if (t == 0) s_flag[0] = 0;
+    __syncthreads();
+    if (neg) s_flag[0] = 1;
+    long long S64;
+    const long long x0 = block_scan_excl<long long>(pa[0] + pa[1], s_w64, S64);
+    if (s_flag[0] || S64 < 1 || S64 > 0x7fffffffLL) {
+        give_up();
+        return;
+    }
+    const int S = (int)S64;
+    if (2 * t < nb) s_P[2 * t] = (int)x0;
+    if (2 * t + 1 < nb) s_P[2 * t + 1] = (int)(x0 + pa[0]);
+    if (t == 0) s_P[nb] = S;
+    long long wt = 0;
+    const bool weighted = weighted_quotas(p, S64, nspk, wt);
+    if (weighted) fill_weighted_starts(p, S64, nspk, wt, s_Q);
+    else
+        for (int c = t; c <= nspk; c += kParThreads)
+            s_Q[c] = (int)((long long)c * (S / nspk) + min(c, S % nspk));
+    __syncthreads();
+    auto Pb = [&](int b) { return s_P[b + 1] - s_P[b]; };
+    auto Qc = [&](int c) { return s_Q[c + 1] - s_Q[c]; };
+    // sequences by (partitions descending, batch), then bins by (quota descending, bin)
+    int n2 = 2;
+    while (n2 < nb) n2 <<= 1;
+    for (int i = t; i < n2; i += kParThreads)
+        s_key[i] = i < nb ? ((uint64_t)(0x7fffffffu - (uint32_t)Pb(i)) << 32) | (uint32_t)i : ~0ull;
+    __syncthreads();
+    block_sort_u64(s_key, n2);
+    for (int k = t; k < nb; k += kParThreads) s_ord[k] = (int)(uint32_t)s_key[k];
+    __syncthreads();
+    int m2 = 2;
+    while (m2 < nspk) m2 <<= 1;
+    for (int i = t; i < m2; i += kParThreads)
+        s_key[i] = i < nspk ? ((uint64_t)(0x7fffffffu - (uint32_t)Qc(i)) << 32) | (uint32_t)i : ~0ull;
+    __syncthreads();
+    block_sort_u64(s_key, m2);
+    for (int j = t; j < nspk; j += kParThreads) s_bo[j] = (int)(uint32_t)s_key[j];
+    if (t == 0) s_flag[0] = 0;
+    __syncthreads();
+    const int m = min(nspk, nb);
+    // every rank k < m fits its bin
+    for (int k = t; k < m; k += kParThreads)
+        if (Pb(s_ord[k]) > Qc(s_bo[k])) s_flag[0] = 1;
+    __syncthreads();
+    if (s_flag[0]) {
+        give_up();
+        return;
+    }
+    // room left in each bin (by rank) and its prefix along the pour line
+    int ga[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int j = 2 * t + i;
+        ga[i] = j < nspk ? Qc(s_bo[j]) - (j < m ? Pb(s_ord[j]) : 0) : 0;
+    }
+    int Yt, y1;
+    const int y0 = scan2(ga[0], ga[1], s_wave, Yt, y1);
+    int Gt, g1;
+    const int g0 = scan2(ga[0] > 0 ? 1 : 0, ga[1] > 0 ? 1 : 0, s_wave, Gt, g1);
+    if (2 * t < nspk) { s_Y[2 * t] = y0; s_G[2 * t] = g0; }
+    if (2 * t + 1 < nspk) { s_Y[2 * t + 1] = y1; s_G[2 * t + 1] = g1; }
+    if (t == 0) { s_Y[nspk] = Yt; s_G[nspk] = Gt; }
+    // pour positions of the ranks past m, and how many of them are empty
+    int la[2], za = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int k = 2 * t + i;
+        la[i] = (k >= m && k < nb) ? Pb(s_ord[k]) : 0;
+        za += (k >= m && k < nb && la[i] == 0) ? 1 : 0;
+    }
+    int Xt, xx1;
+    const int xx0 = scan2(la[0], la[1], s_wave, Xt, xx1);
+    int Zc, zdummy;
+    (void)scan2(za, 0, s_wave, Zc, zdummy);
+    if (2 * t < nb) s_X[2 * t] = xx0;
+    if (2 * t + 1 < nb) s_X[2 * t + 1] = xx1;
+    if (t == 0) s_X[nb] = Xt;
+    __syncthreads();
+    if (Xt != Yt) {  // cannot happen: both are S minus the whole sequences
+        give_up();
+        return;
+    }
+    const int kz = nb - Zc;  // ranks [m, kz) pour, ranks [kz, nb) are empty
+    // the last bin rank with room (the empty sequences' bin), the last rank if none
+    auto last_room = [&]() {
+        int lo = 0, hi = nspk - 1;  // last j with s_G[j] < Gt, i.e. the Gt-th bin with room
+        if (Gt == 0) return nspk - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s_G[mid] < Gt) lo = mid;
+            else hi = mid - 1;
+        }
+        return lo;
+    };
+    const int zrank = last_room();
+    // the bin rank holding pour position x (x < Yt): the last j with s_Y[j] <= x
+    auto bin_at = [&](int x) {
+        int lo = 0, hi = nspk - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s_Y[mid] <= x) lo = mid;
+            else hi = mid - 1;
+        }
+        return lo;
+    };
+    // the pour rank holding position x (x < Yt): the last k in [m, kz) with s_X[k] <= x
+    auto rank_at = [&](int x) {
+        int lo = m, hi = kz - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s_X[mid] <= x) lo = mid;
+            else hi = mid - 1;
+        }
+        return lo;
+    };
+    // works of every batch
+    for (int k = t; k < nb; k += kParThreads) {
+        int w = 1;
+        if (k >= m && k < kz) {
+            const int x = s_X[k], len = Pb(s_ord[k]);
+            w = s_G[bin_at(x + len - 1) + 1] - s_G[bin_at(x)];
+        }
+        s_np[s_ord[k]] = w;
+    }
+    __syncthreads();
+    // split batches and their pieces before each batch
+    int sp[2], sg[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int b = 2 * t + i;
+        const int w = b < nb ? s_np[b] : 0;
+        sp[i] = w > 1 ? w : 0;
+        sg[i] = w > 1 ? 1 : 0;
+    }
+    int T, pb1, G, gb1;
+    const int pb0 = scan2(sp[0], sp[1], s_wave, T, pb1);
+    const int gb0 = scan2(sg[0], sg[1], s_wave, G, gb1);
+    if (2 * t < nb) { s_PB[2 * t] = pb0; s_GB[2 * t] = gb0; }
+    if (2 * t + 1 < nb) { s_PB[2 * t + 1] = pb1; s_GB[2 * t + 1] = gb1; }
+    // works of every bin: its whole sequence, its pour pieces, the empty sequences
+    auto pour_span = [&](int j, int &k0, int &k1) {  // pour ranks meeting bin rank j (k1 < k0 if none)
+        k0 = 0;
+        k1 = -1;
+        const int room = s_Y[j + 1] - s_Y[j];
+        if (room <= 0) return;
+        k0 = rank_at(s_Y[j]);
+        k1 = rank_at(s_Y[j] + room - 1);
+    };
+    for (int j = t; j < nspk; j += kParThreads) {
+        int k0, k1;
+        pour_span(j, k0, k1);
+        s_cnt[s_bo[j]] = (j < m ? 1 : 0) + (k1 >= k0 ? k1 - k0 + 1 : 0) + (j == zrank ? Zc : 0);
+    }
+    __syncthreads();
+    int ca[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = 2 * t + i;
+        ca[i] = c < nspk ? s_cnt[c] : 0;
+    }
+    int W, w1;
+    const int w0 = scan2(ca[0], ca[1], s_wave, W, w1);
+    if (2 * t < nspk) s_WI[2 * t] = w0;
+    if (2 * t + 1 < nspk) s_WI[2 * t + 1] = w1;
+    if (t == 0) s_WI[nspk] = W;
+    __syncthreads();
+    if ((long long)p.nhk * W > p.max_work || T > p.max_split_tiles) {  // within the bounds by construction
+        give_up();
+        return;
+    }
+    // work_info rows of every head
+    auto put = [&](int row, int b, int ploc, int k0, int k1) {
+        const int qs = p.sq[b], qe = p.sq[b + 1];
+        for (int kh = 0; kh < p.nhk; ++kh) {
+            const int32_t qhr = (int32_t)((((unsigned)(kh + 1) * (unsigned)p.gqa) << 16) |
+                                          (((unsigned)kh * (unsigned)p.gqa) & 0xFFFFu));
+            int4 *w = reinterpret_cast<int4 *>(p.work_info) + 2 * ((long long)kh * W + row);
+            w[0] = make_int4(b, ploc, qs, qe);
+            w[1] = make_int4(s_P[b] + k0, s_P[b] + k1, 0, qhr);
+        }
+    };
+    for (int j = t; j < nspk; j += kParThreads) {
+        const int c = s_bo[j];
+        int row = s_WI[c];
+        if (j < m) {
+            const int b = s_ord[j];
+            put(row++, b, -1, 0, Pb(b));
+        }
+        int k0, k1;
+        pour_span(j, k0, k1);
+        for (int k = k0; k <= k1; ++k) {
+            const int b = s_ord[k];
+            const int x = s_X[k], len = Pb(b);
+            const int a = max(x, s_Y[j]) - x, e = min(x + len, s_Y[j + 1]) - x;
+            const int piece = s_G[j] - s_G[bin_at(x)];
+            put(row++, b, s_np[b] > 1 ? p.ql * (s_PB[b] + piece) : -1, a, e);
+        }
+        if (j == zrank)
+            for (int k = kz; k < nb; ++k) put(row++, s_ord[k], -1, 0, 0);
+    }
+    // work_indptr, the reduce maps, the split partial count
+    for (int i = t; i < p.nhk * nspk; i += kParThreads) {
+        const int kh = i / nspk, c = i - kh * nspk;
+        p.work_indptr[i + 1] = kh * W + s_WI[c] + s_cnt[c];
+    }
+    for (int b = t; b < nb; b += kParThreads) {
+        const int w = s_np[b];
+        if (w < 2) continue;
+        const int g = s_GB[b], lb = s_PB[b];
+        p.reduce_indptr[g + 1] = lb + w;
+        p.reduce_final_map[2 * g] = p.sq[b];
+        p.reduce_final_map[2 * g + 1] = p.sq[b + 1];
+        for (int i = 0; i < w; ++i) p.reduce_partial_map[lb + i] = p.ql * (lb + i);
+    }
+    for (int i = G + 1 + t; i <= nb; i += kParThreads) p.reduce_indptr[i] = T;
+    __syncthreads();
+    if (t == 0) {
+        p.reduce_indptr[0] = 0;
+        if (p.partial_count) p.partial_count[0] = T;
+        p.work_indptr[0] = kPackDone;
+    }
 }
 
 // The state machine's output in closed form, computed in parallel.  With
@@ -158,6 +497,11 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
             p.uniform_context[0] = (p.nb == 0 || a == z) ? 1 : 0;
         }
     }
+    if (p.pack && p.work_indptr[0] == kPackDone) {  // pa_metadata_pack_kernel wrote this schedule
+        __syncthreads();
+        if (t == 0) p.work_indptr[0] = 0;
+        return;
+    }
     const bool ok = p.nb <= kParBatches && S64 <= 0x7fffffffLL && (S64 >= nspk || nspk == 1);
     if (!ok) {  // uniform
         if (t == 0) p.work_indptr[0] = kSerialSentinel;
@@ -175,27 +519,12 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
     const int S = (int)S64;
     const int avg = S / nspk, rem = S % nspk;
     const int big = rem * (avg + 1);
-    const int ng = p.bin_groups;
-    // Weighted quotas apply when every bin keeps at least one partition: S >= 4 nspk
-    // and S * (least weight) >= 2 * Wt (a bin's quota is at least S w / Wt - 1).
-    bool weighted = ng > 1 && ng <= 4 && nspk % ng == 0 && (long long)S >= 4LL * nspk && nspk <= kParBins;
-    long long wt = 0, wmin = 1000;
-    if (weighted) {
-        for (int g = 0; g < ng; ++g) {
-            wt += p.bin_weight[g] * (long long)(nspk / ng);
-            wmin = min(wmin, (long long)p.bin_weight[g]);
-        }
-        weighted = S64 * wmin >= 2 * wt;
-    }
+    long long wt = 0;
+    const bool weighted = weighted_quotas(p, S64, nspk, wt);
     // The first partition of every bin, Qs(c) = floor(S * Wc(c) / Wt), tabulated once
     // in LDS (bins are then found by a binary search over the table).
     if (weighted) {
-        const int gm = nspk / ng;
-        for (int c = t; c <= nspk; c += kParThreads) {
-            long long wc = 0;  // weights of the bins before c
-            for (int g = 0; g < ng; ++g) wc += p.bin_weight[g] * (long long)min(max(c - g * gm, 0), gm);
-            s_Q[c] = (int)(S64 * wc / wt);
-        }
+        fill_weighted_starts(p, S64, nspk, wt, s_Q);
         __syncthreads();
     }
     auto Qs = [&](int c) { return weighted ? s_Q[c] : c * avg + min(c, rem); };
@@ -552,6 +881,7 @@ int meta_params(const pa_fp8_metadata_args *a, MetaParams &p) {
     p.partial_count = a->partial_count;
     p.bin_groups = a->bin_groups;
     for (int g = 0; g < 4; ++g) p.bin_weight[g] = a->bin_weight[g];
+    p.pack = a->pack ? 1 : 0;
     return PA_FP8_OK;
 }
 
@@ -566,6 +896,13 @@ extern "C" int pa_fp8_metadata_multi(const pa_fp8_metadata_args *args, int32_t c
         if (st != PA_FP8_OK) return st;
     }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    bool any_pack = false;
+    for (int i = 0; i < count; ++i) any_pack = any_pack || sched.p[i].pack;
+    if (any_pack) {
+        hipLaunchKernelGGL(pa_metadata_pack_kernel, dim3(count), dim3(kParThreads), 0, s, sched);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return PA_FP8_ERR_HIP + (int)e;
+    }
     hipLaunchKernelGGL(pa_metadata_par_kernel, dim3(count), dim3(kParThreads), 0, s, sched);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return PA_FP8_ERR_HIP + (int)err;

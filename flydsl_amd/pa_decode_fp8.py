@@ -930,6 +930,8 @@ def get_pa_metadata(
         _schedule_args(args[k], bufs, seqlens_qo_indptr, ctx, batch_size, gqa, num_kv_heads, s_sm, partition_size,
                        query_length, s_groups, counts[2 * k: 2 * k + 1])
         sched_bufs.append(bufs)
+    if tuned:
+        args[1].pack = 1  # this build's packing schedule where it applies (the reference's stays sequential)
     # the first schedule also writes the derived per-batch values
     args[0].partition_indptr = partition_indptr.data_ptr()
     args[0].uniform_context = counts[1:2].data_ptr()

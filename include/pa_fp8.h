@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define PA_FP8_ABI_VERSION 7
+#define PA_FP8_ABI_VERSION 8
 
 enum pa_fp8_status {
     PA_FP8_OK = 0,
@@ -332,6 +332,20 @@ typedef struct pa_fp8_metadata_args {
     int32_t bin_groups;
     int32_t bin_weight[4];
     int32_t *partial_count;      /* optional [1]: reduce_indptr[num_batches], the split partials */
+    /* 1: the packing schedule where it applies (get_pa_metadata's tuned schedule;
+     * 0 gives the sequential fill, as get_pa_metadata_v1 must).  With the same
+     * quotas, sequences sorted by (partitions descending, batch) and bins by
+     * (quota descending, bin): rank k < min(bins, B) places sequence k whole in
+     * bin k, the remaining sequences are poured in rank order into the bins'
+     * remaining room in bin-rank order (split at its boundaries; an empty one
+     * becomes an empty work in the last bin with room), and split sequences form
+     * the reduce groups in batch order.  It applies when every rank k < min(bins,
+     * B) fits its bin, B <= 2048, bins per head <= 2048, the partitions total
+     * 1 .. 2^31 - 1 and no context length is negative; otherwise the sequential
+     * fill runs.  Fewer split sequences than the sequential fill (c5: 964 split
+     * works instead of 1488) and no sequence is cut at a bin boundary when it fits
+     * a bin whole. */
+    int32_t pack;
 } pa_fp8_metadata_args;
 
 int pa_fp8_metadata_v1(const pa_fp8_metadata_args *args, void *hip_stream);

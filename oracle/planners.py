@@ -266,6 +266,122 @@ def get_pa_metadata_v1(
     }
 
 
+def get_pa_metadata_packed(
+    seqlens_qo_indptr: Sequence[int],
+    context_lens: Sequence[int],
+    num_heads_per_head_k: int,
+    num_heads_k: int,
+    num_cu: int,
+    kv_granularity: int = KV_COMPUTE_BLOCK,
+    query_length: int = 1,
+    quota_of: Optional[Callable[[int, int], int]] = None,
+) -> Optional[Dict[str, np.ndarray]]:
+    """This build's packing schedule (no counterpart in the reference; the device
+    version is pa_metadata.hip's pack kernel).  Same buffers and meaning as
+    get_pa_metadata_v1, with the same per-bin quotas (``quota_of``, else even),
+    but batches are placed whole where they fit:
+
+    * sequences in order of (partitions descending, batch); bins in order of
+      (quota descending, bin);
+    * rank k < min(bins, B): sequence k goes whole into bin k (the rule below
+      guarantees it fits), leaving a gap of quota - partitions;
+    * the remaining sequences (ranks >= bins) are poured, in rank order, into the
+      gaps in bin-rank order, split at gap boundaries; an empty one becomes one
+      empty work in the last bin that has a gap (the last bin if none has);
+    * a bin's works: its whole sequence, then its poured pieces in rank order;
+    * a sequence with several pieces is split: split sequences form the reduce
+      groups in batch order, their pieces taking consecutive partial rows in
+      order of position.
+
+    Returns None (the sequential fill applies) unless every sequence of rank
+    k < min(bins, B) fits bin k, the total is 1 .. 2^31 - 1 partitions, no
+    context length is negative, and B, bins per head <= 2048.
+    """
+    sq = [int(x) for x in seqlens_qo_indptr]
+    ctx = [int(x) for x in context_lens]
+    nb = len(ctx)
+    gqa, nhk, ql = num_heads_per_head_k, num_heads_k, query_length
+    n = num_cu // nhk
+    if nb == 0 or nb > 2048 or n > 2048 or min(ctx) < 0:
+        return None
+    P = [cdiv(c, kv_granularity) for c in ctx]
+    S = sum(P)
+    if S < 1 or S > 0x7FFFFFFF:
+        return None
+    if quota_of is not None:
+        Q = [quota_of(c, S) for c in range(n)]
+    else:
+        Q = [S // n + (1 if c < S % n else 0) for c in range(n)]
+    order = sorted(range(nb), key=lambda b: (-P[b], b))
+    bins = sorted(range(n), key=lambda c: (-Q[c], c))
+    m = min(n, nb)
+    if any(P[order[k]] > Q[bins[k]] for k in range(m)):
+        return None
+    works = [[] for _ in range(n)]  # (batch, p0, p1) in partitions of the batch
+    gap = [0] * n  # by bin rank
+    for k in range(n):
+        c = bins[k]
+        if k < m:
+            works[c].append((order[k], 0, P[order[k]]))
+            gap[k] = Q[c] - P[order[k]]
+        else:
+            gap[k] = Q[c]
+    positive = [k for k in range(n) if gap[k] > 0]
+    zero_bin = bins[positive[-1]] if positive else bins[n - 1]
+    gi, room = 0, (gap[positive[0]] if positive else 0)
+    pieces = {}
+    for k in range(m, nb):
+        b = order[k]
+        if P[b] == 0:
+            works[zero_bin].append((b, 0, 0))
+            continue
+        s = 0
+        while s < P[b]:
+            while room == 0:
+                gi += 1
+                room = gap[positive[gi]]
+            take = min(room, P[b] - s)
+            works[bins[positive[gi]]].append((b, s, s + take))
+            room -= take
+            s += take
+    for c in range(n):
+        for (b, p0, _) in works[c]:
+            pieces.setdefault(b, []).append(p0)
+    split = [b for b in range(nb) if len(pieces[b]) > 1]
+    pidx_of, red_indptr, red_final, red_partial, base = {}, [0], [], [], 0
+    for b in split:
+        for p0 in sorted(pieces[b]):
+            pidx_of[(b, p0)] = ql * base
+            red_partial.append(ql * base)
+            base += 1
+        red_indptr.append(base)
+        red_final.append((sq[b], sq[b + 1]))
+    pind = [0]
+    for x in P:
+        pind.append(pind[-1] + x)
+    W = sum(len(w) for w in works)
+    work_indptr = np.zeros(num_cu + 1, dtype=np.int64)
+    work_info = np.zeros((nhk * W, WORK_INFO_FIELDS), dtype=np.int64)
+    row = 0
+    for kh in range(nhk):
+        qhr = (((kh + 1) * gqa) << 16) | ((kh * gqa) & 0xFFFF)
+        for c in range(n):
+            for (b, p0, p1) in works[c]:
+                work_info[row] = [b, pidx_of.get((b, p0), -1), sq[b], sq[b + 1], pind[b] + p0, pind[b] + p1, 0, qhr]
+                row += 1
+            work_indptr[kh * n + c + 1] = row
+    reduce_indptr = np.full(nb + 1, base, dtype=np.int64)
+    reduce_indptr[: len(red_indptr)] = red_indptr
+    return {
+        "work_indptr": work_indptr.astype(np.int32),
+        "work_info": work_info.astype(np.int32),
+        "reduce_indptr": reduce_indptr.astype(np.int32),
+        "reduce_final_map": np.array(red_final, dtype=np.int32).reshape(-1, 2),
+        "reduce_partial_map": np.array(red_partial, dtype=np.int32),
+        "num_reduce_groups": np.int32(len(split)),
+    }
+
+
 def metadata_valid_prefixes(md: Dict[str, np.ndarray]) -> Dict[str, np.ndarray]:
     """The bytes the reference defines: work_indptr (all), work_info up to
     work_indptr[-1], reduce_indptr (all), reduce_final_map up to the reduce

@@ -31,9 +31,14 @@ def weighted_quota(weights, nspk):
 
 
 def expected_schedule(md, sq, ctx, gqa, nhk, gran=256, ql=1):
-    """The oracle's schedule for one schedule of a get_pa_metadata result (the
-    reference's even one, or the tuned one with its weights)."""
+    """The oracle's schedule for one schedule of a get_pa_metadata result: the
+    reference's even one, or the tuned one (it carries bin_groups) with its
+    weights -- the packing schedule where that applies, else the sequential fill."""
     qf = weighted_quota(md["bin_weight"], md["num_sm"] // nhk) if md.get("bin_groups", 0) > 1 else None
+    if "bin_groups" in md:
+        packed = op.get_pa_metadata_packed(sq, ctx, gqa, nhk, md["num_sm"], gran, ql, quota_of=qf)
+        if packed is not None:
+            return packed
     return op.get_pa_metadata_v1(sq, ctx, gqa, nhk, md["num_sm"], gran, ql, quota_of=qf)
 
 
@@ -123,6 +128,69 @@ def test_device_scheduler_random_wide(seed):
     got, ref = run_device(ctx, ql, gqa, nhk, num_cu, gran)
     for key, val in op.metadata_valid_prefixes(ref).items():
         np.testing.assert_array_equal(op.metadata_valid_prefixes(got)[key], val, err_msg=key)
+
+
+def run_device_schedule(ctx, ql, gqa, nhk, nspk, gran, weights, pack):
+    """One schedule from the device scheduler through the C ABI, with this build's
+    options (bin_groups / bin_weight, pack) set directly; buffers pre-filled with -7."""
+    from flydsl_amd import _lib, get_pa_metadata_info_v1
+
+    dev = torch.device("cuda:0")
+    b = len(ctx)
+    num_cu = nhk * nspk
+    infos = get_pa_metadata_info_v1(b, nhk, num_cu=num_cu)
+    bufs = [torch.full(shape, -7, dtype=torch.int32, device=dev) for shape, _ in infos[1:]]
+    wi, winfo, ri, rfm, rpm = bufs
+    sq = torch.arange(b + 1, dtype=torch.int32, device=dev) * ql
+    ctx_t = torch.tensor(ctx, dtype=torch.int32, device=dev)
+    count = torch.full((1,), -7, dtype=torch.int32, device=dev)
+    a = (_lib.MetadataArgs * 1)()
+    a[0].seqlens_qo_indptr, a[0].context_lens = sq.data_ptr(), ctx_t.data_ptr()
+    a[0].work_indptr, a[0].work_info, a[0].reduce_indptr = wi.data_ptr(), winfo.data_ptr(), ri.data_ptr()
+    a[0].reduce_final_map, a[0].reduce_partial_map = rfm.data_ptr(), rpm.data_ptr()
+    a[0].partial_count = count.data_ptr()
+    a[0].num_batches, a[0].gqa, a[0].num_heads_k, a[0].num_cu = b, gqa, nhk, num_cu
+    a[0].kv_granularity, a[0].query_length = gran, ql
+    a[0].max_work, a[0].max_split_tiles = winfo.numel() // 8, rpm.numel()
+    a[0].bin_groups = len(weights) if weights else 0
+    for g, w in enumerate(weights or ()):
+        a[0].bin_weight[g] = w
+    a[0].pack = 1 if pack else 0
+    _lib.metadata_multi(a, torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize()
+    got = {"work_indptr": wi.cpu().numpy(), "work_info": winfo.cpu().numpy().reshape(-1, 8),
+           "reduce_indptr": ri.cpu().numpy(), "reduce_final_map": rfm.cpu().numpy(),
+           "reduce_partial_map": rpm.cpu().numpy()}
+    return got, int(count.item())
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_device_packing_schedule_matches_oracle(seed):
+    """The device scheduler with pack = 1 (get_pa_metadata's tuned schedule) on the
+    oracle's random packing cases (weights, empty sequences, one bin per head, more
+    bins than batches): bit-exact with the oracle's packing schedule where it
+    applies and with its sequential fill (same quotas) where it does not."""
+    from tests.test_planners import _packed_case
+
+    rng = np.random.default_rng(7000 + seed)
+    nhk, nspk, b, ctx, weights = _packed_case(rng)
+    ql, gqa = int(rng.integers(1, 5)), int(rng.choice([1, 4, 16]))
+    sq = [i * ql for i in range(b + 1)]
+    qf = weighted_quota(weights, nspk) if weights else None
+    ref = op.get_pa_metadata_packed(sq, ctx, gqa, nhk, nhk * nspk, 256, ql, quota_of=qf)
+    if ref is None:
+        ref = op.get_pa_metadata_v1(sq, ctx, gqa, nhk, nhk * nspk, 256, ql, quota_of=qf)
+    got, count = run_device_schedule(ctx, ql, gqa, nhk, nspk, 256, weights, True)
+    got["num_reduce_groups"] = ref["num_reduce_groups"]
+    for key, val in op.metadata_valid_prefixes(ref).items():
+        np.testing.assert_array_equal(op.metadata_valid_prefixes(got)[key], val, err_msg=key)
+    assert count == int(ref["reduce_indptr"][-1])
+    # pack = 0 on the same case is the sequential fill
+    seq = op.get_pa_metadata_v1(sq, ctx, gqa, nhk, nhk * nspk, 256, ql, quota_of=qf)
+    got0, _ = run_device_schedule(ctx, ql, gqa, nhk, nspk, 256, weights, False)
+    got0["num_reduce_groups"] = seq["num_reduce_groups"]
+    for key, val in op.metadata_valid_prefixes(seq).items():
+        np.testing.assert_array_equal(op.metadata_valid_prefixes(got0)[key], val, err_msg=key)
 
 
 def _metadata_for(name):

@@ -286,3 +286,136 @@ def test_scheduler_with_uneven_quotas_covers_every_partition_once():
         ref = op.get_pa_metadata_v1(list(range(b + 1)), ctx, 4, nhk, nspk * nhk, 256, 1)
         for key, val in op.metadata_valid_prefixes(ref).items():
             np.testing.assert_array_equal(op.metadata_valid_prefixes(even)[key], val)
+
+
+# ------------------------------------------------ packing schedule (this build's own)
+def _packed_case(rng):
+    nhk = int(rng.choice([1, 2, 3, 4, 8]))
+    nspk = int(rng.choice([1, 2, 5, 16, 64, 192]))
+    b = int(rng.choice([1, 3, 40, 256, 700]))
+    kind = rng.choice(["uniform", "narrow", "zeros", "equal"])
+    if kind == "uniform":
+        ctx = [int(x) for x in rng.integers(1, int(rng.choice([600, 9000])), size=b)]
+    elif kind == "narrow":
+        lo = int(rng.integers(1000, 4000))
+        ctx = [int(x) for x in rng.integers(lo, 2 * lo, size=b)]
+    elif kind == "zeros":
+        ctx = [int(x) if rng.random() < 0.7 else 0 for x in rng.integers(1, 5000, size=b)]
+    else:
+        ctx = [int(rng.integers(1, 9000))] * b
+    ws = [int(x) for x in rng.integers(90, 140, size=int(rng.choice([1, 2, 3])))]
+    weights = sorted(ws, reverse=True) if nspk % len(ws) == 0 and len(ws) > 1 else None
+    return nhk, nspk, b, ctx, weights
+
+
+def _quota_fn(weights, nspk):
+    if weights is None:
+        return None
+    m = nspk // len(weights)
+    wc = lambda i: sum(w * min(max(i - g * m, 0), m) for g, w in enumerate(weights))  # noqa: E731
+
+    def quota(i, total):
+        return total * wc(i + 1) // wc(nspk) - total * wc(i) // wc(nspk)
+
+    return quota
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_packing_schedule_invariants(seed):
+    """The packing schedule (get_pa_metadata's tuned schedule where it applies),
+    checked against what it must be rather than against a second copy of it:
+    every partition of every sequence runs exactly once per head, every bin holds
+    exactly its quota, sequence rank k < min(bins, B) runs whole in bin rank k (the
+    rank orders recomputed here), a sequence is split exactly when it has several
+    works and then takes consecutive partial rows in position order, reduce groups
+    follow batch order, and the buffers' bounds hold.  When it does not apply, some
+    rank k sequence is larger than its bin."""
+    rng = np.random.default_rng(7000 + seed)
+    nhk, nspk, b, ctx, weights = _packed_case(rng)
+    ql, gqa = int(rng.integers(1, 5)), int(rng.choice([1, 4, 16]))
+    num_cu = nhk * nspk
+    sq = [i * ql for i in range(b + 1)]
+    qf = _quota_fn(weights, nspk)
+    md = op.get_pa_metadata_packed(sq, ctx, gqa, nhk, num_cu, 256, ql, quota_of=qf)
+    P = [(c + 255) // 256 for c in ctx]
+    S = sum(P)
+    Q = [qf(c, S) for c in range(nspk)] if qf else [S // nspk + (1 if c < S % nspk else 0) for c in range(nspk)]
+    order = sorted(range(b), key=lambda x: (-P[x], x))
+    bins = sorted(range(nspk), key=lambda c: (-Q[c], c))
+    m = min(nspk, b)
+    if md is None:
+        assert S < 1 or any(P[order[k]] > Q[bins[k]] for k in range(m))
+        return
+    assert all(P[order[k]] <= Q[bins[k]] for k in range(m))
+    v = op.metadata_valid_prefixes(md)
+    info, wi = v["work_info"], v["work_indptr"]
+    pind = np.concatenate([[0], np.cumsum(P)])
+    W = int(wi[nspk])
+    max_work, max_split = (b + num_cu - 1) * nhk, min(b + num_cu - 1, 2 * (num_cu - 1))
+    assert nhk * W <= max_work and int(v["reduce_indptr"][-1]) <= max_split
+    works_of = {}
+    for k in range(nhk):
+        qhr = (((k + 1) * gqa) << 16) | ((k * gqa) & 0xFFFF)
+        cover = np.zeros(S, np.int64)
+        for c in range(nspk):
+            rows = info[wi[k * nspk + c]:wi[k * nspk + c + 1]]
+            assert (rows[:, 7] == qhr).all()
+            assert int((rows[:, 5] - rows[:, 4]).sum()) == Q[c]  # the bin's quota
+            for r in rows:
+                bb = int(r[0])
+                assert pind[bb] <= r[4] <= r[5] <= pind[bb + 1] and r[2] == sq[bb] and r[3] == sq[bb + 1]
+                cover[r[4]:r[5]] += 1
+                if k == 0:
+                    works_of.setdefault(bb, []).append((int(r[4]), int(r[1]), c))
+        assert (cover == 1).all()  # every partition exactly once
+        assert int(wi[(k + 1) * nspk]) == (k + 1) * W
+    for k in range(m):  # rank k runs whole in bin rank k
+        bb = order[k]
+        assert works_of[bb] == [(int(pind[bb]), -1, bins[k])]
+    split = [bb for bb in range(b) if len(works_of[bb]) > 1]
+    assert int(md["num_reduce_groups"]) == len(split)
+    nxt = 0
+    for g, bb in enumerate(split):  # groups in batch order, consecutive partial rows by position
+        pieces = sorted(works_of[bb])
+        assert [p for (_, p, _) in pieces] == [ql * (nxt + i) for i in range(len(pieces))]
+        assert list(v["reduce_partial_map"][v["reduce_indptr"][g]:v["reduce_indptr"][g + 1]]) == \
+            [p for (_, p, _) in pieces]
+        assert tuple(v["reduce_final_map"][g]) == (sq[bb], sq[bb + 1])
+        nxt += len(pieces)
+    for bb in range(b):
+        if len(works_of[bb]) == 1:
+            assert works_of[bb][0][1] == -1
+    assert int(v["reduce_indptr"][0]) == 0 and (md["reduce_indptr"][len(split):] == nxt).all()
+
+
+def test_packing_schedule_benchmark_shapes():
+    """c5's shape packs (fewer split works than the sequential fill over the same
+    weighted quotas); c3's does not apply (its longest sequences outgrow every bin)."""
+    from flydsl_amd.workloads import CONFIGS, context_lengths_for
+
+    ctx = context_lengths_for(CONFIGS["c5"])
+    qf = _quota_fn([130, 114, 100], 192)
+    sq = [4 * i for i in range(len(ctx) + 1)]
+    packed = op.get_pa_metadata_packed(sq, ctx, 16, 4, 768, 256, 4, quota_of=qf)
+    seq = op.get_pa_metadata_v1(sq, ctx, 16, 4, 768, 256, 4, quota_of=qf)
+    assert packed is not None
+    split = lambda md: int((op.metadata_valid_prefixes(md)["work_info"][:, 1] >= 0).sum())  # noqa: E731
+    assert split(packed) == 964 and split(seq) == 1488
+    ctx3 = context_lengths_for(CONFIGS["c3"])
+    assert op.get_pa_metadata_packed(list(range(129)), ctx3, 4, 8, 512, 256, 1,
+                                     quota_of=_quota_fn([105, 100], 64)) is None
+
+
+def test_packing_schedule_hand_example():
+    """Two bins of 5 partitions, sequences of 4, 3 and 3 partitions: the 4 goes whole
+    to bin 0, a 3 whole to bin 1, and the last 3 is poured into bin 0's 1 left and
+    bin 1's 2 left (split, partial rows 0 and ql); its group is the only one."""
+    gran = 256
+    ctx = [3 * gran, 4 * gran, 3 * gran]  # batch 1 is the largest; batches 0 and 2 tie (batch order)
+    md = op.get_pa_metadata_packed([0, 1, 2, 3], ctx, 1, 1, 2, gran, 1)
+    v = op.metadata_valid_prefixes(md)
+    # pind = [0, 3, 7, 10]; rank order: batch 1 (4), batch 0 (3), batch 2 (3)
+    assert v["work_indptr"].tolist() == [0, 2, 4]
+    assert v["work_info"][:, [0, 1, 4, 5]].tolist() == [[1, -1, 3, 7], [2, 0, 7, 8], [0, -1, 0, 3], [2, 1, 8, 10]]
+    assert v["reduce_indptr"].tolist() == [0, 2, 2, 2]
+    assert v["reduce_final_map"].tolist() == [[2, 3]] and v["reduce_partial_map"].tolist() == [0, 1]
