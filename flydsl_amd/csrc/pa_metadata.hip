@@ -28,7 +28,7 @@ struct MetaParams {
     int32_t nb, gqa, nhk, num_cu, kv_gran, ql, max_work, max_split_tiles;
     int32_t bin_groups;      // > 1: weighted quotas over this many equal groups of each head's bins
     int32_t bin_weight[4];   // weight of group g (bins [g*nspk/G, (g+1)*nspk/G) of every head)
-    int32_t pack;            // 1: the packing schedule where it applies (pa_metadata_pack_kernel)
+    int32_t pack;            // 1: the packing schedule where it applies (pack_schedule)
 };
 
 __device__ __forceinline__ int cdiv_u(int a, int b) { return (int)(((unsigned)a + (unsigned)b - 1u) / (unsigned)b); }
@@ -44,10 +44,13 @@ constexpr int kParThreads = 1024;
 constexpr int kParBatches = 4 * kParThreads;         // batches the parallel scheduler handles
 constexpr int kParBins = 4096;                       // bins per head the weighted quota table holds
 constexpr int32_t kSerialSentinel = INT32_MIN + 7;   // work_indptr[0]: "the serial scheduler runs"
-constexpr int32_t kPackDone = INT32_MIN + 9;         // work_indptr[0]: "the pack kernel wrote the schedule"
-constexpr int32_t kPackNo = INT32_MIN + 11;          // work_indptr[0]: "the packing schedule does not apply"
-constexpr int kPackBatches = 2048;                   // batches the pack kernel handles
-constexpr int kPackBins = 2048;                      // bins per head the pack kernel handles
+constexpr int kPackBatches = 2048;                   // batches the packing schedule handles
+constexpr int kPackBins = 2048;                      // bins per head the packing schedule handles
+// LDS of the packing schedule (pack_schedule's arrays)
+constexpr int kPackInts = 8 * (kPackBatches + 4) + 2 * 12 + 6 * (kPackBins + 4);
+// LDS of the sequential fill's per-batch arrays (works, split works, split batches, first bin)
+constexpr int kFillInts = 4 * (kParBatches + 4);
+constexpr int kUnionInts = kPackInts > kFillInts ? kPackInts : kFillInts;
 
 // The schedules of one launch: workgroup i of each kernel computes p[i].
 struct MetaSchedules {
@@ -108,182 +111,229 @@ __device__ __forceinline__ void fill_weighted_starts(const MetaParams &p, long l
     }
 }
 
-// Sorts n <= 2 * kParThreads 64-bit keys in LDS ascending (bitonic; n a power of two).
-__device__ void block_sort_u64(uint64_t *key, int n) {
-    for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = threadIdx.x; i < n / 2; i += blockDim.x) {
-                const int lo = 2 * i - (i & (stride - 1));  // first of the pair
-                const int hi = lo + stride;
-                const bool up = (lo & size) == 0;
-                const uint64_t a = key[lo], b = key[hi];
-                if ((a > b) == up) {
-                    key[lo] = b;
-                    key[hi] = a;
-                }
-            }
-            __syncthreads();
-        }
-    }
+// Two non-negative ints per thread scanned at once (packed into one 64-bit value;
+// every total here is below 2^31, so the low half never carries): exclusive
+// prefixes of (a0 + a1) and (b0 + b1) over the workgroup, and their totals.
+__device__ __forceinline__ void scan_pair(int a, int b, long long *s_w64, int &pa, int &pb, int &ta, int &tb) {
+    long long tot;
+    const long long x = block_scan_excl<long long>((long long)a + ((long long)b << 32), s_w64, tot);
+    pa = (int)(x & 0xffffffffLL);
+    pb = (int)(x >> 32);
+    ta = (int)(tot & 0xffffffffLL);
+    tb = (int)(tot >> 32);
 }
 
-// Exclusive prefix of two values per thread (entries 2t, 2t+1 of v) over the
-// workgroup; total gets the sum.
-__device__ __forceinline__ int scan2(int v0, int v1, int *s_wave, int &total, int &x1) {
-    const int x0 = block_scan_excl<int>(v0 + v1, s_wave, total);
-    x1 = x0 + v0;
-    return x0;
+// Four such values per thread in one pass (two 64-bit lanes scanned together).
+__device__ __forceinline__ void scan_quad(int a, int b, int c, int d, long long *s_w64, int &pa, int &pb, int &pc,
+                                          int &pd, int &ta, int &tb, int &tc, int &td) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    long long x = (long long)a + ((long long)b << 32), y = (long long)c + ((long long)d << 32);
+    const long long x_in = x, y_in = y;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const long long ux = __shfl_up(x, o, 64), uy = __shfl_up(y, o, 64);
+        if (lane >= o) {
+            x += ux;
+            y += uy;
+        }
+    }
+    if (lane == 63) {
+        s_w64[2 * wave] = x;
+        s_w64[2 * wave + 1] = y;
+    }
+    __syncthreads();
+    long long bx = 0, by = 0, tx = 0, ty = 0;
+#pragma unroll
+    for (int w = 0; w < kParThreads / 64; ++w) {
+        const long long vx = s_w64[2 * w], vy = s_w64[2 * w + 1];
+        bx += w < wave ? vx : 0;
+        by += w < wave ? vy : 0;
+        tx += vx;
+        ty += vy;
+    }
+    __syncthreads();
+    x = bx + x - x_in;
+    y = by + y - y_in;
+    pa = (int)(x & 0xffffffffLL);
+    pb = (int)(x >> 32);
+    pc = (int)(y & 0xffffffffLL);
+    pd = (int)(y >> 32);
+    ta = (int)(tx & 0xffffffffLL);
+    tb = (int)(tx >> 32);
+    tc = (int)(ty & 0xffffffffLL);
+    td = (int)(ty >> 32);
 }
 
 // The packing schedule (get_pa_metadata's tuned schedule, when it applies): with
 // the same quotas as the sequential fill, sequences in order of (partitions
 // descending, batch) and bins in order of (quota descending, bin), rank k < min(n,
 // B) places sequence k whole in bin k; the other sequences are poured in rank
-// order into the bins' remaining room (gaps, in bin-rank order), split at gap
-// boundaries, and an empty one becomes an empty work in the last bin with a gap.
+// order into the bins' remaining room (in bin-rank order), split at room
+// boundaries, and an empty one becomes an empty work in the last bin with room.
 // A bin runs its whole sequence, then its poured pieces in rank order.  Split
-// sequences form the reduce groups in batch order, their pieces taking consecutive
-// partial rows by position.  It applies when every rank k < min(n, B) fits its bin
-// (then a head has at most B + gaps - 1 works and at most 2 (gaps - 1) split
-// pieces, within the buffers' bounds), B <= kPackBatches and n <= kPackBins.
-// Writes the schedule and kPackDone to work_indptr[0], else kPackNo (the
-// sequential fill then runs).  Schedules without `pack` are left alone.
-__global__ __launch_bounds__(kParThreads) void pa_metadata_pack_kernel(const MetaSchedules sched) {
-    const MetaParams &p = sched.p[blockIdx.x];
-    if (!p.pack) return;
-    __shared__ int32_t s_P[kPackBatches + 1];    // partitions before batch b
-    __shared__ uint64_t s_key[kPackBatches];     // sort keys: sequences, then bins
-    __shared__ int32_t s_ord[kPackBatches];      // batch of rank k
-    __shared__ int32_t s_bo[kPackBins];          // bin of rank j
-    __shared__ int32_t s_Q[kPackBins + 1];       // first partition of bin c
-    __shared__ int32_t s_Y[kPackBins + 1];       // room of the bin ranks before j (the pour line)
-    __shared__ int32_t s_G[kPackBins + 1];       // bin ranks with room before j
-    __shared__ int32_t s_X[kPackBatches + 1];    // pour position of rank k (ranks >= m)
-    __shared__ int32_t s_np[kPackBatches];       // works of batch b
-    __shared__ int32_t s_PB[kPackBatches + 1];   // pieces of split batches before b
-    __shared__ int32_t s_GB[kPackBatches + 1];   // split batches before b
-    __shared__ int32_t s_cnt[kPackBins];         // works of bin c
-    __shared__ int32_t s_WI[kPackBins + 1];      // works of the bins before c (one head)
-    __shared__ int32_t s_wave[kParThreads / 64];
-    __shared__ long long s_w64[kParThreads / 64];
-    __shared__ int32_t s_flag[2];
-    const int t = threadIdx.x;
+// sequences form the reduce groups in batch order, their pieces taking
+// consecutive partial rows by position.  It applies when every rank k < min(n, B)
+// fits its bin (then a head has at most B + bins with room - 1 works and at most
+// 2 (bins - 1) split pieces, within the buffers' bounds), B <= kPackBatches,
+// n <= kPackBins, no context length is negative and the partitions total 1 ..
+// 2^31 - 1.  Returns true when it wrote the schedule (work_indptr[0] = 0), false
+// (nothing written, its LDS free again) when the sequential fill is to run.  The
+// caller has the partition prefix in s_P and the total S; `u` is LDS for
+// kPackInts ints.
+// Ranks are counted directly (the lanes of an element compare it with every
+// other one, read as LDS broadcasts), which for the batch sizes of a decode step
+// is several times quicker than a barrier-per-stage sort.
+__device__ bool pack_schedule(const MetaParams &p, const int S, const int32_t *s_P, int32_t *s_Qs, int32_t *u,
+                              long long *s_w64, int32_t *s_red, int32_t *s_flag) {
+    int32_t *s_Pv = u;                            // partitions of batch b (padded to 16-value rounds)
+    int32_t *s_sq = s_Pv + kPackBatches + 16;     // query rows before batch b
+    int32_t *s_ord = s_sq + kPackBatches + 4;     // batch of rank k
+    int32_t *s_Qv = s_ord + kPackBatches;         // quota of bin c (padded to 16-value rounds)
+    int32_t *s_bo = s_Qv + kPackBins + 16;        // bin of rank j
+    int32_t *s_Y = s_bo + kPackBins;              // room of the bin ranks before j (the pour line)
+    int32_t *s_G = s_Y + kPackBins + 4;           // bin ranks with room before j
+    int32_t *s_X = s_G + kPackBins + 4;           // pour position of rank k (ranks >= m)
+    int32_t *s_np = s_X + kPackBatches + 4;       // works of batch b
+    int32_t *s_PB = s_np + kPackBatches;          // pieces of split batches before b
+    int32_t *s_GB = s_PB + kPackBatches + 4;      // split batches before b
+    int32_t *s_cnt = s_GB + kPackBatches + 4;     // works of bin c
+    int32_t *s_WI = s_cnt + kPackBins;            // works of the bins before c (one head)
+    int32_t *s_J = s_WI + kPackBins + 4;          // first bin rank of pour rank k
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int nb = p.nb, nspk = p.num_cu / p.nhk;
     auto give_up = [&]() {
         __syncthreads();
-        if (t == 0) p.work_indptr[0] = kPackNo;
+        return false;
     };
-    if (nb < 1 || nb > kPackBatches || nspk > kPackBins) {
-        give_up();
-        return;
+    int pmax = 0;
+    for (int b = t; b < nb; b += kParThreads) {
+        const int v = s_P[b + 1] - s_P[b];
+        s_Pv[b] = v;
+        pmax = max(pmax, v);
     }
-    // partitions per batch and their prefix (two per thread); a negative context
-    // length is left to the sequential fill
-    long long pa[2];
-    int neg = 0;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int b = 2 * t + i;
-        const int c = b < nb ? p.ctx[b] : 0;
-        neg |= c < 0 ? 1 : 0;
-        pa[i] = c > 0 ? cdiv_u(c, p.kv_gran) : 0;
-    }
+    for (int sh = 32; sh >= 1; sh >>= 1) pmax = max(pmax, __shfl_xor(pmax, sh, 64));
+    if (lane == 0) s_red[wv] = pmax;
     if (t == 0) s_flag[0] = 0;
-    __syncthreads();
-    if (neg) s_flag[0] = 1;
-    long long S64;
-    const long long x0 = block_scan_excl<long long>(pa[0] + pa[1], s_w64, S64);
-    if (s_flag[0] || S64 < 1 || S64 > 0x7fffffffLL) {
-        give_up();
-        return;
-    }
-    const int S = (int)S64;
-    if (2 * t < nb) s_P[2 * t] = (int)x0;
-    if (2 * t + 1 < nb) s_P[2 * t + 1] = (int)(x0 + pa[0]);
-    if (t == 0) s_P[nb] = S;
+    const long long S64 = S;
     long long wt = 0;
     const bool weighted = weighted_quotas(p, S64, nspk, wt);
-    if (weighted) fill_weighted_starts(p, S64, nspk, wt, s_Q);
+    if (weighted) fill_weighted_starts(p, S64, nspk, wt, s_Qs);
     else
         for (int c = t; c <= nspk; c += kParThreads)
-            s_Q[c] = (int)((long long)c * (S / nspk) + min(c, S % nspk));
+            s_Qs[c] = (int)((long long)c * (S / nspk) + min(c, S % nspk));
+    __syncthreads();  // s_Qs, s_Pv, s_sq, the batch maxima
+    int qmax = 0;
+    for (int c = t; c < nspk; c += kParThreads) {
+        s_Qv[c] = s_Qs[c + 1] - s_Qs[c];
+        qmax = max(qmax, s_Qv[c]);
+    }
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) qmax = max(qmax, __shfl_xor(qmax, sh, 64));
+    if (lane == 0) s_red[kParThreads / 64 + wv] = qmax;
+    if (t < 16) {  // padding past the last batch and bin: never counted (real values are >= 0)
+        s_Pv[nb + t] = -1;
+        s_Qv[nspk + t] = -1;
+    }
     __syncthreads();
-    auto Pb = [&](int b) { return s_P[b + 1] - s_P[b]; };
-    auto Qc = [&](int c) { return s_Q[c + 1] - s_Q[c]; };
-    // sequences by (partitions descending, batch), then bins by (quota descending, bin)
-    int n2 = 2;
-    while (n2 < nb) n2 <<= 1;
-    for (int i = t; i < n2; i += kParThreads)
-        s_key[i] = i < nb ? ((uint64_t)(0x7fffffffu - (uint32_t)Pb(i)) << 32) | (uint32_t)i : ~0ull;
+    int Pmax = 0, Qmax = 0;
+#pragma unroll
+    for (int w = 0; w < kParThreads / 64; ++w) {
+        Pmax = max(Pmax, s_red[w]);
+        Qmax = max(Qmax, s_red[kParThreads / 64 + w]);
+    }
+    // the largest sequence fits no bin (the rule fails at rank 0), or a quota too
+    // large for the 31-bit rank keys below
+    if (Pmax > Qmax || Qmax >= (1 << 19)) return give_up();
+    for (int b = t; b <= nb; b += kParThreads) s_sq[b] = p.sq[b];  // read before the writes' barriers
+    // ranks: batch b goes before b' when P_b > P_b', or equal and b < b' (bins alike
+    // by quota), i.e. when its key v << 12 | (4095 - index) is larger (values <
+    // 2^19, indices < 4096).  Batches are ranked by the first half of the threads,
+    // bins by the second.  Each element's rank is counted by tpe adjacent lanes
+    // (tpe = the power of two <= 512 / n, at most 64); lane `part` reads the
+    // 16-byte pieces part, part + tpe, ... (adjacent lanes, adjacent pieces: no bank
+    // conflicts), and the counts are summed across the lanes.  The keys replace
+    // the values in s_Pv / s_Qv only for the count (the values come back after).
+    auto make_keys = [&](int32_t *v, int n, int tid) {
+        for (int i = tid; i < n; i += kParThreads / 2) v[i] = (v[i] << 12) | (4095 - i);
+        for (int i = tid; i < 16; i += kParThreads / 2) v[n + i] = -1;  // the padding never counts
+    };
+    if (t < kParThreads / 2) make_keys(s_Pv, nb, t);
+    else make_keys(s_Qv, nspk, t - kParThreads / 2);
     __syncthreads();
-    block_sort_u64(s_key, n2);
-    for (int k = t; k < nb; k += kParThreads) s_ord[k] = (int)(uint32_t)s_key[k];
+    auto count = [&](const int32_t *v, int n, int32_t *out, int tid) {
+        int tpe = 1;
+        while (tpe < 64 && tpe * 2 * n <= kParThreads / 2) tpe <<= 1;
+        const int n4 = (n + 3) >> 2;  // 16-byte pieces (the -1 padding covers the tail)
+        for (int base = 0; base < n * tpe; base += kParThreads / 2) {
+            const int e = (base + tid) / tpe, part = (base + tid) % tpe;
+            const int ki = v[e < n ? e : 0];
+            int r = 0;
+            for (int q = part; q < n4; q += 4 * tpe) {
+                int4 w[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    w[u] = q + u * tpe < n4 ? *reinterpret_cast<const int4 *>(v + 4 * (q + u * tpe))
+                                            : make_int4(-1, -1, -1, -1);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    r += (w[u].x > ki) + (w[u].y > ki) + (w[u].z > ki) + (w[u].w > ki);
+            }
+            for (int o = 1; o < tpe; o <<= 1) r += __shfl_xor(r, o, 64);
+            if (part == 0 && e < n) out[r] = e;
+        }
+    };
+    if (t < kParThreads / 2) count(s_Pv, nb, s_ord, t);
+    else count(s_Qv, nspk, s_bo, t - kParThreads / 2);
     __syncthreads();
-    int m2 = 2;
-    while (m2 < nspk) m2 <<= 1;
-    for (int i = t; i < m2; i += kParThreads)
-        s_key[i] = i < nspk ? ((uint64_t)(0x7fffffffu - (uint32_t)Qc(i)) << 32) | (uint32_t)i : ~0ull;
-    __syncthreads();
-    block_sort_u64(s_key, m2);
-    for (int j = t; j < nspk; j += kParThreads) s_bo[j] = (int)(uint32_t)s_key[j];
-    if (t == 0) s_flag[0] = 0;
+    for (int i = t; i < nb; i += kParThreads) s_Pv[i] >>= 12;  // the values again
+    for (int i = t; i < nspk; i += kParThreads) s_Qv[i] >>= 12;
     __syncthreads();
     const int m = min(nspk, nb);
-    // every rank k < m fits its bin
-    for (int k = t; k < m; k += kParThreads)
-        if (Pb(s_ord[k]) > Qc(s_bo[k])) s_flag[0] = 1;
-    __syncthreads();
-    if (s_flag[0]) {
-        give_up();
-        return;
-    }
-    // room left in each bin (by rank) and its prefix along the pour line
-    int ga[2];
+    for (int k = t; k < m; k += kParThreads)  // every rank k < m fits its bin
+        if (s_Pv[s_ord[k]] > s_Qv[s_bo[k]]) s_flag[0] = 1;
+    // room left in each bin (by rank), then the pour lengths of the ranks past m
+    int ga[2], la[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int j = 2 * t + i;
-        ga[i] = j < nspk ? Qc(s_bo[j]) - (j < m ? Pb(s_ord[j]) : 0) : 0;
+        ga[i] = j < nspk ? s_Qv[s_bo[j]] - (j < m ? s_Pv[s_ord[j]] : 0) : 0;
+        la[i] = (j >= m && j < nb) ? s_Pv[s_ord[j]] : 0;
     }
-    int Yt, y1;
-    const int y0 = scan2(ga[0], ga[1], s_wave, Yt, y1);
-    int Gt, g1;
-    const int g0 = scan2(ga[0] > 0 ? 1 : 0, ga[1] > 0 ? 1 : 0, s_wave, Gt, g1);
-    if (2 * t < nspk) { s_Y[2 * t] = y0; s_G[2 * t] = g0; }
-    if (2 * t + 1 < nspk) { s_Y[2 * t + 1] = y1; s_G[2 * t + 1] = g1; }
-    if (t == 0) { s_Y[nspk] = Yt; s_G[nspk] = Gt; }
-    // pour positions of the ranks past m, and how many of them are empty
-    int la[2], za = 0;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int k = 2 * t + i;
-        la[i] = (k >= m && k < nb) ? Pb(s_ord[k]) : 0;
-        za += (k >= m && k < nb && la[i] == 0) ? 1 : 0;
+    const int za = (2 * t >= m && 2 * t < nb && la[0] == 0) + (2 * t + 1 >= m && 2 * t + 1 < nb && la[1] == 0);
+    int y0, g0, Yt, Gt, x0p, z0, Xt, Zc;
+    scan_quad(ga[0] + ga[1], (ga[0] > 0) + (ga[1] > 0), la[0] + la[1], za, s_w64, y0, g0, x0p, z0, Yt, Gt, Xt, Zc);
+    if (s_flag[0]) return give_up();  // read after the scan's barriers
+    if (2 * t < nspk) {
+        s_Y[2 * t] = y0;
+        s_G[2 * t] = g0;
     }
-    int Xt, xx1;
-    const int xx0 = scan2(la[0], la[1], s_wave, Xt, xx1);
-    int Zc, zdummy;
-    (void)scan2(za, 0, s_wave, Zc, zdummy);
-    if (2 * t < nb) s_X[2 * t] = xx0;
-    if (2 * t + 1 < nb) s_X[2 * t + 1] = xx1;
+    if (2 * t + 1 < nspk) {
+        s_Y[2 * t + 1] = y0 + ga[0];
+        s_G[2 * t + 1] = g0 + (ga[0] > 0);
+    }
+    if (t == 0) {
+        s_Y[nspk] = Yt;
+        s_G[nspk] = Gt;
+    }
+    if (2 * t < nb) s_X[2 * t] = x0p;
+    if (2 * t + 1 < nb) s_X[2 * t + 1] = x0p + la[0];
     if (t == 0) s_X[nb] = Xt;
     __syncthreads();
-    if (Xt != Yt) {  // cannot happen: both are S minus the whole sequences
-        give_up();
-        return;
-    }
+    if (Xt != Yt) return give_up();  // cannot happen: both are S minus the whole sequences
     const int kz = nb - Zc;  // ranks [m, kz) pour, ranks [kz, nb) are empty
-    // the last bin rank with room (the empty sequences' bin), the last rank if none
-    auto last_room = [&]() {
-        int lo = 0, hi = nspk - 1;  // last j with s_G[j] < Gt, i.e. the Gt-th bin with room
-        if (Gt == 0) return nspk - 1;
+    // the last bin rank with room (the empty sequences' bin), the last rank if none:
+    // the last j with s_G[j] < Gt
+    int zrank = nspk - 1;
+    if (Gt > 0) {
+        int lo = 0, hi = nspk - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
             if (s_G[mid] < Gt) lo = mid;
             else hi = mid - 1;
         }
-        return lo;
-    };
-    const int zrank = last_room();
+        zrank = lo;
+    }
     // the bin rank holding pour position x (x < Yt): the last j with s_Y[j] <= x
     auto bin_at = [&](int x) {
         int lo = 0, hi = nspk - 1;
@@ -304,31 +354,8 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_pack_kernel(const Met
         }
         return lo;
     };
-    // works of every batch
-    for (int k = t; k < nb; k += kParThreads) {
-        int w = 1;
-        if (k >= m && k < kz) {
-            const int x = s_X[k], len = Pb(s_ord[k]);
-            w = s_G[bin_at(x + len - 1) + 1] - s_G[bin_at(x)];
-        }
-        s_np[s_ord[k]] = w;
-    }
-    __syncthreads();
-    // split batches and their pieces before each batch
-    int sp[2], sg[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int b = 2 * t + i;
-        const int w = b < nb ? s_np[b] : 0;
-        sp[i] = w > 1 ? w : 0;
-        sg[i] = w > 1 ? 1 : 0;
-    }
-    int T, pb1, G, gb1;
-    const int pb0 = scan2(sp[0], sp[1], s_wave, T, pb1);
-    const int gb0 = scan2(sg[0], sg[1], s_wave, G, gb1);
-    if (2 * t < nb) { s_PB[2 * t] = pb0; s_GB[2 * t] = gb0; }
-    if (2 * t + 1 < nb) { s_PB[2 * t + 1] = pb1; s_GB[2 * t + 1] = gb1; }
-    // works of every bin: its whole sequence, its pour pieces, the empty sequences
+    // works of every batch (and the first bin rank of every pour rank, kept in s_J),
+    // and of every bin: its whole sequence, its pour pieces, the empty sequences
     auto pour_span = [&](int j, int &k0, int &k1) {  // pour ranks meeting bin rank j (k1 < k0 if none)
         k0 = 0;
         k1 = -1;
@@ -337,53 +364,72 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_pack_kernel(const Met
         k0 = rank_at(s_Y[j]);
         k1 = rank_at(s_Y[j] + room - 1);
     };
+    for (int k = t; k < nb; k += kParThreads) {
+        int w = 1;
+        if (k >= m && k < kz) {
+            const int x = s_X[k], len = s_Pv[s_ord[k]];
+            const int j0 = bin_at(x);
+            s_J[k] = j0;
+            w = s_G[bin_at(x + len - 1) + 1] - s_G[j0];
+        }
+        s_np[s_ord[k]] = w;
+    }
     for (int j = t; j < nspk; j += kParThreads) {
         int k0, k1;
         pour_span(j, k0, k1);
         s_cnt[s_bo[j]] = (j < m ? 1 : 0) + (k1 >= k0 ? k1 - k0 + 1 : 0) + (j == zrank ? Zc : 0);
     }
     __syncthreads();
-    int ca[2];
+    // split batches and their pieces before each batch, works of the bins before each bin
+    int sp[2], sg[2], ca[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int c = 2 * t + i;
-        ca[i] = c < nspk ? s_cnt[c] : 0;
+        const int b = 2 * t + i;
+        const int w = b < nb ? s_np[b] : 0;
+        sp[i] = w > 1 ? w : 0;
+        sg[i] = w > 1 ? 1 : 0;
+        ca[i] = b < nspk ? s_cnt[b] : 0;
     }
-    int W, w1;
-    const int w0 = scan2(ca[0], ca[1], s_wave, W, w1);
+    int pb0, gb0, w0, dz, T, G, W, dzt;
+    scan_quad(sp[0] + sp[1], sg[0] + sg[1], ca[0] + ca[1], 0, s_w64, pb0, gb0, w0, dz, T, G, W, dzt);
+    if (2 * t < nb) {
+        s_PB[2 * t] = pb0;
+        s_GB[2 * t] = gb0;
+    }
+    if (2 * t + 1 < nb) {
+        s_PB[2 * t + 1] = pb0 + sp[0];
+        s_GB[2 * t + 1] = gb0 + sg[0];
+    }
     if (2 * t < nspk) s_WI[2 * t] = w0;
-    if (2 * t + 1 < nspk) s_WI[2 * t + 1] = w1;
+    if (2 * t + 1 < nspk) s_WI[2 * t + 1] = w0 + ca[0];
     if (t == 0) s_WI[nspk] = W;
     __syncthreads();
-    if ((long long)p.nhk * W > p.max_work || T > p.max_split_tiles) {  // within the bounds by construction
-        give_up();
-        return;
-    }
+    if ((long long)p.nhk * W > p.max_work || T > p.max_split_tiles) return give_up();  // within bounds by construction
     // work_info rows of every head
     auto put = [&](int row, int b, int ploc, int k0, int k1) {
-        const int qs = p.sq[b], qe = p.sq[b + 1];
+        const int qs = s_sq[b], qe = s_sq[b + 1];
+        const int4 lo = make_int4(b, ploc, qs, qe);
         for (int kh = 0; kh < p.nhk; ++kh) {
             const int32_t qhr = (int32_t)((((unsigned)(kh + 1) * (unsigned)p.gqa) << 16) |
                                           (((unsigned)kh * (unsigned)p.gqa) & 0xFFFFu));
             int4 *w = reinterpret_cast<int4 *>(p.work_info) + 2 * ((long long)kh * W + row);
-            w[0] = make_int4(b, ploc, qs, qe);
+            w[0] = lo;
             w[1] = make_int4(s_P[b] + k0, s_P[b] + k1, 0, qhr);
         }
     };
     for (int j = t; j < nspk; j += kParThreads) {
-        const int c = s_bo[j];
-        int row = s_WI[c];
+        int row = s_WI[s_bo[j]];
         if (j < m) {
             const int b = s_ord[j];
-            put(row++, b, -1, 0, Pb(b));
+            put(row++, b, -1, 0, s_Pv[b]);
         }
         int k0, k1;
         pour_span(j, k0, k1);
         for (int k = k0; k <= k1; ++k) {
             const int b = s_ord[k];
-            const int x = s_X[k], len = Pb(b);
+            const int x = s_X[k], len = s_Pv[b];
             const int a = max(x, s_Y[j]) - x, e = min(x + len, s_Y[j + 1]) - x;
-            const int piece = s_G[j] - s_G[bin_at(x)];
+            const int piece = s_G[j] - s_G[s_J[k]];
             put(row++, b, s_np[b] > 1 ? p.ql * (s_PB[b] + piece) : -1, a, e);
         }
         if (j == zrank)
@@ -399,17 +445,17 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_pack_kernel(const Met
         if (w < 2) continue;
         const int g = s_GB[b], lb = s_PB[b];
         p.reduce_indptr[g + 1] = lb + w;
-        p.reduce_final_map[2 * g] = p.sq[b];
-        p.reduce_final_map[2 * g + 1] = p.sq[b + 1];
+        p.reduce_final_map[2 * g] = s_sq[b];
+        p.reduce_final_map[2 * g + 1] = s_sq[b + 1];
         for (int i = 0; i < w; ++i) p.reduce_partial_map[lb + i] = p.ql * (lb + i);
     }
     for (int i = G + 1 + t; i <= nb; i += kParThreads) p.reduce_indptr[i] = T;
-    __syncthreads();
     if (t == 0) {
         p.reduce_indptr[0] = 0;
         if (p.partial_count) p.partial_count[0] = T;
-        p.work_indptr[0] = kPackDone;
+        p.work_indptr[0] = 0;
     }
+    return true;
 }
 
 // The state machine's output in closed form, computed in parallel.  With
@@ -435,14 +481,18 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_pack_kernel(const Met
 __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const MetaSchedules sched) {
     const MetaParams &p = sched.p[blockIdx.x];
     __shared__ int32_t s_P[kParBatches + 1];  // partitions before batch b
-    __shared__ int32_t s_W[kParBatches + 1];  // works of head 0 before batch b
-    __shared__ int32_t s_L[kParBatches + 1];  // works of split batches before batch b
-    __shared__ int32_t s_G[kParBatches + 1];  // split batches before batch b
-    __shared__ int32_t s_F[kParBatches];      // first bin of batch b
     __shared__ int32_t s_Q[kParBins + 1];     // weighted quotas: first partition of bin c
-    __shared__ long long s_w64[kParThreads / 64];
+    // the sequential fill's arrays and the packing schedule's share one region
+    __shared__ __attribute__((aligned(16))) int32_t s_u[kUnionInts];
+    int32_t *s_W = s_u;                        // works of head 0 before batch b
+    int32_t *s_L = s_W + kParBatches + 4;      // works of split batches before batch b
+    int32_t *s_G = s_L + kParBatches + 4;      // split batches before batch b
+    int32_t *s_F = s_G + kParBatches + 4;      // first bin of batch b
+    __shared__ long long s_w64[2 * (kParThreads / 64)];
     __shared__ int32_t s_w32[kParThreads / 64];
     __shared__ int32_t s_mm[2 * (kParThreads / 64)];
+    __shared__ int32_t s_pk[2 * (kParThreads / 64)];
+    __shared__ int32_t s_flag[1];
     const int t = threadIdx.x;
     const int nspk = p.num_cu / p.nhk;
     // partitions per batch and their prefix (four consecutive batches per thread,
@@ -497,10 +547,46 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
             p.uniform_context[0] = (p.nb == 0 || a == z) ? 1 : 0;
         }
     }
-    if (p.pack && p.work_indptr[0] == kPackDone) {  // pa_metadata_pack_kernel wrote this schedule
+    // the packing schedule, where it applies, instead of the sequential fill
+    if (p.pack && p.nb >= 1 && p.nb <= kPackBatches && nspk <= kPackBins && S64 >= 1 && S64 <= 0x7fffffffLL) {
+        // no negative context length (the sequential fill keeps those), and the
+        // largest sequence within an upper bound on any bin's quota (S / bins rounded
+        // up, or S w_max / Wt + 1 with weights), checked before any packing work;
+        // s_pk is touched by nothing else, so a rejection needs no further barrier
+        int lo = cmin, hi = max(max(np4[0], np4[1]), max(np4[2], np4[3]));
+#pragma unroll
+        for (int sh = 32; sh >= 1; sh >>= 1) {
+            lo = min(lo, __shfl_xor(lo, sh, 64));
+            hi = max(hi, __shfl_xor(hi, sh, 64));
+        }
+        if ((t & 63) == 0) {
+            s_pk[2 * (t >> 6)] = lo;
+            s_pk[2 * (t >> 6) + 1] = hi;
+        }
         __syncthreads();
-        if (t == 0) p.work_indptr[0] = 0;
-        return;
+        for (int w = 0; w < kParThreads / 64; ++w) {
+            lo = min(lo, s_pk[2 * w]);
+            hi = max(hi, s_pk[2 * w + 1]);
+        }
+        long long wt = 0, bound = (S64 + nspk - 1) / nspk;
+        if (weighted_quotas(p, S64, nspk, wt)) {
+            long long wmax = 0;
+            for (int g = 0; g < p.bin_groups; ++g) wmax = max(wmax, (long long)p.bin_weight[g]);
+            bound = S64 * wmax / wt + 1;
+        }
+        if (lo >= 0 && hi <= bound) {
+            long long r = run;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {  // one chunk: run and np4 are this thread's prefix and counts
+                const int b = 4 * t + i;
+                if (b <= p.nb) s_P[b] = (int)r;
+                r += np4[i];
+            }
+            if (t == 0) s_P[p.nb] = (int)S64;
+            __syncthreads();
+            if (pack_schedule(p, (int)S64, s_P, s_Q, s_u, s_w64, s_mm, s_flag)) return;
+            __syncthreads();  // s_mm, s_Q and the shared region are free again
+        }
     }
     const bool ok = p.nb <= kParBatches && S64 <= 0x7fffffffLL && (S64 >= nspk || nspk == 1);
     if (!ok) {  // uniform
@@ -896,13 +982,6 @@ extern "C" int pa_fp8_metadata_multi(const pa_fp8_metadata_args *args, int32_t c
         if (st != PA_FP8_OK) return st;
     }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    bool any_pack = false;
-    for (int i = 0; i < count; ++i) any_pack = any_pack || sched.p[i].pack;
-    if (any_pack) {
-        hipLaunchKernelGGL(pa_metadata_pack_kernel, dim3(count), dim3(kParThreads), 0, s, sched);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return PA_FP8_ERR_HIP + (int)e;
-    }
     hipLaunchKernelGGL(pa_metadata_par_kernel, dim3(count), dim3(kParThreads), 0, s, sched);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return PA_FP8_ERR_HIP + (int)err;

@@ -340,9 +340,9 @@ typedef struct pa_fp8_metadata_args {
      * remaining room in bin-rank order (split at its boundaries; an empty one
      * becomes an empty work in the last bin with room), and split sequences form
      * the reduce groups in batch order.  It applies when every rank k < min(bins,
-     * B) fits its bin, B <= 2048, bins per head <= 2048, the partitions total
-     * 1 .. 2^31 - 1 and no context length is negative; otherwise the sequential
-     * fill runs.  Fewer split sequences than the sequential fill (c5: 964 split
+     * B) fits its bin, B <= 2048, bins per head <= 2048, every quota is below
+     * 2^19 partitions, the partitions total 1 .. 2^31 - 1 and no context length
+     * is negative; otherwise the sequential fill runs.  Fewer split sequences than the sequential fill (c5: 964 split
      * works instead of 1488) and no sequence is cut at a bin boundary when it fits
      * a bin whole. */
     int32_t pack;

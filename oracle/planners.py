@@ -294,8 +294,9 @@ def get_pa_metadata_packed(
       order of position.
 
     Returns None (the sequential fill applies) unless every sequence of rank
-    k < min(bins, B) fits bin k, the total is 1 .. 2^31 - 1 partitions, no
-    context length is negative, and B, bins per head <= 2048.
+    k < min(bins, B) fits bin k, the total is 1 .. 2^31 - 1 partitions, every
+    quota is below 2^19 partitions, no context length is negative, and B, bins
+    per head <= 2048.
     """
     sq = [int(x) for x in seqlens_qo_indptr]
     ctx = [int(x) for x in context_lens]
@@ -312,6 +313,8 @@ def get_pa_metadata_packed(
         Q = [quota_of(c, S) for c in range(n)]
     else:
         Q = [S // n + (1 if c < S % n else 0) for c in range(n)]
+    if max(Q) >= 1 << 19:  # (the device ranks by 31-bit keys)
+        return None
     order = sorted(range(nb), key=lambda b: (-P[b], b))
     bins = sorted(range(n), key=lambda c: (-Q[c], c))
     m = min(n, nb)
