@@ -40,7 +40,7 @@ _REFERENCE_BINS_PER_CU = 3  # the reference's _PA_METADATA_GRID_OVERSUB (kernels
 # the others): with even quotas, c5's three per CU ran 287 / 308 / 329 us and
 # c3's two per CU 145 / 153 us.  The weights are the fastest of a sweep
 # (three per CU: 108..145 for the first group; two per CU: 105..120).
-_BIN_WEIGHTS = {2: (105, 100), 3: (130, 114, 100)}
+_BIN_WEIGHTS = {2: (105, 100), 3: (115, 107, 100)}
 
 
 def _metadata_bins_per_cu(query_length: int, query_group_size: int, head_dim: int = 128) -> int:

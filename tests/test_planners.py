@@ -394,13 +394,13 @@ def test_packing_schedule_benchmark_shapes():
     from flydsl_amd.workloads import CONFIGS, context_lengths_for
 
     ctx = context_lengths_for(CONFIGS["c5"])
-    qf = _quota_fn([130, 114, 100], 192)
+    qf = _quota_fn([115, 107, 100], 192)
     sq = [4 * i for i in range(len(ctx) + 1)]
     packed = op.get_pa_metadata_packed(sq, ctx, 16, 4, 768, 256, 4, quota_of=qf)
     seq = op.get_pa_metadata_v1(sq, ctx, 16, 4, 768, 256, 4, quota_of=qf)
     assert packed is not None
     split = lambda md: int((op.metadata_valid_prefixes(md)["work_info"][:, 1] >= 0).sum())  # noqa: E731
-    assert split(packed) == 964 and split(seq) == 1488
+    assert split(packed) == 984 and split(seq) == 1520
     ctx3 = context_lengths_for(CONFIGS["c3"])
     assert op.get_pa_metadata_packed(list(range(129)), ctx3, 4, 8, 512, 256, 1,
                                      quota_of=_quota_fn([105, 100], 64)) is None
