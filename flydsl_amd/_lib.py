@@ -272,6 +272,7 @@ EXPORTED_SYMBOLS = (
     "pa_fp8_metadata_v1",
     "pa_fp8_metadata_multi",
     "pa_fp8_rope_cache",
+    "pa_fp8_hw_reciprocal",
     "pa_fp8_status_string",
     "pa_fp8_abi_version",
 )
@@ -313,6 +314,8 @@ def _load() -> ctypes.CDLL:
     lib.pa_fp8_metadata_multi.restype = ctypes.c_int
     lib.pa_fp8_rope_cache.argtypes = [ctypes.POINTER(RopeCacheArgs), _vp]
     lib.pa_fp8_rope_cache.restype = ctypes.c_int
+    lib.pa_fp8_hw_reciprocal.argtypes = [_vp, _vp, ctypes.c_int64, _vp]
+    lib.pa_fp8_hw_reciprocal.restype = ctypes.c_int
     lib.pa_fp8_status_string.argtypes = [ctypes.c_int]
     lib.pa_fp8_status_string.restype = ctypes.c_char_p
     return lib
@@ -357,3 +360,8 @@ def metadata_multi(args, stream: int) -> None:
 
 def rope_cache(args: RopeCacheArgs, stream: int) -> None:
     check("pa_fp8_rope_cache", LIB.pa_fp8_rope_cache(ctypes.byref(args), _vp(stream)))
+
+
+def hw_reciprocal(x_ptr: int, y_ptr: int, n: int, stream: int) -> None:
+    """y[i] = v_rcp_f32(x[i]) on the device (float32 buffers of n elements)."""
+    check("pa_fp8_hw_reciprocal", LIB.pa_fp8_hw_reciprocal(_vp(x_ptr), _vp(y_ptr), n, _vp(stream)))

@@ -16,9 +16,11 @@
 // rounded to bf16 / f16 (computed in f32 -- exact products of two 16-bit values --
 // then rounded to nearest even).  fp8 cache codes come from v_cvt_pk_fp8_f32
 // (round to nearest even; |x| > 464 -> NaN, as torch's float8_e4m3fn cast).
-// Per-tensor scales are applied as x * (1/scale) with the reciprocal computed
-// once per lane by IEEE division (the reference uses the approximate v_rcp_f32,
-// :282-283, which equals it at scales such as 0.1 and powers of two).
+// Per-tensor scales are applied as x * v_rcp_f32(scale), the hardware reciprocal
+// the reference takes (:282-283): within 1 ulp of 1/scale, exact at powers of two,
+// and not always the correctly rounded quotient (one ulp off at 3.0, and at about
+// 11% of scales over a log-uniform sweep), so the cache codes follow the
+// reference's bytes at every scale.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -362,8 +364,8 @@ __device__ __forceinline__ void finish_kv_row(const RopeParams &p, const RowIn &
 
     if constexpr (FMT == PA_FP8_CACHE_FP8_TENSOR) {
         if (write) {
-            const float rk = 1.0f / kscale;
-            const float rv = 1.0f / vscale;
+            const float rk = __builtin_amdgcn_rcpf(kscale);
+            const float rv = __builtin_amdgcn_rcpf(vscale);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 x1[i] *= rk;
@@ -562,6 +564,11 @@ hipError_t launch_format(const RopeParams &p, int fmt, int layout, dim3 grid, hi
 
 inline bool aligned(const void *ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; }
 
+__global__ __launch_bounds__(256) void hw_reciprocal_kernel(const float *x, float *y, int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) y[i] = __builtin_amdgcn_rcpf(x[i]);
+}
+
 }  // namespace
 }  // namespace pa
 
@@ -677,5 +684,16 @@ extern "C" int pa_fp8_rope_cache(const pa_fp8_rope_cache_args *a, void *hip_stre
     const hipError_t e = a->elem_dtype == PA_FP8_BF16
                              ? launch_format<PA_FP8_BF16>(p, a->cache_format, a->kv_layout, grid, s)
                              : launch_format<PA_FP8_F16>(p, a->cache_format, a->kv_layout, grid, s);
+    return e == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + int(e);
+}
+
+extern "C" int pa_fp8_hw_reciprocal(const float *x, float *y, int64_t n, void *hip_stream) {
+    if (n < 0) return PA_FP8_ERR_SHAPE;
+    if (n > 0 && (x == nullptr || y == nullptr)) return PA_FP8_ERR_NULL_POINTER;
+    if (n == 0) return PA_FP8_OK;
+    if ((n + 255) / 256 > 0x7fffffffLL) return PA_FP8_ERR_SHAPE;
+    hipLaunchKernelGGL(pa::hw_reciprocal_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(hip_stream), x, y, n);
+    const hipError_t e = hipGetLastError();
     return e == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + int(e);
 }

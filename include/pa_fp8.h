@@ -362,7 +362,7 @@ int pa_fp8_metadata_multi(const pa_fp8_metadata_args *args, int32_t count, void 
 /* KV-cache formats written by pa_fp8_rope_cache */
 enum pa_fp8_cache_format {
     PA_FP8_CACHE_ELEM = 0,       /* cache of the element dtype (bf16 / f16), written unscaled   */
-    PA_FP8_CACHE_FP8_TENSOR = 1, /* fp8 e4m3fn, code = e4m3(x * (1 / scale[0])), scale read     */
+    PA_FP8_CACHE_FP8_TENSOR = 1, /* fp8 e4m3fn, code = e4m3(x * v_rcp_f32(scale[0])), scale read */
     PA_FP8_CACHE_FP8_TOKEN = 2   /* fp8 e4m3fn, scale = amax/448 per (token, kv head) written,
                                     code = e4m3(x / scale)                                     */
 };
@@ -440,6 +440,16 @@ typedef struct pa_fp8_rope_cache_args {
 } pa_fp8_rope_cache_args;
 
 int pa_fp8_rope_cache(const pa_fp8_rope_cache_args *args, void *hip_stream);
+
+/*
+ * y[i] = v_rcp_f32(x[i]) for i < n (device pointers, n >= 0): the hardware
+ * reciprocal pa_fp8_rope_cache applies to per-tensor scales, as the reference
+ * writer does (kernels/fused_rope_cache_kernel.py:282-283, `rocdl.rcp`).  It is
+ * within 1 ulp of 1/x but not always the correctly rounded quotient, so the
+ * cache codes of a scale depend on it; this entry exposes the value for
+ * checkers that restate the writer.  No counterpart of its own in the reference.
+ */
+int pa_fp8_hw_reciprocal(const float *x, float *y, int64_t n, void *hip_stream);
 
 /* Human-readable text of a status code (static storage). */
 const char *pa_fp8_status_string(int status);

@@ -12,8 +12,9 @@ torch model of it, ``_rope_ref`` (tests/kernels/test_fused_rope_cache.py:166-235
   (``reuse_freqs_front_part``, :190) or ``cos/sin[pos, d + D/2]`` for full ones;
 * cache write (:252-429): tokens with ``slot >= 0`` go to block ``slot // bs``,
   position ``slot % bs``; K receives the rotated key, V the value;
-* fp8 per-tensor (:270-296): codes of ``x * (1 / scale)`` (float32 product);
-  the reciprocal here is float32 division -- see ``reciprocal``;
+* fp8 per-tensor (:270-296): codes of ``x * rcp`` (float32 product) with
+  ``rcp = v_rcp_f32(scale)``, the hardware reciprocal (:282-283) -- see
+  ``reciprocal``;
 * fp8 per-token (this build's extension for the decode kernels' per-token
   format): ``pertoken_quant`` of each (token, kv head) vector.
 
@@ -85,13 +86,18 @@ def rope_neox(x, cos_rows, sin_rows, elem: str, round_steps: bool = True) -> np.
     return np.concatenate([first, second], axis=-1)
 
 
-def reciprocal(scale) -> np.float32:
-    """1 / scale as float32 division (correctly rounded).
+def reciprocal(scale, hw=None) -> np.float32:
+    """The reciprocal the reference multiplies by: ``v_rcp_f32(scale)`` (:282-283).
 
-    The reference multiplies by ``v_rcp_f32(scale)`` (:282-283), an
-    approximation within 1 ulp that equals this value for scales such as 0.1
-    and powers of two; the gfx950 writer computes this correctly rounded value.
+    v_rcp_f32 is a hardware approximation within 1 ulp of 1/scale whose last bit
+    no published formula fixes, so a checker passes the device's own value as
+    ``hw`` (read back through ``pa_fp8_hw_reciprocal``); its 1-ulp bound and the
+    scales where it is exact are pinned in tests/test_gpu_rope_cache.py.
+    Without ``hw`` this is 1/scale correctly rounded, which v_rcp_f32 equals at
+    powers of two and at the scales the CPU tests use (0.1 among them).
     """
+    if hw is not None:
+        return np.float32(hw)
     return np.float32(np.float32(1.0) / np.float32(scale))
 
 
@@ -129,6 +135,7 @@ def _put(cache, kind: str, layout: str, blk: int, pos: int, h: int, row):
 def fused_rope_cache(
     q, k, v, positions, cos, sin, slots, key_cache, value_cache, *,
     elem: str, layout: str, block_size: int, fmt: str = "elem", k_scale=None, v_scale=None,
+    k_rcp=None, v_rcp=None,
 ):
     """Restatement of one launch; returns (q_out, k_out) and writes the caches in place.
 
@@ -137,6 +144,8 @@ def fused_rope_cache(
     ``fmt``: "elem" (caches hold uint16 bit patterns), "fp8_tensor" (uint8
     codes, ``k_scale`` / ``v_scale`` scalars) or "fp8_token" (uint8 codes,
     ``k_scale`` / ``v_scale`` arrays [nb, KH, bs, 1] written at each slot).
+    ``k_rcp`` / ``v_rcp``: the device's v_rcp_f32 of the per-tensor scales
+    (``reciprocal``).
     """
     T = q.shape[0]
     positions = np.clip(np.asarray(positions, dtype=np.int64)[:T], 0, cos.shape[0] - 1)
@@ -155,8 +164,8 @@ def fused_rope_cache(
             if fmt == "elem":
                 kc, vc = elem_bits(krow, elem), elem_bits(vrow, elem)
             elif fmt == "fp8_tensor":
-                kc = e4m3_encode((krow * reciprocal(k_scale)).astype(np.float32))
-                vc = e4m3_encode((vrow * reciprocal(v_scale)).astype(np.float32))
+                kc = e4m3_encode((krow * reciprocal(k_scale, k_rcp)).astype(np.float32))
+                vc = e4m3_encode((vrow * reciprocal(v_scale, v_rcp)).astype(np.float32))
             elif fmt == "fp8_token":
                 kc, ks = pertoken_quant(krow, E4M3_MAX)
                 vc, vs = pertoken_quant(vrow, E4M3_MAX)

@@ -38,8 +38,8 @@ def declared_functions():
 def test_header_declares_the_expected_api():
     assert declared_functions() == sorted(
         ["pa_fp8_decode_partitions", "pa_fp8_decode_partitions_noalloc", "pa_fp8_lse_reduce", "pa_fp8_decode_worklist", "pa_fp8_reduce_v1",
-         "pa_fp8_metadata_v1", "pa_fp8_metadata_multi", "pa_fp8_rope_cache", "pa_fp8_status_string",
-         "pa_fp8_abi_version"]
+         "pa_fp8_metadata_v1", "pa_fp8_metadata_multi", "pa_fp8_rope_cache", "pa_fp8_hw_reciprocal",
+         "pa_fp8_status_string", "pa_fp8_abi_version"]
     )
 
 
@@ -281,3 +281,10 @@ def _rope_args(lib, **over):
 )
 def test_rope_cache_validation_codes(lib, over, status):
     assert lib.LIB.pa_fp8_rope_cache(ctypes.byref(_rope_args(lib, **over)), None) == status
+
+
+def test_hw_reciprocal_validation_codes(lib):
+    # checked before any device call; an empty range is a no-op
+    assert lib.LIB.pa_fp8_hw_reciprocal(None, None, -1, None) == 5  # PA_FP8_ERR_SHAPE
+    assert lib.LIB.pa_fp8_hw_reciprocal(None, None, 4, None) == 1  # PA_FP8_ERR_NULL_POINTER
+    assert lib.LIB.pa_fp8_hw_reciprocal(None, None, 0, None) == 0

@@ -119,16 +119,17 @@ def run_case(
 
     # oracle on the same inputs
     okc, ovc = orc.new_caches(nb, bs, KH, D, layout, fmt != "elem")
-    oks = ovs = None
+    oks = ovs = krcp = vrcp = None
     if fmt == "fp8_tensor":
         oks, ovs = np.float32(scale[0]), np.float32(scale[1])
+        krcp, vrcp = hw_reciprocal([scale[0], scale[1]])
     elif fmt == "fp8_token":
         oks, ovs = np.zeros((nb, KH, bs, 1), np.float32), np.zeros((nb, KH, bs, 1), np.float32)
     pos_np = orc.low_word(pos_t.cpu().numpy())
     slot_np = orc.low_word(slot_t.cpu().numpy())
     oq_out, ok_out = orc.fused_rope_cache(
         _np(q), _np(k), _np(v), pos_np, _np(cos), _np(sin), slot_np, okc, ovc, elem=elem, layout=layout,
-        block_size=bs, fmt=fmt, k_scale=oks, v_scale=ovs,
+        block_size=bs, fmt=fmt, k_scale=oks, v_scale=ovs, k_rcp=krcp, v_rcp=vrcp,
     )
     np.testing.assert_array_equal(_bits(q_out), orc.elem_bits(oq_out, elem), err_msg="Q_out")
     np.testing.assert_array_equal(_bits(k_out), orc.elem_bits(ok_out, elem), err_msg="K_out")
@@ -252,10 +253,45 @@ def test_fp8_cache(T, layout, QH, KH, D):
 # ---- this build's additions --------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("scale", [(0.37, 1.3), (1.0, 1.0), (3.0e-3, 7.0)])
+@pytest.mark.parametrize("scale", [(0.37, 1.3), (1.0, 1.0), (3.0e-3, 7.0), (3.0, 0.37)])
 def test_fp8_scales_where_the_approximate_reciprocal_differs(scale):
-    # v_rcp_f32 is off by one ulp at e.g. 3.0 and 0.37; the writer's reciprocal is correctly rounded
+    # the writer multiplies by v_rcp_f32(scale), as the reference does, also where it is
+    # not the correctly rounded 1/scale
     run_case(64, 128, 8, 2, layout="x5", fmt="fp8_tensor", scale=scale)
+
+
+def hw_reciprocal(xs):
+    """v_rcp_f32 of each value, computed on the device (float32 numpy array)."""
+    from flydsl_amd import _lib
+
+    x = torch.tensor(np.asarray(xs, dtype=np.float32), device=DEV)
+    y = torch.full_like(x, float("nan"))
+    _lib.hw_reciprocal(x.data_ptr(), y.data_ptr(), x.numel(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def test_hw_reciprocal_within_one_ulp():
+    # the primitive the writer's per-tensor codes rest on: within 1 ulp of 1/x over a
+    # sweep of scales, exact at powers of two, and equal to the correctly rounded
+    # quotient at the scales the CPU oracle tests use
+    rng = np.random.default_rng(7)
+    xs = np.concatenate([
+        np.exp(rng.uniform(np.log(1e-6), np.log(1e6), 200000)).astype(np.float32),
+        np.float32(2.0) ** np.arange(-40, 41, dtype=np.float32),
+        np.array([0.1, 0.05, 0.25, 3.0, 0.37, 1.3, 7.0, 3.0e-3], np.float32),
+    ])
+    got = hw_reciprocal(xs).astype(np.float64)
+    exact = 1.0 / xs.astype(np.float64)
+    crr = (np.float32(1.0) / xs).astype(np.float64)  # correctly rounded
+    ulp = np.spacing(crr.astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= ulp), "v_rcp_f32 more than 1 ulp from 1/x"
+    pow2 = slice(200000, 200000 + 81)
+    np.testing.assert_array_equal(got[pow2], crr[pow2])
+    tail = got[-8:]
+    np.testing.assert_array_equal(tail[:3], crr[-8:-5])  # 0.1, 0.05, 0.25
+    print(f"v_rcp_f32 differs from the correctly rounded 1/x on {int((got != crr).sum())} of {xs.size} "
+          f"values; at 3.0: {got[-5] != crr[-5]}, at 0.37: {got[-4] != crr[-4]}", flush=True)
 
 
 @pytest.mark.parametrize("layout", ["flash", "x4", "x5"])

@@ -214,4 +214,6 @@ def test_reciprocal_and_low_word():
         exact = 1.0 / float(s)
         for nb in (np.nextafter(r, np.float32(np.inf)), np.nextafter(r, np.float32(-np.inf))):
             assert abs(float(r) - exact) <= abs(float(nb) - exact)
+    # a device reciprocal, when given, is the one the codes use
+    assert orc.reciprocal(3.0, hw=np.float32(0.33333331)) == np.float32(0.33333331)
     np.testing.assert_array_equal(orc.low_word([5, -1, 2**32 + 7, -(2**32) + 3]), [5, -1, 7, 3])
