@@ -33,6 +33,10 @@ struct MetaParams {
 
 __device__ __forceinline__ int cdiv_u(int a, int b) { return (int)(((unsigned)a + (unsigned)b - 1u) / (unsigned)b); }
 
+// query offset of batch b: the caller's seqlens_qo_indptr, or b * query_length for
+// a null pointer (every batch decodes query_length tokens)
+__device__ __forceinline__ int sq_at(const MetaParams &p, int b) { return p.sq ? p.sq[b] : b * p.ql; }
+
 constexpr int kStagedBatches = 4096;   // batches whose qo offsets and partition counts are staged in LDS
 constexpr int kRingRows = 1024;        // work_info rows buffered in LDS before a coalesced copy-out
 constexpr int kStagedIndptr = 4097;    // work_indptr entries kept in LDS (num_cu + 1)
@@ -81,6 +85,16 @@ __device__ __forceinline__ T block_scan_excl(T v, T *s_wave, T &total) {
     return before + x - v;
 }
 
+// floor(a / b) for 0 <= a < 2^53 and b > 0: the correctly rounded double quotient
+// is within 1 of a / b there, and one integer step either way makes it exact (a
+// fraction of the cost of the 64-bit integer division routine)
+__device__ __forceinline__ long long floor_div_ll(long long a, long long b) {
+    long long q = (long long)((double)a / (double)b);
+    if (q * b > a) --q;
+    else if ((q + 1) * b <= a) ++q;
+    return q;
+}
+
 // Weighted quotas apply when every bin keeps at least one partition: S >= 4 nspk
 // and S * (least weight) >= 2 * Wt (a bin's quota is at least S w / Wt - 1), and a
 // head has at most kParBins bins.  wt gets Wt.
@@ -107,7 +121,7 @@ __device__ __forceinline__ void fill_weighted_starts(const MetaParams &p, long l
     for (int c = threadIdx.x; c <= nspk; c += blockDim.x) {
         long long wc = 0;
         for (int g = 0; g < ng; ++g) wc += p.bin_weight[g] * (long long)min(max(c - g * gm, 0), gm);
-        s_Q[c] = (int)(S64 * wc / wt);
+        s_Q[c] = (int)floor_div_ll(S64 * wc, wt);  // S < 2^31, wc <= Wt < 2^22
     }
 }
 
@@ -245,7 +259,7 @@ __device__ bool pack_schedule(const MetaParams &p, const int S, const int32_t *s
     // the largest sequence fits no bin (the rule fails at rank 0), or a quota too
     // large for the 31-bit rank keys below
     if (Pmax > Qmax || Qmax >= (1 << 19)) return give_up();
-    for (int b = t; b <= nb; b += kParThreads) s_sq[b] = p.sq[b];  // read before the writes' barriers
+    for (int b = t; b <= nb; b += kParThreads) s_sq[b] = sq_at(p, b);  // read before the writes' barriers
     // ranks: batch b goes before b' when P_b > P_b', or equal and b < b' (bins alike
     // by quota), i.e. when its key v << 12 | (4095 - index) is larger (values <
     // 2^19, indices < 4096).  Batches are ranked by the first half of the threads,
@@ -489,7 +503,6 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
     int32_t *s_G = s_L + kParBatches + 4;      // split batches before batch b
     int32_t *s_F = s_G + kParBatches + 4;      // first bin of batch b
     __shared__ long long s_w64[2 * (kParThreads / 64)];
-    __shared__ int32_t s_w32[kParThreads / 64];
     __shared__ int32_t s_mm[2 * (kParThreads / 64)];
     __shared__ int32_t s_pk[2 * (kParThreads / 64)];
     __shared__ int32_t s_flag[1];
@@ -568,11 +581,11 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
             lo = min(lo, s_pk[2 * w]);
             hi = max(hi, s_pk[2 * w + 1]);
         }
-        long long wt = 0, bound = (S64 + nspk - 1) / nspk;
+        long long wt = 0, bound = floor_div_ll(S64 + nspk - 1, nspk);
         if (weighted_quotas(p, S64, nspk, wt)) {
             long long wmax = 0;
             for (int g = 0; g < p.bin_groups; ++g) wmax = max(wmax, (long long)p.bin_weight[g]);
-            bound = S64 * wmax / wt + 1;
+            bound = floor_div_ll(S64 * wmax, wt) + 1;
         }
         if (lo >= 0 && hi <= bound) {
             long long r = run;
@@ -645,10 +658,9 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
         ll += l4[i];
         gl += g4[i];
     }
-    int W, Lt, G;
-    int wr = block_scan_excl<int>(wl, s_w32, W);
-    int lr = block_scan_excl<int>(ll, s_w32, Lt);
-    int gr = block_scan_excl<int>(gl, s_w32, G);
+    int W, Lt, G, zr, zt;
+    int wr, lr, gr;
+    scan_quad(wl, ll, gl, 0, s_w64, wr, lr, gr, zr, W, Lt, G, zt);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int b = 4 * t + i;
@@ -676,7 +688,7 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
         const int pb = s_P[b], pe = s_P[b + 1];
         const int c0 = s_F[b], nw = works_of(b);
         const int wb = s_W[b], lb = s_L[b];
-        const int qs = p.sq[b], qe = p.sq[b + 1];
+        const int qs = sq_at(p, b), qe = sq_at(p, b + 1);
         for (int j = 0; j < nw; ++j) {
             const int c = c0 + j;
             const int ks = pe > pb ? max(pb, Qs(c)) : pb;
@@ -713,8 +725,8 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
         if (nw < 2) continue;
         const int g = s_G[b], lb = s_L[b];
         p.reduce_indptr[g + 1] = lb + nw;
-        p.reduce_final_map[2 * g] = p.sq[b];
-        p.reduce_final_map[2 * g + 1] = p.sq[b + 1];
+        p.reduce_final_map[2 * g] = sq_at(p, b);
+        p.reduce_final_map[2 * g + 1] = sq_at(p, b + 1);
         for (int j = 0; j < nw; ++j)
             if (lb + j < p.max_split_tiles) p.reduce_partial_map[lb + j] = p.ql * (lb + j);
     }
@@ -755,7 +767,7 @@ __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaSchedules 
         part += n;
         if (b < staged) s_np[b] = n;
     }
-    for (int b = lane; b <= staged; b += 64) s_sq[b] = p.sq[b];
+    for (int b = lane; b <= staged; b += 64) s_sq[b] = sq_at(p, b);
 #pragma unroll
     for (int sh = 32; sh >= 1; sh >>= 1) part += __shfl_xor(part, sh, 64);
     __syncthreads();
@@ -765,7 +777,7 @@ __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaSchedules 
     const int reminder = (int)(sum_blocks % nspk);
     auto quota = [&](int c) { return average + ((c % nspk) < reminder ? 1 : 0); };
     auto npart = [&](int b) { return b < staged ? s_np[b] : cdiv_u(p.ctx[b], p.kv_gran); };
-    auto sq = [&](int b) { return b <= staged ? s_sq[b] : p.sq[b]; };
+    auto sq = [&](int b) { return b <= staged ? s_sq[b] : sq_at(p, b); };
     auto put_wi = [&](int i, int v) {
         if (wi_lds) { if (lead) s_wi[i] = v; }
         else if (lead) p.work_indptr[i] = v;
@@ -938,7 +950,9 @@ int meta_params(const pa_fp8_metadata_args *a, MetaParams &p) {
     // pointer): one bin per kv head leaves reduce_partial_map empty, and every
     // write to work_info, reduce_final_map and reduce_partial_map is bounded by
     // max_work, num_batches and max_split_tiles
-    if (!a->seqlens_qo_indptr || !a->context_lens || !a->work_indptr || !a->reduce_indptr ||
+    // a NULL seqlens_qo_indptr stands for b * query_length
+    if (!a->seqlens_qo_indptr && (int64_t)a->num_batches * a->query_length > 0x7fffffffLL) return PA_FP8_ERR_SHAPE;
+    if (!a->context_lens || !a->work_indptr || !a->reduce_indptr ||
         (!a->work_info && a->max_work > 0) || (!a->reduce_final_map && a->num_batches > 0) ||
         (!a->reduce_partial_map && a->max_split_tiles > 0))
         return PA_FP8_ERR_NULL_POINTER;

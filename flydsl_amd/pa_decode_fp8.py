@@ -794,25 +794,6 @@ def _build_plan_checked(
                              exp_sums, max_logits, temporary_output, is_graph_capturing, path, tag)
 
 
-_SEQLENS_CACHE: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
-
-
-def _seqlens_qo_indptr(dev: torch.device, batch_size: int, query_length: int, graph_safe: bool) -> torch.Tensor:
-    """arange(B + 1) * ql on the device, cached per shape outside graph capture.  A
-    graph-safe call makes its own tensor: a captured graph must not hold a cached
-    one that a later eviction frees."""
-    if graph_safe:
-        return torch.arange(batch_size + 1, dtype=torch.int32, device=dev) * query_length
-    key = (dev, batch_size, query_length)
-    t = _SEQLENS_CACHE.get(key)
-    if t is None:
-        t = torch.arange(batch_size + 1, dtype=torch.int32, device=dev) * query_length
-        _SEQLENS_CACHE[key] = t
-        if len(_SEQLENS_CACHE) > 32:
-            _SEQLENS_CACHE.popitem(last=False)
-    return t
-
-
 def _schedule_layout(batch_size: int, num_kv_heads: int, num_sm: int) -> list:
     """int32 element counts of one schedule's buffers: work_indptr, work_info (flat),
     reduce_indptr, reduce_final_map (flat), reduce_partial_map."""
@@ -820,10 +801,10 @@ def _schedule_layout(batch_size: int, num_kv_heads: int, num_sm: int) -> list:
     return [int(torch.Size(shape).numel()) for shape, _ in infos[1:]]
 
 
-def _schedule_args(a, bufs, seqlens_qo_indptr, ctx, batch_size, gqa, num_kv_heads, num_sm, partition_size,
+def _schedule_args(a, bufs, ctx, batch_size, gqa, num_kv_heads, num_sm, partition_size,
                    query_length, bin_groups, partial_count):
     work_indptr, work_info, reduce_indptr, reduce_final_map, reduce_partial_map = bufs
-    a.seqlens_qo_indptr = seqlens_qo_indptr.data_ptr()
+    a.seqlens_qo_indptr = None  # the scheduler's b * query_length: no offsets tensor to build
     a.context_lens = ctx.data_ptr()
     a.work_indptr = work_indptr.data_ptr()
     a.work_info = work_info.data_ptr()
@@ -906,7 +887,6 @@ def get_pa_metadata(
             tuned = False
         else:
             schedules.append((t_sm, t_groups))
-    seqlens_qo_indptr = _seqlens_qo_indptr(dev, batch_size, query_length, graph_safe)
     ctx = context_lengths if context_lengths.dtype == torch.int32 else context_lengths.to(torch.int32)
     ctx = ctx.contiguous()
     # Every int32 output in one allocation: four counters first (the reference
@@ -927,7 +907,7 @@ def get_pa_metadata(
     sched_bufs = []
     for k, (s_sm, s_groups) in enumerate(schedules):
         bufs = piece[1 + 5 * k: 6 + 5 * k]
-        _schedule_args(args[k], bufs, seqlens_qo_indptr, ctx, batch_size, gqa, num_kv_heads, s_sm, partition_size,
+        _schedule_args(args[k], bufs, ctx, batch_size, gqa, num_kv_heads, s_sm, partition_size,
                        query_length, s_groups, counts[2 * k: 2 * k + 1])
         sched_bufs.append(bufs)
     if tuned:

@@ -312,7 +312,7 @@ int pa_fp8_reduce_v1(const pa_fp8_reduce_v1_args *args, void *hip_stream);
  * called from get_pa_metadata_v1 at :515-524).
  */
 typedef struct pa_fp8_metadata_args {
-    const int32_t *seqlens_qo_indptr;
+    const int32_t *seqlens_qo_indptr;  /* [B+1]; NULL: b * query_length (a decode step) */
     const int32_t *context_lens;
     int32_t *work_indptr;
     int32_t *work_info;

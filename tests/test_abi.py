@@ -190,6 +190,21 @@ def test_metadata_accepts_null_for_empty_buffers(lib):
     assert lib.LIB.pa_fp8_metadata_v1(ctypes.byref(m), None) == 1
 
 
+def test_metadata_null_query_offsets_mean_uniform_query_length(lib):
+    """A NULL seqlens_qo_indptr stands for b * query_length (what get_pa_metadata
+    passes); it is refused with a shape error when that would overflow int32."""
+    m = lib.MetadataArgs()
+    m.num_batches, m.gqa, m.num_heads_k, m.num_cu, m.kv_granularity, m.query_length = 3, 4, 1, 2, 256, 4
+    buf = (ctypes.c_int32 * 64)()
+    for name in ("context_lens", "work_indptr", "work_info", "reduce_indptr", "reduce_final_map", "reduce_partial_map"):
+        setattr(m, name, ctypes.cast(buf, ctypes.c_void_p).value)
+    m.seqlens_qo_indptr = None
+    m.max_work, m.max_split_tiles = 4, 2
+    assert lib.LIB.pa_fp8_metadata_v1(ctypes.byref(m), None) not in (1, 5)
+    m.num_batches, m.query_length = 1 << 20, 4096
+    assert lib.LIB.pa_fp8_metadata_v1(ctypes.byref(m), None) == 5
+
+
 def _worklist_args(lib, **over):
     a = lib.WorklistArgs()
     a.batch_size, a.num_kv_heads, a.query_group_size, a.query_length = 0, 1, 8, 1
