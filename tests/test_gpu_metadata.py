@@ -130,9 +130,10 @@ def test_device_scheduler_random_wide(seed):
         np.testing.assert_array_equal(op.metadata_valid_prefixes(got)[key], val, err_msg=key)
 
 
-def run_device_schedule(ctx, ql, gqa, nhk, nspk, gran, weights, pack):
+def run_device_schedule(ctx, ql, gqa, nhk, nspk, gran, weights, pack, null_sq=False):
     """One schedule from the device scheduler through the C ABI, with this build's
-    options (bin_groups / bin_weight, pack) set directly; buffers pre-filled with -7."""
+    options (bin_groups / bin_weight, pack) set directly; buffers pre-filled with -7.
+    ``null_sq`` passes a NULL seqlens_qo_indptr (the scheduler's b * query_length)."""
     from flydsl_amd import _lib, get_pa_metadata_info_v1
 
     dev = torch.device("cuda:0")
@@ -145,7 +146,7 @@ def run_device_schedule(ctx, ql, gqa, nhk, nspk, gran, weights, pack):
     ctx_t = torch.tensor(ctx, dtype=torch.int32, device=dev)
     count = torch.full((1,), -7, dtype=torch.int32, device=dev)
     a = (_lib.MetadataArgs * 1)()
-    a[0].seqlens_qo_indptr, a[0].context_lens = sq.data_ptr(), ctx_t.data_ptr()
+    a[0].seqlens_qo_indptr, a[0].context_lens = (None if null_sq else sq.data_ptr()), ctx_t.data_ptr()
     a[0].work_indptr, a[0].work_info, a[0].reduce_indptr = wi.data_ptr(), winfo.data_ptr(), ri.data_ptr()
     a[0].reduce_final_map, a[0].reduce_partial_map = rfm.data_ptr(), rpm.data_ptr()
     a[0].partial_count = count.data_ptr()
@@ -162,6 +163,43 @@ def run_device_schedule(ctx, ql, gqa, nhk, nspk, gran, weights, pack):
            "reduce_indptr": ri.cpu().numpy(), "reduce_final_map": rfm.cpu().numpy(),
            "reduce_partial_map": rpm.cpu().numpy()}
     return got, int(count.item())
+
+
+@pytest.mark.parametrize(
+    "case",
+    ["closed_form", "few_partitions", "all_empty", "serial_batches", "weighted", "packed"],
+)
+def test_device_scheduler_null_query_offsets(case):
+    """A NULL seqlens_qo_indptr (what get_pa_metadata passes) gives the schedule of the
+    offsets b * query_length on the closed-form, serial, weighted and packing paths,
+    bit-exact with the oracle."""
+    rng = np.random.default_rng(sum(map(ord, case)) + 11)
+    ql, gqa, gran, weights, pack = 3, 4, 256, None, False
+    if case == "closed_form":
+        ctx, nhk, nspk = [int(x) for x in rng.integers(0, 4000, size=70)], 4, 16
+    elif case == "few_partitions":
+        ctx, nhk, nspk = [int(x) for x in rng.integers(1, 300, size=5)], 2, 32
+    elif case == "all_empty":
+        ctx, nhk, nspk = [0] * 9, 4, 8
+    elif case == "serial_batches":
+        ctx, nhk, nspk = [int(x) for x in rng.integers(0, 2000, size=4097)], 8, 64
+    elif case == "weighted":
+        ctx, nhk, nspk, weights = [int(x) for x in rng.integers(500, 9000, size=90)], 2, 24, [130, 114, 100]
+    else:
+        ctx, nhk, nspk, weights, pack = [int(x) for x in rng.integers(4096, 8193, size=64)], 4, 48, [115, 107, 100], True
+    got, _ = run_device_schedule(ctx, ql, gqa, nhk, nspk, gran, weights, pack, null_sq=True)
+    want, _ = run_device_schedule(ctx, ql, gqa, nhk, nspk, gran, weights, pack)
+    for key in got:
+        np.testing.assert_array_equal(got[key], want[key], err_msg=key)
+    sq = [ql * i for i in range(len(ctx) + 1)]
+    qf = weighted_quota(weights, nspk) if weights else None
+    ref = op.get_pa_metadata_packed(sq, ctx, gqa, nhk, nhk * nspk, gran, ql, quota_of=qf) if pack else None
+    assert (ref is not None) == pack  # the packed case packs
+    if ref is None:
+        ref = op.get_pa_metadata_v1(sq, ctx, gqa, nhk, nhk * nspk, gran, ql, quota_of=qf)
+    got["num_reduce_groups"] = ref["num_reduce_groups"]
+    for key, val in op.metadata_valid_prefixes(ref).items():
+        np.testing.assert_array_equal(op.metadata_valid_prefixes(got)[key], val, err_msg=key)
 
 
 @pytest.mark.parametrize("seed", range(60))
