@@ -786,11 +786,16 @@ __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaSchedules 
         if (red_lds) { if (lead) s_ri[i] = v; }
         else if (lead) p.reduce_indptr[i] = v;
     };
+    // entries [0, rfm_top) / [0, rpm_top) of the LDS reduce maps hold written values (the
+    // copy-out leaves the caller's buffer alone past them, as the direct writes do)
+    int rfm_top = 0, rpm_top = 0;
     auto put_rfm = [&](int g, int a, int b) {
+        rfm_top = max(rfm_top, g + 1);
         if (red_lds) { if (lead) { s_rfm[2 * g] = a; s_rfm[2 * g + 1] = b; } }
         else if (lead) { p.reduce_final_map[2 * g] = a; p.reduce_final_map[2 * g + 1] = b; }
     };
     auto put_rpm = [&](int i, int v) {
+        rpm_top = max(rpm_top, i + 1);
         if (rpm_lds) { if (lead) s_rpm[i] = v; }
         else if (lead) p.reduce_partial_map[i] = v;
     };
@@ -812,6 +817,7 @@ __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaSchedules 
     put_wi(0, 0);
     put_ri(0, 0);
     int cid = 0, num_works = 0, lri = 0, grt = 0;
+    int last_slot = -1;  // the ring slot written last (the current work's, emitted or not)
     // one kv head of the state machine (kernels/pa_metadata.py:212-387), from the current cid
     auto run_head = [&](int kh) {
         const int32_t qhr =
@@ -838,6 +844,7 @@ __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaSchedules 
                     w[0] = make_int4(batch, w_ploc, qo_start, qo_end);
                     w[1] = make_int4(kv_start, w_kv_end, 0, qhr);
                 }
+                last_slot = num_works;
             } else {
                 overflow = true;
             }
@@ -921,18 +928,21 @@ __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaSchedules 
     }
     for (int i = cid; i <= p.num_cu; ++i) put_wi(i, num_works);
     for (int i = grt; i <= p.nb; ++i) put_ri(i, lri);
-    // The ring still holds rows [flushed, num_works]; the last slot written (num_works) is
-    // copied too, as the reference leaves it in the buffer.  After a replication the ring
-    // holds head 0's W rows only (its slot W would overwrite head 1's first row).
-    flush(replicated ? W : min(num_works + 1, flushed + kRingRows));
+    // The ring still holds rows [flushed, num_works); slot num_works is copied too when
+    // the last iteration wrote it without emitting it, as the reference leaves that row in
+    // the buffer (a slot no iteration wrote holds stale LDS and stays out).  After a
+    // replication the ring holds head 0's W rows only (its slot W would overwrite head
+    // 1's first row).
+    const int tail = last_slot == num_works ? num_works + 1 : num_works;
+    flush(replicated ? W : min(tail, flushed + kRingRows));
     if (wi_lds)
         for (int i = lane; i <= p.num_cu; i += 64) p.work_indptr[i] = s_wi[i];
     if (red_lds) {
         for (int i = lane; i <= p.nb; i += 64) p.reduce_indptr[i] = s_ri[i];
-        for (int i = lane; i < 2 * min(grt + 1, p.nb); i += 64) p.reduce_final_map[i] = s_rfm[i];
+        for (int i = lane; i < 2 * rfm_top; i += 64) p.reduce_final_map[i] = s_rfm[i];
     }
     if (rpm_lds)
-        for (int i = lane; i < min(lri + 1, p.max_split_tiles); i += 64) p.reduce_partial_map[i] = s_rpm[i];
+        for (int i = lane; i < rpm_top; i += 64) p.reduce_partial_map[i] = s_rpm[i];
     __syncthreads();
     if (lead && p.partial_count) p.partial_count[0] = lri;
     if (lead && overflow) p.work_indptr[0] = -1;
