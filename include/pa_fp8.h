@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define PA_FP8_ABI_VERSION 8
+#define PA_FP8_ABI_VERSION 9
 
 enum pa_fp8_status {
     PA_FP8_OK = 0,
