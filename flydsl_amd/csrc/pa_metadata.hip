@@ -97,10 +97,13 @@ __device__ __forceinline__ long long floor_div_ll(long long a, long long b) {
 
 // Weighted quotas apply when every bin keeps at least one partition: S >= 4 nspk
 // and S * (least weight) >= 2 * Wt (a bin's quota is at least S w / Wt - 1), and a
-// head has at most kParBins bins.  wt gets Wt.
-__device__ __forceinline__ bool weighted_quotas(const MetaParams &p, long long S64, int nspk, long long &wt) {
+// head has at most kParBins bins, and the context lengths are not all equal (equal
+// sequences fill equal bins whole, which the weights would break into split
+// pieces).  wt gets Wt.
+__device__ __forceinline__ bool weighted_quotas(const MetaParams &p, long long S64, int nspk, bool equal_ctx,
+                                                long long &wt) {
     const int ng = p.bin_groups;
-    bool weighted = ng > 1 && ng <= 4 && nspk % ng == 0 && S64 >= 4LL * nspk && nspk <= kParBins;
+    bool weighted = !equal_ctx && ng > 1 && ng <= 4 && nspk % ng == 0 && S64 >= 4LL * nspk && nspk <= kParBins;
     long long wmin = 1000;
     wt = 0;
     if (weighted) {
@@ -197,7 +200,8 @@ __device__ __forceinline__ void scan_quad(int a, int b, int c, int d, long long 
 // Ranks are counted directly (the lanes of an element compare it with every
 // other one, read as LDS broadcasts), which for the batch sizes of a decode step
 // is several times quicker than a barrier-per-stage sort.
-__device__ bool pack_schedule(const MetaParams &p, const int S, const int32_t *s_P, int32_t *s_Qs, int32_t *u,
+__device__ bool pack_schedule(const MetaParams &p, const int S, const bool equal_ctx, const int32_t *s_P,
+                              int32_t *s_Qs, int32_t *u,
                               long long *s_w64, int32_t *s_red, int32_t *s_flag) {
     int32_t *s_Pv = u;                            // partitions of batch b (padded to 16-value rounds)
     int32_t *s_sq = s_Pv + kPackBatches + 16;     // query rows before batch b
@@ -231,7 +235,7 @@ __device__ bool pack_schedule(const MetaParams &p, const int S, const int32_t *s
     if (t == 0) s_flag[0] = 0;
     const long long S64 = S;
     long long wt = 0;
-    const bool weighted = weighted_quotas(p, S64, nspk, wt);
+    const bool weighted = weighted_quotas(p, S64, nspk, equal_ctx, wt);
     if (weighted) fill_weighted_starts(p, S64, nspk, wt, s_Qs);
     else
         for (int c = t; c <= nspk; c += kParThreads)
@@ -540,7 +544,9 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
         S64 += total;
     }
     if (p.partition_indptr && t == 0) p.partition_indptr[p.nb] = (int)S64;
-    if (p.uniform_context) {
+    // every context length equal: the uniform_context output, and no weighted quotas
+    bool equal_ctx = false;
+    if (p.uniform_context || p.bin_groups > 1) {
 #pragma unroll
         for (int sh = 32; sh >= 1; sh >>= 1) {
             cmin = min(cmin, __shfl_xor(cmin, sh, 64));
@@ -551,14 +557,13 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
             s_mm[2 * (t >> 6) + 1] = cmax;
         }
         __syncthreads();
-        if (t == 0) {
-            int a = INT32_MAX, z = INT32_MIN;
-            for (int w = 0; w < kParThreads / 64; ++w) {
-                a = min(a, s_mm[2 * w]);
-                z = max(z, s_mm[2 * w + 1]);
-            }
-            p.uniform_context[0] = (p.nb == 0 || a == z) ? 1 : 0;
+        int a = INT32_MAX, z = INT32_MIN;
+        for (int w = 0; w < kParThreads / 64; ++w) {
+            a = min(a, s_mm[2 * w]);
+            z = max(z, s_mm[2 * w + 1]);
         }
+        equal_ctx = p.nb == 0 || a == z;
+        if (t == 0 && p.uniform_context) p.uniform_context[0] = equal_ctx ? 1 : 0;
     }
     // the packing schedule, where it applies, instead of the sequential fill
     if (p.pack && p.nb >= 1 && p.nb <= kPackBatches && nspk <= kPackBins && S64 >= 1 && S64 <= 0x7fffffffLL) {
@@ -582,7 +587,7 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
             hi = max(hi, s_pk[2 * w + 1]);
         }
         long long wt = 0, bound = floor_div_ll(S64 + nspk - 1, nspk);
-        if (weighted_quotas(p, S64, nspk, wt)) {
+        if (weighted_quotas(p, S64, nspk, equal_ctx, wt)) {
             long long wmax = 0;
             for (int g = 0; g < p.bin_groups; ++g) wmax = max(wmax, (long long)p.bin_weight[g]);
             bound = floor_div_ll(S64 * wmax, wt) + 1;
@@ -597,7 +602,7 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
             }
             if (t == 0) s_P[p.nb] = (int)S64;
             __syncthreads();
-            if (pack_schedule(p, (int)S64, s_P, s_Q, s_u, s_w64, s_mm, s_flag)) return;
+            if (pack_schedule(p, (int)S64, equal_ctx, s_P, s_Q, s_u, s_w64, s_mm, s_flag)) return;
             __syncthreads();  // s_mm, s_Q and the shared region are free again
         }
     }
@@ -619,7 +624,7 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
     const int avg = S / nspk, rem = S % nspk;
     const int big = rem * (avg + 1);
     long long wt = 0;
-    const bool weighted = weighted_quotas(p, S64, nspk, wt);
+    const bool weighted = weighted_quotas(p, S64, nspk, equal_ctx, wt);
     // The first partition of every bin, Qs(c) = floor(S * Wc(c) / Wt), tabulated once
     // in LDS (bins are then found by a binary search over the table).
     if (weighted) {

@@ -303,7 +303,9 @@ int pa_fp8_reduce_v1(const pa_fp8_reduce_v1_args *args, void *hip_stream);
  * scheduler splits the partitions in proportion to bin_weight[g] (1..1000) of
  * each bin's group instead of evenly, when every bin still gets a partition
  * (sum of partitions S >= 4 * bins per head, S * least weight >= 2 * Wt with Wt
- * the sum of every bin's weight, at most 4096 bins per head).  Workgroups that share a CU progress
+ * the sum of every bin's weight, at most 4096 bins per head) and the context
+ * lengths are not all equal (equal sequences fill equal bins whole; weights would
+ * split them).  Workgroups that share a CU progress
  * at different rates (issue arbitration favours the one dispatched first), and
  * pa_fp8_decode_worklist with the same bin_groups runs group a on the
  * workgroups of dispatch round a.

@@ -10,11 +10,15 @@ from oracle import planners as op
 pytestmark = pytest.mark.gpu
 
 
-def weighted_quota(weights, nspk):
+def weighted_quota(weights, nspk, ctx):
     """get_pa_metadata's weighted split as a per-bin quota for the oracle's state
     machine: a head's bins form len(weights) equal groups and bin i starts at
     floor(S * Wc(i) / Wt), Wc(i) the weights of the bins before it, when
-    nspk % groups == 0 and S >= 4 * nspk; otherwise the reference's even quota."""
+    nspk % groups == 0 and S >= 4 * nspk; otherwise the reference's even quota.
+    Context lengths that are all equal take the even quota too (equal sequences
+    fill equal bins whole): None then."""
+    if len(set(ctx)) <= 1:
+        return None
     ng = len(weights)
     m = nspk // ng
 
@@ -34,7 +38,7 @@ def expected_schedule(md, sq, ctx, gqa, nhk, gran=256, ql=1):
     """The oracle's schedule for one schedule of a get_pa_metadata result: the
     reference's even one, or the tuned one (it carries bin_groups) with its
     weights -- the packing schedule where that applies, else the sequential fill."""
-    qf = weighted_quota(md["bin_weight"], md["num_sm"] // nhk) if md.get("bin_groups", 0) > 1 else None
+    qf = weighted_quota(md["bin_weight"], md["num_sm"] // nhk, ctx) if md.get("bin_groups", 0) > 1 else None
     if "bin_groups" in md:
         packed = op.get_pa_metadata_packed(sq, ctx, gqa, nhk, md["num_sm"], gran, ql, quota_of=qf)
         if packed is not None:
@@ -192,7 +196,7 @@ def test_device_scheduler_null_query_offsets(case):
     for key in got:
         np.testing.assert_array_equal(got[key], want[key], err_msg=key)
     sq = [ql * i for i in range(len(ctx) + 1)]
-    qf = weighted_quota(weights, nspk) if weights else None
+    qf = weighted_quota(weights, nspk, ctx) if weights else None
     ref = op.get_pa_metadata_packed(sq, ctx, gqa, nhk, nhk * nspk, gran, ql, quota_of=qf) if pack else None
     assert (ref is not None) == pack  # the packed case packs
     if ref is None:
@@ -214,7 +218,7 @@ def test_device_packing_schedule_matches_oracle(seed):
     nhk, nspk, b, ctx, weights = _packed_case(rng)
     ql, gqa = int(rng.integers(1, 5)), int(rng.choice([1, 4, 16]))
     sq = [i * ql for i in range(b + 1)]
-    qf = weighted_quota(weights, nspk) if weights else None
+    qf = weighted_quota(weights, nspk, ctx) if weights else None
     ref = op.get_pa_metadata_packed(sq, ctx, gqa, nhk, nhk * nspk, 256, ql, quota_of=qf)
     if ref is None:
         ref = op.get_pa_metadata_v1(sq, ctx, gqa, nhk, nhk * nspk, 256, ql, quota_of=qf)
@@ -275,6 +279,24 @@ def test_get_pa_metadata_c3_tuned_schedule():
     v = assert_schedule_equal(t, expected_schedule(t, list(range(129)), ctx, 4, 8), "c3 tuned")
     npart = int(v["reduce_indptr"][-1])
     assert t["partial_output"].shape == ((npart + 1) * 1, 1, 32, 128)
+
+
+def test_get_pa_metadata_equal_contexts_take_even_quotas():
+    """Equal context lengths (c2) keep the tuned schedule's quotas even: the 64
+    sequences of 16 partitions fill the 64 bins of each kv head whole, so nothing
+    is split and nothing is merged, bit-exact with the oracle's packing schedule
+    under even quotas."""
+    md, ctx, b, ql, hq, hk = _metadata_for("c2")
+    t = md["tuned"]
+    assert len(set(ctx)) == 1 and t["bin_groups"] == 2  # weights requested, not applied
+    sq = [ql * i for i in range(b + 1)]
+    ref = op.get_pa_metadata_packed(sq, ctx, hq // hk, hk, t["num_sm"], 256, ql)
+    assert ref is not None
+    v = assert_schedule_equal(t, ref, "c2 tuned")
+    if t["num_sm"] // hk == b:  # one bin per sequence and head
+        assert int(v["reduce_indptr"][-1]) == 0
+        info = v["work_info"]
+        assert (info[:, 1] == -1).all() and len(info) == b * hk
 
 
 def test_get_pa_metadata_c5_shape_weighted_quotas():
