@@ -128,32 +128,44 @@ __device__ __forceinline__ void fill_weighted_starts(const MetaParams &p, long l
     }
 }
 
-// Two non-negative ints per thread scanned at once (packed into one 64-bit value;
-// every total here is below 2^31, so the low half never carries): exclusive
-// prefixes of (a0 + a1) and (b0 + b1) over the workgroup, and their totals.
-__device__ __forceinline__ void scan_pair(int a, int b, long long *s_w64, int &pa, int &pb, int &ta, int &tb) {
-    long long tot;
-    const long long x = block_scan_excl<long long>((long long)a + ((long long)b << 32), s_w64, tot);
-    pa = (int)(x & 0xffffffffLL);
-    pb = (int)(x >> 32);
-    ta = (int)(tot & 0xffffffffLL);
-    tb = (int)(tot >> 32);
+// Inclusive prefix sum of x over the 64 lanes of a wave by DPP: row shifts by 1, 2,
+// 4 and 8 inside each row of 16 lanes, then the broadcasts of lane 15 into rows 1
+// and 3 and of lane 31 into rows 2 and 3 (row_bcast, GFX9 family).  Six VALU adds
+// instead of six dependent cross-lane LDS round trips.
+__device__ __forceinline__ int wave_scan_incl(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return x;
 }
 
-// Four such values per thread in one pass (two 64-bit lanes scanned together).
+// The largest (MAX) or smallest x of a wave, in every lane: the same DPP steps with
+// the operation's identity for lanes without a source, then lane 63 read out.
+template <bool MAX>
+__device__ __forceinline__ int wave_extreme(int x) {
+    const int id = MAX ? INT32_MIN : INT32_MAX;
+    auto op = [](int u, int v) { return MAX ? max(u, v) : min(u, v); };
+    x = op(x, __builtin_amdgcn_update_dpp(id, x, 0x111, 0xf, 0xf, false));
+    x = op(x, __builtin_amdgcn_update_dpp(id, x, 0x112, 0xf, 0xf, false));
+    x = op(x, __builtin_amdgcn_update_dpp(id, x, 0x114, 0xf, 0xf, false));
+    x = op(x, __builtin_amdgcn_update_dpp(id, x, 0x118, 0xf, 0xf, false));
+    x = op(x, __builtin_amdgcn_update_dpp(id, x, 0x142, 0xa, 0xf, false));
+    x = op(x, __builtin_amdgcn_update_dpp(id, x, 0x143, 0xc, 0xf, false));
+    return __builtin_amdgcn_readlane(x, 63);
+}
+
+// Four non-negative ints per thread scanned over the workgroup in one pass: exclusive
+// prefixes and totals of a, b, c and d.  Every total here is below 2^31, so each
+// pair of wave totals shares one 64-bit LDS word (the low half never carries).
 __device__ __forceinline__ void scan_quad(int a, int b, int c, int d, long long *s_w64, int &pa, int &pb, int &pc,
                                           int &pd, int &ta, int &tb, int &tc, int &td) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    long long x = (long long)a + ((long long)b << 32), y = (long long)c + ((long long)d << 32);
-    const long long x_in = x, y_in = y;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const long long ux = __shfl_up(x, o, 64), uy = __shfl_up(y, o, 64);
-        if (lane >= o) {
-            x += ux;
-            y += uy;
-        }
-    }
+    long long x = (long long)wave_scan_incl(a) + ((long long)wave_scan_incl(b) << 32);
+    long long y = (long long)wave_scan_incl(c) + ((long long)wave_scan_incl(d) << 32);
+    const long long x_in = (long long)a + ((long long)b << 32), y_in = (long long)c + ((long long)d << 32);
     if (lane == 63) {
         s_w64[2 * wave] = x;
         s_w64[2 * wave + 1] = y;
@@ -229,8 +241,7 @@ __device__ bool pack_schedule(const MetaParams &p, const int S, const bool equal
         s_Pv[b] = v;
         pmax = max(pmax, v);
     }
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) pmax = max(pmax, __shfl_xor(pmax, sh, 64));
+    pmax = wave_extreme<true>(pmax);
     if (lane == 0) s_red[wv] = pmax;
     if (t == 0) s_flag[0] = 0;
     const long long S64 = S;
@@ -246,8 +257,7 @@ __device__ bool pack_schedule(const MetaParams &p, const int S, const bool equal
         s_Qv[c] = s_Qs[c + 1] - s_Qs[c];
         qmax = max(qmax, s_Qv[c]);
     }
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) qmax = max(qmax, __shfl_xor(qmax, sh, 64));
+    qmax = wave_extreme<true>(qmax);
     if (lane == 0) s_red[kParThreads / 64 + wv] = qmax;
     if (t < 16) {  // padding past the last batch and bin: never counted (real values are >= 0)
         s_Pv[nb + t] = -1;
@@ -547,11 +557,8 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
     // every context length equal: the uniform_context output, and no weighted quotas
     bool equal_ctx = false;
     if (p.uniform_context || p.bin_groups > 1) {
-#pragma unroll
-        for (int sh = 32; sh >= 1; sh >>= 1) {
-            cmin = min(cmin, __shfl_xor(cmin, sh, 64));
-            cmax = max(cmax, __shfl_xor(cmax, sh, 64));
-        }
+        cmin = wave_extreme<false>(cmin);
+        cmax = wave_extreme<true>(cmax);
         if ((t & 63) == 0) {
             s_mm[2 * (t >> 6)] = cmin;
             s_mm[2 * (t >> 6) + 1] = cmax;
@@ -572,11 +579,8 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
         // up, or S w_max / Wt + 1 with weights), checked before any packing work;
         // s_pk is touched by nothing else, so a rejection needs no further barrier
         int lo = cmin, hi = max(max(np4[0], np4[1]), max(np4[2], np4[3]));
-#pragma unroll
-        for (int sh = 32; sh >= 1; sh >>= 1) {
-            lo = min(lo, __shfl_xor(lo, sh, 64));
-            hi = max(hi, __shfl_xor(hi, sh, 64));
-        }
+        lo = wave_extreme<false>(lo);
+        hi = wave_extreme<true>(hi);
         if ((t & 63) == 0) {
             s_pk[2 * (t >> 6)] = lo;
             s_pk[2 * (t >> 6) + 1] = hi;
