@@ -10,7 +10,6 @@ mapping exactly.
 
 from __future__ import annotations
 
-import math
 
 import numpy as np
 import pytest

@@ -5,7 +5,6 @@ Pinned by brute-force enumeration, invariants and a hand-worked example; the
 Python and plain-C restatements of the scheduler are cross-checked bit-exact."""
 
 import ctypes
-import math
 import subprocess
 from pathlib import Path
 
