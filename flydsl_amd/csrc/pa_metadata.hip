@@ -2,9 +2,9 @@
 //
 // The reference runs the schedule as a serial state machine over (CU bin, batch)
 // pairs.  Here a parallel kernel computes the same output in closed form for the
-// common case (pa_metadata_par_kernel) and the serial machine runs only where it
-// cannot (pa_metadata_v1_kernel); both keep the caller free of a device->host copy
-// of context_lens.  Buffers are written
+// common case (pa_metadata_par_kernel) and the serial machine runs, on one wave of
+// the same workgroup, only where it cannot (serial_schedule); one launch either way,
+// and the caller needs no device->host copy of context_lens.  Buffers are written
 // exactly where the reference writes them, including its overwrite-safe
 // unconditional stores; only the valid prefixes are defined.  Every store is
 // bounds-checked against the buffer sizes the host passes; a schedule that
@@ -47,7 +47,6 @@ constexpr int kMaxSchedules = 4;       // schedules one launch computes (one wor
 constexpr int kParThreads = 1024;
 constexpr int kParBatches = 4 * kParThreads;         // batches the parallel scheduler handles
 constexpr int kParBins = 4096;                       // bins per head the weighted quota table holds
-constexpr int32_t kSerialSentinel = INT32_MIN + 7;   // work_indptr[0]: "the serial scheduler runs"
 constexpr int kPackBatches = 2048;                   // batches the packing schedule handles
 constexpr int kPackBins = 2048;                      // bins per head the packing schedule handles
 // LDS of the packing schedule (pack_schedule's arrays)
@@ -55,6 +54,34 @@ constexpr int kPackInts = 8 * (kPackBatches + 4) + 2 * 12 + 6 * (kPackBins + 4);
 // LDS of the sequential fill's per-batch arrays (works, split works, split batches, first bin)
 constexpr int kFillInts = 4 * (kParBatches + 4);
 constexpr int kUnionInts = kPackInts > kFillInts ? kPackInts : kFillInts;
+// The closed-form kernel's LDS: partitions before each batch, bin starts, and the region
+// the sequential fill and the packing schedule share (offsets in ints, 16-byte aligned).
+constexpr int kParP = 0;
+constexpr int kParQ = kParP + kParBatches + 4;
+constexpr int kParU = kParQ + kParBins + 4;
+constexpr int kParInts = kParU + kUnionInts;
+// The serial state machine's LDS, carved from the same array when it runs instead:
+// partition counts, query offsets, the work_info ring, work_indptr, the reduce maps.
+constexpr int kSerialNp = 0;
+constexpr int kSerialSq = kSerialNp + kStagedBatches;
+constexpr int kSerialRing = kSerialSq + kStagedBatches + 4;
+constexpr int kSerialWi = kSerialRing + kRingRows * 8;
+constexpr int kSerialRi = kSerialWi + (kStagedIndptr + 3) / 4 * 4;
+constexpr int kSerialRfm = kSerialRi + (kStagedReduce + 1 + 3) / 4 * 4;
+constexpr int kSerialRpm = kSerialRfm + 2 * kStagedReduce;
+constexpr int kSerialInts = kSerialRpm + kStagedSplits;
+constexpr int kSharedInts = kParInts > kSerialInts ? kParInts : kSerialInts;
+static_assert(kParU % 4 == 0 && kSerialRing % 4 == 0, "16-byte aligned regions");
+
+// One wave's LDS and global writes ordered before its later reads (the serial state
+// machine runs on a single wave of the workgroup, so it synchronises with no barrier).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+__device__ void serial_schedule(const MetaParams &p, int32_t *lds);
 
 // The schedules of one launch: workgroup i of each kernel computes p[i].
 struct MetaSchedules {
@@ -496,8 +523,7 @@ __device__ bool pack_schedule(const MetaParams &p, const int S, const bool equal
 // When every bin has a partition (avg >= 1) or a head has one bin, head 0 ends in
 // its last bin and every head repeats its schedule nspk bins later, as in the
 // serial machine.  Otherwise (or with more than kParBatches batches, or more than
-// 2^31 partitions) it leaves kSerialSentinel in work_indptr[0] for the serial
-// kernel launched after it.
+// 2^31 partitions) the workgroup's first wave runs the serial machine itself.
 // With bin_groups = G > 1 (get_pa_metadata's option, off for get_pa_metadata_v1)
 // the quotas are weighted instead: the bins of each head form G equal groups and
 // bin c takes Qs(c) = floor(S * Wc(c) / Wt), Wc(c) the weights of the bins before
@@ -508,10 +534,11 @@ __device__ bool pack_schedule(const MetaParams &p, const int S, const bool equal
 // Workgroup i computes schedule sched.p[i] (one launch can hold several).
 __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const MetaSchedules sched) {
     const MetaParams &p = sched.p[blockIdx.x];
-    __shared__ int32_t s_P[kParBatches + 1];  // partitions before batch b
-    __shared__ int32_t s_Q[kParBins + 1];     // weighted quotas: first partition of bin c
+    __shared__ __attribute__((aligned(16))) int32_t s_all[kSharedInts];
+    int32_t *s_P = s_all + kParP;  // partitions before batch b
+    int32_t *s_Q = s_all + kParQ;  // weighted quotas: first partition of bin c
     // the sequential fill's arrays and the packing schedule's share one region
-    __shared__ __attribute__((aligned(16))) int32_t s_u[kUnionInts];
+    int32_t *s_u = s_all + kParU;
     int32_t *s_W = s_u;                        // works of head 0 before batch b
     int32_t *s_L = s_W + kParBatches + 4;      // works of split batches before batch b
     int32_t *s_G = s_L + kParBatches + 4;      // split batches before batch b
@@ -611,8 +638,10 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
         }
     }
     const bool ok = p.nb <= kParBatches && S64 <= 0x7fffffffLL && (S64 >= nspk || nspk == 1);
-    if (!ok) {  // uniform
-        if (t == 0) p.work_indptr[0] = kSerialSentinel;
+    if (!ok) {  // uniform: the serial machine on the first wave, the other waves end here
+        // (every wave has passed a barrier since its last read of s_all, and the serial
+        // machine synchronises within its wave only)
+        if (t < 64) serial_schedule(p, s_all);
         return;
     }
     // one chunk (nb <= kParBatches): run and np4 are this thread's prefix and counts
@@ -747,24 +776,23 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
     }
 }
 
-// Every lane runs the same serial state machine on the same (uniform) values.
-// Its outputs go to LDS -- a ring of work_info rows, work_indptr and the reduce
+// The serial state machine, run by the first wave of the closed-form kernel's
+// workgroup where the closed form does not hold.  Every lane runs it on the same
+// (uniform) values.  Its outputs go to LDS -- a ring of work_info rows, work_indptr and the reduce
 // maps -- and the 64 lanes copy them to global memory with coalesced stores, so
 // the loop is not throttled by single-lane global stores.  Per-batch partition
 // counts and qo offsets are staged in LDS first (and the counts summed by all
 // lanes).  Buffers larger than the LDS copies are written to global memory
 // directly by lane 0.
-__global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaSchedules sched) {
-    const MetaParams &p = sched.p[blockIdx.x];
-    if (p.work_indptr[0] != kSerialSentinel) return;  // the parallel scheduler wrote the schedule
-    __shared__ int32_t s_np[kStagedBatches];
-    __shared__ int32_t s_sq[kStagedBatches + 1];
-    __shared__ __attribute__((aligned(16))) int32_t s_ring[kRingRows * 8];
-    __shared__ int32_t s_wi[kStagedIndptr];
-    __shared__ int32_t s_ri[kStagedReduce + 1];
-    __shared__ int32_t s_rfm[2 * kStagedReduce];
-    __shared__ int32_t s_rpm[kStagedSplits];
-    const int lane = threadIdx.x;
+__device__ void serial_schedule(const MetaParams &p, int32_t *lds) {
+    int32_t *s_np = lds + kSerialNp;
+    int32_t *s_sq = lds + kSerialSq;
+    int32_t *s_ring = lds + kSerialRing;  // 16-byte aligned (lds is)
+    int32_t *s_wi = lds + kSerialWi;
+    int32_t *s_ri = lds + kSerialRi;
+    int32_t *s_rfm = lds + kSerialRfm;
+    int32_t *s_rpm = lds + kSerialRpm;
+    const int lane = threadIdx.x;  // 0..63: the workgroup's first wave
     const bool lead = lane == 0;
     const int staged = min(p.nb, kStagedBatches);
     const bool wi_lds = p.num_cu + 1 <= kStagedIndptr;
@@ -779,7 +807,7 @@ __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaSchedules 
     for (int b = lane; b <= staged; b += 64) s_sq[b] = sq_at(p, b);
 #pragma unroll
     for (int sh = 32; sh >= 1; sh >>= 1) part += __shfl_xor(part, sh, 64);
-    __syncthreads();
+    wave_sync();
     const int nspk = p.num_cu / p.nhk;
     const long long sum_blocks = part;
     const int average = (int)(sum_blocks / nspk);
@@ -811,14 +839,14 @@ __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaSchedules 
     // rows [flushed, upto) of the ring go to work_info (rows past max_work are dropped)
     int flushed = 0;
     auto flush = [&](int upto) {
-        __syncthreads();
+        wave_sync();
         for (int i = flushed * 2 + lane; i < upto * 2; i += 64) {  // half rows of 16 bytes
             const int row = i >> 1;
             if (row < p.max_work)
                 reinterpret_cast<int4 *>(p.work_info)[i] =
                     reinterpret_cast<const int4 *>(s_ring)[((row % kRingRows) << 1) | (i & 1)];
         }
-        __syncthreads();
+        wave_sync();
         flushed = upto;
     };
     bool overflow = false;
@@ -909,7 +937,7 @@ __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaSchedules 
     const int W = num_works;
     const bool replicated = p.nhk > 1 && cid == nspk && W <= kRingRows && flushed == 0;
     if (replicated) {
-        __syncthreads();
+        wave_sync();
         for (int i = lane; i < (p.nhk - 1) * W; i += 64) {
             const int k = 1 + i / W, j = i - (k - 1) * W;
             const int row = k * W + j;
@@ -929,7 +957,7 @@ __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaSchedules 
             if (wi_lds) s_wi[k * nspk + j] = v;
             else p.work_indptr[k * nspk + j] = v;
         }
-        __syncthreads();
+        wave_sync();
         cid = p.nhk * nspk;
         num_works = p.nhk * W;
     } else {
@@ -952,7 +980,7 @@ __global__ __launch_bounds__(64) void pa_metadata_v1_kernel(const MetaSchedules 
     }
     if (rpm_lds)
         for (int i = lane; i < rpm_top; i += 64) p.reduce_partial_map[i] = s_rpm[i];
-    __syncthreads();
+    wave_sync();
     if (lead && p.partial_count) p.partial_count[0] = lri;
     if (lead && overflow) p.work_indptr[0] = -1;
 }
@@ -1016,10 +1044,7 @@ extern "C" int pa_fp8_metadata_multi(const pa_fp8_metadata_args *args, int32_t c
     }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(pa_metadata_par_kernel, dim3(count), dim3(kParThreads), 0, s, sched);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return PA_FP8_ERR_HIP + (int)err;
-    hipLaunchKernelGGL(pa_metadata_v1_kernel, dim3(count), dim3(64), 0, s, sched);
-    err = hipGetLastError();
+    const hipError_t err = hipGetLastError();
     return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
 }
 
