@@ -13,9 +13,13 @@ are rotated step to step so the working set (>= 1.5 GiB for c2) defeats the
 
   value          = algorithmic fp8 K+V bytes per step / us per step (GB/s)
   roofline       = the decode kernel alone: its algorithmic bytes per launch /
-                   its mean duration from HIP events on the launch stream
+                   its mean time per launch from HIP events on the launch stream
+                   (the step's own events when the step is that one kernel, else
+                   back-to-back launches of it alone), never longer than the step
   cpu_baseline   = the reference's torch path (restated with torch CPU ops) timed
                    on this host's cores over 3 full steps of the workload (median)
+  configs        = c3, c4 and c5 measured the same way in the same run, with
+                   --config-steps timed steps each
 """
 
 from __future__ import annotations
@@ -54,6 +58,9 @@ def _parse():
     ap.add_argument("--path", default="decode", choices=["decode", "rope_cache"],
                     help="decode: the headline paged decode; rope_cache: the fused RoPE + KV-cache writer")
     ap.add_argument("--rope-tokens", type=int, default=16384, help="tokens per writer launch (--path rope_cache)")
+    ap.add_argument("--configs", default="c3,c4,c5",
+                    help="other configurations measured in the same run (the line's `configs` block; '' for none)")
+    ap.add_argument("--config-steps", type=int, default=50, help="timed steps of each configuration in --configs")
     return ap.parse_args()
 
 
@@ -67,23 +74,17 @@ def graph_schedule_plus_decode(torch, cfg, works, scale, timed):
     captures its decode step would), replayed in rotation."""
     from flydsl_amd import get_pa_metadata, pa_decode_ps_launch
 
-    eqgs = cfg.query_length * cfg.group_size
     keep, graphs = [], []
     out = torch.empty_like(works[0]["query"])
     for w in works:
-        # the small-block route requires caller partials under capture (the reference's
-        # rule), which its worklist kernel does not touch
-        partials = {"exp_sums": torch.empty(cfg.batch, cfg.num_kv_heads, 1, eqgs, device=out.device),
-                    "max_logits": torch.empty(cfg.batch, cfg.num_kv_heads, 1, eqgs, device=out.device),
-                    "temporary_output": torch.empty(cfg.batch, cfg.num_kv_heads, 1, eqgs, cfg.head_dim,
-                                                    dtype=torch.bfloat16, device=out.device)}
-
-        def body(w=w, partials=partials):
+        # no split-context partials: the small-block route then runs the worklist
+        # kernel over the captured schedule (it allocates nothing)
+        def body(w=w):
             md = get_pa_metadata(w["query"], w["key_cache"], w["context_lengths"], w["kv_indptr"],
                                  cfg.num_q_heads, cfg.num_kv_heads, graph_safe=True)
             pa_decode_ps_launch(out, w["query"], w["key_cache"], w["value_cache"], w["context_lengths"],
                                 w["kv_page_indices"], w["kv_indptr"], scale, w["key_scale"], w["value_scale"],
-                                metadata=md, block_tables=w["block_tables"], **partials)
+                                metadata=md, block_tables=w["block_tables"])
             return md
 
         side = torch.cuda.Stream()
@@ -95,7 +96,7 @@ def graph_schedule_plus_decode(torch, cfg, works, scale, timed):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             md = body()
-        keep.append((md, partials))
+        keep.append(md)
         graphs.append(g)
     us = timed(lambda i: graphs[i % len(graphs)].replay())[0] * 1e3
     torch.cuda.synchronize()
@@ -397,41 +398,79 @@ def rope_main(args):
     print(json.dumps(line), flush=True)
 
 
-def main():
-    args = _parse()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(
-            f"bench.py measures one GPU only: the decode path runs on a single MI355X here "
-            f"(requested --gpus {args.gpus}, WORLD_SIZE {world}); multi-GPU sharding is design-only.",
-            file=sys.stderr,
-        )
-        sys.exit(2)
-    if args.path == "rope_cache":
-        return rope_main(args)
+def _timed(torch, fn, steps, warmup):
+    """ms per call of fn(i) over ``steps`` calls between two HIP events on the
+    launch stream (torch's current stream), after ``warmup`` calls; also the host
+    wall time per call."""
+    for i in range(warmup):
+        fn(i)
+    e0, e1 = _events(torch, 2)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(steps):
+        fn(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps, (time.perf_counter() - t0) / steps
 
-    import torch
 
+def _kernel_alone_ms(torch, plans, j, steps, warmup):
+    """ms per launch of the plans' j-th kernel alone: ``steps`` back-to-back launches
+    of only that kernel (the plans of the rotated KV copies in turn) between two HIP
+    events on the launch stream.  A GPU-side sleep holds the stream until every
+    launch is queued, so host submission never gaps the launches.  The interval per
+    launch is the kernel's duration plus the dependency gap to the next launch; it
+    cannot exceed the step that runs this kernel and the others."""
+    handle = torch.cuda.current_stream().cuda_stream
+    for i in range(warmup):
+        fn, a = plans[i % len(plans)].launches[j]
+        fn(a, handle)
+    e0, e1 = _events(torch, 2)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2.5e6 + 2e4 * steps))  # cycles: several ms of queue head start
+    e0.record()
+    for i in range(steps):
+        fn, a = plans[i % len(plans)].launches[j]
+        fn(a, handle)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def _reference_parts(cfg):
+    """The partition count the reference harness passes (tests/kernels/test_pa.py:852-856
+    calls get_recommended_splits; 8 for the small-block configs, 17 for c4's window)."""
+    from flydsl_amd import get_recommended_splits
+
+    if cfg.sliding_window:
+        return get_recommended_splits(cfg.batch, cfg.num_kv_heads, sliding_window=cfg.sliding_window,
+                                      query_length=cfg.query_length)
+    return get_recommended_splits(cfg.batch, cfg.num_kv_heads, split_kv_blocks=max(1, 256 // cfg.block_size))
+
+
+def measure_decode(torch, cfg, dev, steps, warmup, copies=3, max_parts=0, use_metadata=True, extras=True):
+    """One configuration through ``pa_decode_ps_launch``: the step time (events around
+    ``steps`` steps, ``copies`` KV caches rotated), the dominant kernel's time alone,
+    its algorithmic bytes and the reference harness's partition count.  Returns a
+    dict; ``extras`` adds the partition-kernel and graph-captured variants."""
     from flydsl_amd import get_pa_metadata, pa_decode_ps_launch
     from flydsl_amd.pa_decode_fp8 import _PLAN_CACHE
-    from flydsl_amd.workloads import CONFIGS, build_workload_copies, kv_bytes
+    from flydsl_amd.workloads import build_workload_copies, kv_bytes
 
-    cfg = CONFIGS[args.config]
-    dev = torch.device("cuda:0")
-    print(f"[bench] building {cfg.name} x{args.copies}: {cfg.description}", file=sys.stderr, flush=True)
+    print(f"[bench] building {cfg.name} x{copies}: {cfg.description}", file=sys.stderr, flush=True)
     # the copies differ only in their KV bytes and scales; each cache holds exactly
     # the pages the shared block tables index
-    works = build_workload_copies(cfg, dev, args.copies)
+    works = build_workload_copies(cfg, dev, copies)
     base = works[0]
     ctx = base["context_list"]
-    max_parts = args.max_parts  # 0: the launcher's default for this kernel
     # partials are allocated by the launcher and reused across steps through its plan cache
     out = torch.empty_like(base["query"])
-    scale = 1.0 / math.sqrt(128)
+    scale = 1.0 / math.sqrt(cfg.head_dim)
 
     # the worklist schedule, built once for the batch as the reference harness does
     metadata, metadata_us = None, None
-    if not cfg.sliding_window and not args.no_metadata:
+    if not cfg.sliding_window and use_metadata:
         def build_metadata():
             return get_pa_metadata(base["query"], base["key_cache"], base["context_lengths"], base["kv_indptr"],
                                    cfg.num_q_heads, cfg.num_kv_heads)
@@ -454,96 +493,50 @@ def main():
             block_tables=w["block_tables"], max_context_partition_num=max_parts if parts is None else parts,
         )
 
-    if args.traffic_run:
-        # calibration: a plain copy of known size, then the decode steps to count
-        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        for i in range(args.steps):
-            tag = step(i)
-        torch.cuda.synchronize()
-        print(json.dumps({"traffic_run": cfg.name, "copy_bytes": src.numel(), "steps": args.steps, "path": tag}))
-        return
-
-    def timed(fn):
-        for i in range(args.warmup):
-            fn(i)
-        e0, e1 = _events(torch, 2)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        e0.record()
-        for i in range(args.steps):
-            fn(i)
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / args.steps, (time.perf_counter() - t0) / args.steps
-
-    # ---- headline: K steps through the drop-in launcher
-    for i in range(args.warmup):
+    # ---- the step: K steps through the drop-in launcher
+    for i in range(warmup):
         tag = step(i)
-    ms_per_step, host_s = timed(step)
-
-    # ---- secondary: the split-context partition kernel at the launcher's default
-    # partition count and at the reference's default (get_recommended_splits)
-    from flydsl_amd import get_recommended_splits
-
-    ref_parts = (
-        get_recommended_splits(cfg.batch, cfg.num_kv_heads, sliding_window=cfg.sliding_window,
-                               query_length=cfg.query_length)
-        if cfg.sliding_window
-        else get_recommended_splits(cfg.batch, cfg.num_kv_heads, split_kv_blocks=max(1, 256 // cfg.block_size))
-    )
-    others = {}
-    if metadata is not None and cfg.block_size in (16, 64):
-        others["partition_kernel_auto_partitions"] = timed(lambda i: step(i, md=None))[0] * 1e3
-    ref_us = timed(lambda i: step(i, md=None, parts=ref_parts))[0] * 1e3 if cfg.block_size in (16, 64) or cfg.sliding_window else None
-    # ---- secondary: the schedule rebuilt every step together with the decode, both
-    # captured in one HIP graph per KV copy (get_pa_metadata(graph_safe=True) reads
-    # nothing back to the host), replayed in rotation
-    if metadata is not None:
-        others["graph_schedule_plus_decode"] = graph_schedule_plus_decode(torch, cfg, works, scale, timed)
-    for i in range(len(works)):  # the default plans become the newest cache entries again
-        step(i)
-    torch.cuda.synchronize()
-
-    # ---- per-kernel durations: HIP events around each launch on the launch stream.
-    # A GPU-side sleep holds the stream until every launch and event is queued, so
-    # no interval includes a wait for the host to submit its kernel.
+    ms_per_step, host_s = _timed(torch, step, steps, warmup)
     plans = [_PLAN_CACHE[k] for k in list(_PLAN_CACHE.keys())[-len(works):]]
     names = [fn.__name__ for fn, _ in plans[0].launches]
-    handle = torch.cuda.current_stream(dev).cuda_stream
-    nl = len(names)
-    evs = _events(torch, (nl + 1) * args.steps)
-    torch.cuda.synchronize()
-    torch.cuda._sleep(int(2.5e6 + 4e4 * args.steps))  # cycles: several ms of queue head start
-    for i in range(args.steps):
-        p = plans[i % len(plans)]
-        evs[(nl + 1) * i].record()
-        for j, (fn, a) in enumerate(p.launches):
-            fn(a, handle)
-            evs[(nl + 1) * i + j + 1].record()
-    torch.cuda.synchronize()
-    kernel_ms = {}
-    for j, n in enumerate(names):
-        kernel_ms[_KERNEL_NAMES[n]] = sorted(
-            evs[(nl + 1) * i + j].elapsed_time(evs[(nl + 1) * i + j + 1]) for i in range(args.steps)
-        )
     main_kernel = _KERNEL_NAMES[names[0]]
-    k_ms = kernel_ms[main_kernel]
-    k_mean = sum(k_ms) / len(k_ms)
-    max_parts = plans[0].max_parts
-
-    kvb = kv_bytes(cfg, ctx)
+    used_parts = plans[0].max_parts
     us_step = ms_per_step * 1e3
-    gbs = kvb / (us_step * 1e-6) / 1e9
+
+    # ---- the dominant (first) kernel alone.  With one kernel per step, the step's own
+    # events time it; otherwise back-to-back launches of it alone.
+    if len(names) == 1:
+        k_us = us_step
+        k_timing = "events around the timed steps (each step is this one kernel)"
+    else:
+        k_us = _kernel_alone_ms(torch, plans, 0, steps, warmup) * 1e3
+        k_timing = "events around back-to-back launches of this kernel alone, KV copies rotated"
+    if k_us > us_step:
+        raise RuntimeError(f"{cfg.name}: {main_kernel} alone took {k_us:.2f} us, longer than the step ({us_step:.2f} us)")
     if main_kernel == "pa_decode_worklist_kernel":
         kbytes = _worklist_kernel_bytes(cfg, ctx, metadata)
     else:
-        kbytes = _partition_kernel_bytes(cfg, ctx, max_parts)
-    achieved = kbytes / (k_mean * 1e-3) / 1e9
+        kbytes = _partition_kernel_bytes(cfg, ctx, used_parts)
+    achieved = kbytes / (k_us * 1e-6) / 1e9
 
+    # ---- the reference harness's explicit partition count on the partition kernel
+    # (no metadata: the reference's small-block route ignores it)
+    ref_parts = _reference_parts(cfg)
+    ref_us = _timed(torch, lambda i: step(i, md=None, parts=ref_parts), steps, warmup)[0] * 1e3
+
+    others = {}
+    if extras:
+        if metadata is not None and cfg.block_size in (16, 64):
+            others["partition_kernel_auto_partitions"] = _timed(torch, lambda i: step(i, md=None), steps, warmup)[0] * 1e3
+        # the schedule rebuilt every step together with the decode, both captured in one
+        # HIP graph per KV copy (get_pa_metadata(graph_safe=True) reads nothing back to
+        # the host), replayed in rotation
+        if metadata is not None:
+            others["graph_schedule_plus_decode"] = graph_schedule_plus_decode(
+                torch, cfg, works, scale, lambda fn: _timed(torch, fn, steps, warmup))
+
+    kvb = kv_bytes(cfg, ctx)
+    gbs = kvb / (us_step * 1e-6) / 1e9
     traffic = None
     tfile = ROOT / "profiles" / f"{main_kernel}_{cfg.name}_traffic.json"
     if tfile.exists():
@@ -551,23 +544,137 @@ def main():
             traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
         except Exception:
             traffic = None
+    res = {
+        "works": works,
+        "tag": tag,
+        "us_step": us_step,
+        "host_s": host_s,
+        "gbs": gbs,
+        "kvb": kvb,
+        "metadata_us": metadata_us,
+        "used_parts": used_parts,
+        "kernels": [_KERNEL_NAMES[n] for n in names],
+        "main_kernel": main_kernel,
+        "kernel_us": k_us,
+        "kernel_timing": k_timing,
+        "kbytes": kbytes,
+        "achieved": achieved,
+        "traffic": traffic,
+        "ref_parts": ref_parts,
+        "ref_us": ref_us,
+        "others": others,
+    }
+    return res
+
+
+def main():
+    args = _parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(
+            f"bench.py measures one GPU only: the decode path runs on a single MI355X here "
+            f"(requested --gpus {args.gpus}, WORLD_SIZE {world}); multi-GPU sharding is design-only.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    if args.path == "rope_cache":
+        return rope_main(args)
+
+    import torch
+
+    from flydsl_amd.workloads import CONFIGS
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+
+    if args.traffic_run:
+        from flydsl_amd import get_pa_metadata, pa_decode_ps_launch
+        from flydsl_amd.workloads import build_workload_copies
+
+        works = build_workload_copies(cfg, dev, args.copies)
+        base = works[0]
+        out = torch.empty_like(base["query"])
+        md = None
+        if not cfg.sliding_window and not args.no_metadata:
+            md = get_pa_metadata(base["query"], base["key_cache"], base["context_lengths"], base["kv_indptr"],
+                                 cfg.num_q_heads, cfg.num_kv_heads)
+        # calibration: a plain copy of known size, then the decode steps to count
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            w = works[i % len(works)]
+            tag = pa_decode_ps_launch(
+                out, w["query"], w["key_cache"], w["value_cache"], w["context_lengths"], w["kv_page_indices"],
+                w["kv_indptr"], 1.0 / math.sqrt(cfg.head_dim), w["key_scale"], w["value_scale"],
+                sliding_window=cfg.sliding_window, metadata=md, block_tables=w["block_tables"],
+                max_context_partition_num=args.max_parts)
+        torch.cuda.synchronize()
+        print(json.dumps({"traffic_run": cfg.name, "copy_bytes": src.numel(), "steps": args.steps, "path": tag}))
+        return
+
+    r = measure_decode(torch, cfg, dev, args.steps, args.warmup, copies=args.copies, max_parts=args.max_parts,
+                       use_metadata=not args.no_metadata, extras=True)
+    base = r.pop("works")[0]
 
     cpu = None
     if args.cpu_baseline == "on":
         print("[bench] cpu baseline (the reference's torch path on the host cores, 3 full steps)", file=sys.stderr,
               flush=True)
         cpu = cpu_baseline(base)
+    del base
+    torch.cuda.empty_cache()
 
+    # ---- the other GPU configurations, measured in the same run with a smaller step
+    # budget (inputs resident in HBM, metadata outside the timed steps, as above)
+    configs = {}
+    extra = [c for c in (args.configs.split(",") if args.configs else []) if c and c != cfg.name]
+    for name in extra:
+        c = CONFIGS[name]
+        o = measure_decode(torch, c, dev, args.config_steps, min(args.warmup, 10), copies=args.copies,
+                           use_metadata=not args.no_metadata, extras=False)
+        o.pop("works")
+        torch.cuda.empty_cache()
+        configs[name] = {
+            "workload": c.description,
+            "path": o["tag"],
+            "kernels": o["kernels"],
+            "us_per_step": round(o["us_step"], 2),
+            "kv_gbs": round(o["gbs"], 1),
+            "pct_of_peak": round(100.0 * o["gbs"] / HBM_PEAK_GBS, 2),
+            "kv_bytes_per_step": o["kvb"],
+            "max_context_partition_num": o["used_parts"],
+            "metadata_us": round(o["metadata_us"], 2) if o["metadata_us"] is not None else None,
+            "kernel": {
+                "name": o["main_kernel"],
+                "us": round(o["kernel_us"], 2),
+                "timing": o["kernel_timing"],
+                "algorithmic_bytes_per_launch": o["kbytes"],
+                "achieved_gbs": round(o["achieved"], 1),
+                "frac": round(o["achieved"] / HBM_PEAK_GBS, 4),
+                "traffic": o["traffic"],
+            },
+            "reference_default_partitions": {
+                "max_context_partition_num": o["ref_parts"],
+                "us_per_step": round(o["ref_us"], 2),
+                "kv_gbs": round(o["kvb"] / (o["ref_us"] * 1e-6) / 1e9, 1),
+            },
+            "steps": args.config_steps,
+        }
+
+    us_step = r["us_step"]
     line = {
         "metric": METRIC,
-        "value": round(gbs, 1),
+        "value": round(r["gbs"], 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
+        "ms_per_step": round(us_step * 1e-3, 5),
         "us_per_step": round(us_step, 2),
-        "pct_of_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "pct_of_peak": round(100.0 * r["gbs"] / HBM_PEAK_GBS, 2),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -579,41 +686,41 @@ def main():
             "query_length": cfg.query_length,
             "num_q_heads": cfg.num_q_heads,
             "num_kv_heads": cfg.num_kv_heads,
-            "head_dim": 128,
+            "head_dim": cfg.head_dim,
             "block_size": cfg.block_size,
             "kv_dtype": "fp8_e4m3fn",
             "scales": "per-token" if cfg.per_token else "per-tensor",
             "sliding_window": cfg.sliding_window,
-            "max_context_partition_num": max_parts,
-            "kv_bytes_per_step": kvb,
-            "kv_cache_copies_rotated": len(works),
-            "path": tag,
-            "kernels": [_KERNEL_NAMES[n] for n in names],
-            "metadata": "get_pa_metadata once per batch, outside the timed steps" if metadata is not None else None,
+            "max_context_partition_num": r["used_parts"],
+            "kv_bytes_per_step": r["kvb"],
+            "kv_cache_copies_rotated": args.copies,
+            "path": r["tag"],
+            "kernels": r["kernels"],
+            "metadata": "get_pa_metadata once per batch, outside the timed steps" if r["metadata_us"] is not None else None,
         },
-        "kernels_us": {
-            **{k: round(sum(v) / len(v) * 1e3, 2) for k, v in kernel_ms.items()},
-            f"{main_kernel}_median": round(k_ms[len(k_ms) // 2] * 1e3, 2),
-        },
-        "metadata_us": round(metadata_us, 2) if metadata_us is not None else None,
-        "host_us_per_step": round(host_s * 1e6, 2),
-        "other_paths_us_per_step": {k: round(v, 2) for k, v in others.items()},
-        "reference_default_partitions": None if ref_us is None else {
-            "max_context_partition_num": ref_parts,
-            "us_per_step": round(ref_us, 2),
-            "kv_gbs": round(kvb / (ref_us * 1e-6) / 1e9, 1),
+        "kernels_us": {r["main_kernel"]: round(r["kernel_us"], 2)},
+        "metadata_us": round(r["metadata_us"], 2) if r["metadata_us"] is not None else None,
+        "host_us_per_step": round(r["host_s"] * 1e6, 2),
+        "other_paths_us_per_step": {k: round(v, 2) for k, v in r["others"].items()},
+        "reference_default_partitions": {
+            "max_context_partition_num": r["ref_parts"],
+            "us_per_step": round(r["ref_us"], 2),
+            "kv_gbs": round(r["kvb"] / (r["ref_us"] * 1e-6) / 1e9, 1),
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(achieved, 1),
+            "achieved": round(r["achieved"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "kernel": main_kernel,
-            "algorithmic_bytes_per_launch": kbytes,
+            "frac": round(r["achieved"] / HBM_PEAK_GBS, 4),
+            "traffic": r["traffic"],
+            "kernel": r["main_kernel"],
+            "algorithmic_bytes_per_launch": r["kbytes"],
+            "kernel_us": round(r["kernel_us"], 2),
+            "kernel_timing": r["kernel_timing"],
         },
         "cpu_baseline": cpu,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
 

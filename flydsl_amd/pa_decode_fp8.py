@@ -387,7 +387,11 @@ def _partitioned_plan(
         )
     output_5d = output.view(batch_size, query_length, num_kv_heads, query_group_size, head_size)
     given_es, given_ml, given_to = exp_sums is not None, max_logits is not None, temporary_output is not None
-    direct = max_parts == 1
+    # One slot per sequence: the kernel writes the output itself.  On the small-block
+    # path the reference fills caller-passed partials even at one slot (its reduce
+    # then reads them), so those calls keep the partials; its fused sliding-window
+    # kernel writes the output directly (kernels/pa_decode_fp8.py:2923, :2977-2979).
+    direct = max_parts == 1 and (sliding_window > 0 or not (given_es or given_ml or given_to))
     if direct:
         # one slot per sequence: the partition kernel writes the output itself
         exp_sums = max_logits = temporary_output = None
@@ -739,24 +743,27 @@ def _build_plan_checked(
     small = block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES
     # Block sizes other than 16 / 64 take the persistent path, as in the reference.
     # The small-block path also runs the worklist kernel when the caller hands
-    # in get_pa_metadata's schedule with the flat page list and the batch is
-    # ragged: the schedule balances ragged batches across CUs, which fixed
-    # partition slots cannot (equal-length batches keep the partition kernel,
-    # whose slots are balanced already and which skips the worklist reads).  The
-    # tag stays "ps_small_block" and exp_sums / max_logits / temporary_output are
-    # not touched (they are scratch of the split-context kernels).
+    # in get_pa_metadata's schedule with the flat page list, the batch is ragged
+    # and no split-context partials are passed: the schedule balances ragged
+    # batches across CUs, which fixed partition slots cannot (equal-length batches
+    # keep the partition kernel, whose slots are balanced already and which skips
+    # the worklist reads).  The tag stays "ps_small_block".  A caller that passes
+    # exp_sums / max_logits / temporary_output gets them filled in the reference's
+    # partition-slot format, as the reference's small-block route (which ignores
+    # metadata) fills them: that call runs the partition kernel at the caller's
+    # partition count (kernels/pa_decode_fp8.py:3010-3121).
+    caller_partials = exp_sums is not None or max_logits is not None or temporary_output is not None
     balanced_worklist = (metadata is not None and kv_page_indices is not None and kv_indptr is not None
-                         and not metadata.get("uniform_context", False))
+                         and not metadata.get("uniform_context", False) and not caller_partials)
     if small and sliding_window <= 0 and not trans_v:
         # the reference's small-block kernel reads trans_v only (kernels/pa_decode_fp8.py:2082-2083)
         raise NotImplementedError("compile_pa_decode_ps: trans_v=False not yet supported.")
     if sliding_window <= 0 and (not small or balanced_worklist):
         if small:
-            if is_graph_capturing and (exp_sums is None or max_logits is None or temporary_output is None):
-                raise ValueError(  # the reference's small-block rule (kernels/pa_decode_fp8.py:3030-3034)
-                    "CUDA graph capture requires preallocated `exp_sums`, `max_logits`, "
-                    "and `temporary_output` for the small-block PS path."
-                )
+            # The reference requires preallocated partials under capture on this path
+            # because its kernel writes them (kernels/pa_decode_fp8.py:3030-3034); the
+            # worklist route writes none and allocates nothing, so it is capturable
+            # without them (the partition route below keeps the reference's rule).
             plan = _worklist_plan(output, query, key_cache, value_cache, context_lengths, kv_page_indices, kv_indptr,
                                   metadata, softmax_scale, key_scale, value_scale, per_token_kv, is_graph_capturing)
             plan.tag = "ps_small_block"

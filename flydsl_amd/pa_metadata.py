@@ -91,6 +91,17 @@ def get_pa_metadata_v1(
         raise ValueError("reduce_indptr / reduce_final_map too small")
     if work_info.numel() % _WORK_INFO_FIELDS:
         raise ValueError("work_info must hold 8 int32 per work")
+    # The schedule can need every row get_pa_metadata_info_v1 sizes (kernels/pa_metadata.py:
+    # 63-72); the device marks an overflow only in work_indptr[0], which the decode would
+    # read as a truncated worklist, so smaller buffers are refused here (no device read).
+    max_work = (num_batches + num_cu - 1) * num_heads_k
+    max_split = min(num_batches + num_cu - 1, 2 * (num_cu - 1))
+    if work_info.numel() // _WORK_INFO_FIELDS < max_work:
+        raise ValueError(f"work_info holds {work_info.numel() // _WORK_INFO_FIELDS} works; the schedule may need "
+                         f"{max_work} ((batch + num_cu - 1) * num_heads_k, get_pa_metadata_info_v1)")
+    if reduce_partial_map.numel() < max_split:
+        raise ValueError(f"reduce_partial_map holds {reduce_partial_map.numel()} entries; the schedule may need "
+                         f"{max_split} (min(batch + num_cu - 1, 2 * (num_cu - 1)), get_pa_metadata_info_v1)")
     if work_metadata_ptrs is not None and work_metadata_ptrs.numel() >= 2:
         # device fills (capturable into a graph), not host-to-device copies
         ptrs = work_metadata_ptrs.view(torch.int64)

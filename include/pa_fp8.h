@@ -136,7 +136,8 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *args, void *hip_stream);
  * The partials need B * Hkv * P * ql*g * (8 + 2 * head_dim) bytes (each piece
  * rounded up to 256); more returns PA_FP8_ERR_SCRATCH.  Outputs are bit-identical
  * to the two-call path.  The scratch is looked up (hipGetSymbolAddress) on the
- * first call on each device and never allocated or freed.  Every call on a GPU
+ * first call on each device and never allocated or freed; make that first call
+ * before capturing the entry point into a HIP graph.  Every call on a GPU
  * shares that GPU's one scratch: calls that overlap on one GPU (several streams,
  * or host threads, at once) race; calls ordered on one stream do not.
  *

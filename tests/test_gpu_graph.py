@@ -83,16 +83,22 @@ def test_graph_safe_metadata_matches_host_sized(name):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("partials", [False, True])
 @pytest.mark.parametrize("name", list(CASES))
-def test_captured_metadata_and_decode_replay_over_new_contexts(name):
+def test_captured_metadata_and_decode_replay_over_new_contexts(name, partials):
     cfg = _case(name)
-    w = build_workload(cfg, DEV, seed=12)
     small = cfg.block_size in (16, 64)
+    if partials and not small:
+        pytest.skip("caller partials belong to the small-block route")
+    w = build_workload(cfg, DEV, seed=12)
     ql = cfg.query_length
     max_ctx = list(w["context_list"])
-    # preallocated split-context scratch: the capture rule of the small-block path
+    # Small blocks without partials: the worklist route over the captured schedule
+    # (it allocates nothing).  With preallocated split-context partials (the
+    # reference's capture rule for its small-block path): the partition kernel at
+    # the caller's partition count, filling them.
     extra = {}
-    if small:
+    if partials:
         P = 8
         eqgs = ql * (cfg.num_q_heads // cfg.num_kv_heads)
         extra = dict(

@@ -26,14 +26,15 @@ def _spread(n: int, k: int):
 
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
 def test_baseline_config_outputs(name):
-    """Every benchmark configuration at full size; oracle on a spread of sequences."""
+    """Every benchmark configuration at full size, every sequence against the oracle
+    (the reference counts any mismatching element, tests/kernels/test_pa.py:626-641)."""
     cfg = CONFIGS[name]
     print(f"[parity] {name}: {cfg.description}", flush=True)
     w = build_workload(cfg, "cuda")
     out, tag, _ = launch(w)
     # one slot per sequence under a window is the reference's "fused" variant
     assert tag in (("ps_sw_partitioned", "ps_sw_fused_partitioned") if cfg.sliding_window else ("ps_small_block",))
-    worst = compare_outputs(w, out, _spread(cfg.batch, 6))
+    worst = compare_outputs(w, out, range(cfg.batch))
     print(f"[parity] {name}: max |diff| {worst:.3e}", flush=True)
 
 
@@ -84,11 +85,13 @@ def test_small_cases_with_partials(case, max_parts):
 @pytest.mark.parametrize("name", ["c2", "c4"])
 @pytest.mark.parametrize("max_parts", [1, 8])
 def test_baseline_config_partition_counts(name, max_parts):
-    """Full-size configs at the direct-output and the reference-default partition counts."""
+    """Full-size configs at the direct-output and the reference-default partition
+    counts, every sequence against the oracle."""
     cfg = CONFIGS[name]
+    print(f"[parity] {name} P={max_parts}", flush=True)
     w = build_workload(cfg, "cuda")
     out, _, _ = launch(w, max_parts=max_parts)
-    compare_outputs(w, out, _spread(cfg.batch, 4))
+    compare_outputs(w, out, range(cfg.batch))
 
 
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
@@ -139,6 +142,38 @@ def test_reference_call_pattern_with_recommended_partials(name):
                               max_context_partition_num=0, **partials)
     torch.cuda.synchronize()
     assert tag == ("ps_sw_partitioned" if cfg.sliding_window else "ps_small_block")
-    batches = _spread(cfg.batch, 5)
-    compare_outputs(w, out, batches)
-    check_partials(w, partials, parts, batches)
+    compare_outputs(w, out, range(cfg.batch))
+    check_partials(w, partials, parts, _spread(cfg.batch, 16))
+
+
+@pytest.mark.parametrize("parts", [1, 8])
+def test_caller_partials_with_metadata_on_a_ragged_batch(parts):
+    """The reference harness's arguments on a ragged c3 batch -- get_pa_metadata's
+    schedule, the flat page list, an explicit partition count -- plus caller-passed
+    exp_sums / max_logits / temporary_output: the reference's small-block route
+    ignores the metadata and fills the partials slot by slot
+    (kernels/pa_decode_fp8.py:3010-3121), and so does this launcher (even at one
+    slot, where its reduce reads them).  Every slot is checked against the oracle's
+    token range, every sequence's output against the oracle."""
+    from flydsl_amd import get_pa_metadata, pa_decode_ps_launch
+
+    cfg = CONFIGS["c3"]
+    print(f"[parity] c3 with metadata and caller partials, P={parts}", flush=True)
+    w = build_workload(cfg, "cuda")
+    md = get_pa_metadata(w["query"], w["key_cache"], w["context_lengths"], w["kv_indptr"], cfg.num_q_heads,
+                         cfg.num_kv_heads)
+    assert md["uniform_context"] is False
+    eqgs = cfg.query_length * cfg.group_size
+    shape = (cfg.batch, cfg.num_kv_heads, parts, eqgs)
+    partials = {"exp_sums": torch.full(shape, float("nan"), device="cuda"),
+                "max_logits": torch.full(shape, float("nan"), device="cuda"),
+                "temporary_output": torch.full(shape + (128,), float("nan"), dtype=torch.bfloat16, device="cuda")}
+    out = torch.empty_like(w["query"])
+    tag = pa_decode_ps_launch(out, w["query"], w["key_cache"], w["value_cache"], w["context_lengths"],
+                              w["kv_page_indices"], w["kv_indptr"], 1.0 / math.sqrt(128), w["key_scale"],
+                              w["value_scale"], metadata=md, block_tables=w["block_tables"],
+                              max_context_partition_num=parts, **partials)
+    torch.cuda.synchronize()
+    assert tag == "ps_small_block"
+    compare_outputs(w, out, range(cfg.batch))
+    check_partials(w, partials, parts, _spread(cfg.batch, 16))

@@ -330,9 +330,39 @@ def test_small_block_with_metadata_runs_the_worklist(bs):
     assert plan(t, max_parts=4, kv_indptr=None).dargs is not None
     assert plan(t, max_parts=4, metadata=dict(t["metadata"], uniform_context=True)).dargs is not None
     assert plan(t, sliding_window=300, max_parts=4).dargs is not None
-    # the reference's graph-capture rule for this path still holds
+    # the worklist route allocates nothing, so it is capturable without partials; the
+    # partition route keeps the reference's graph-capture rule
+    assert plan(t, capturing=True).wargs is not None
     with pytest.raises(ValueError, match="small-block PS path"):
-        plan(t, capturing=True)
+        plan(t, capturing=True, metadata=None)
+
+
+@pytest.mark.parametrize("bs", [16, 64])
+@pytest.mark.parametrize("parts", [1, 3, 8])
+def test_caller_partials_get_the_partition_slot_format(bs, parts):
+    """Caller-passed exp_sums / max_logits / temporary_output on the small-block route
+    are filled in the reference's partition-slot format at the caller's count, as the
+    reference's small-block route (which ignores metadata) fills them
+    (kernels/pa_decode_fp8.py:3010-3121): the partition kernel runs even with the
+    schedule of a ragged batch, at one slot too (then with the reduce)."""
+    t = make_paged(bs=bs, ctx=(1027, 300, 2000), num_cu=3)
+    hkv = t["key_cache"].shape[1]
+    eqgs = (t["query"].shape[0] // 3) * (t["query"].shape[1] // hkv)  # query_length * group size
+    shape = (3, hkv, parts, eqgs)
+    es, ml = torch.empty(shape), torch.empty(shape)
+    to = torch.empty(shape + (128,), dtype=torch.bfloat16)
+    for explicit in (0, parts):
+        p = plan(t, max_parts=explicit, exp_sums=es, max_logits=ml, temporary_output=to)
+        assert p.tag == "ps_small_block" and p.wargs is None and p.dargs is not None
+        assert p.max_parts == parts and p.dargs.max_context_partition_num == parts
+        assert p.dargs.direct_output == 0 and p.rargs is not None
+        assert p.dargs.exp_sums == es.data_ptr() and p.dargs.max_logits == ml.data_ptr()
+        assert p.dargs.tmp_out == to.data_ptr()
+    # under capture too (the reference's rule is met: the partials are preallocated)
+    assert plan(t, max_parts=parts, exp_sums=es, max_logits=ml, temporary_output=to, capturing=True).dargs is not None
+    # one slot without caller partials writes the output directly
+    p = plan(t, max_parts=1, metadata=None)
+    assert p.dargs.direct_output == 1 and p.rargs is None
 
 
 def test_default_partition_count_follows_caller_partials():
@@ -442,3 +472,22 @@ def test_worklist_prefers_the_tuned_schedule():
     assert p_ref.wargs.num_cu == 4 and p_ref.wargs.work_indptr == ref["work_indptr"].data_ptr()
     with pytest.raises(ValueError, match="tuned"):
         plan(t, metadata=dict(ref, tuned={"num_sm": 2}), max_parts=0)
+
+
+def test_metadata_v1_refuses_buffers_below_the_schedule_bound():
+    """get_pa_metadata_v1 refuses work_info / reduce_partial_map smaller than
+    get_pa_metadata_info_v1's sizes (kernels/pa_metadata.py:63-72) before launching:
+    the device only marks an overflow in work_indptr[0], which a decode would read as
+    a truncated worklist."""
+    from flydsl_amd.pa_metadata import get_pa_metadata_v1
+
+    b, hkv, num_cu = 5, 2, 8
+    i32 = lambda *s: torch.zeros(*s, dtype=torch.int32)  # noqa: E731
+    infos = get_pa_metadata_info_v1(b, hkv, num_cu=num_cu)
+    ptrs, wi, winfo, ri, rfm, rpm = [torch.zeros(shape, dtype=dtype) for shape, dtype in infos]
+    sq, ctx = torch.arange(b + 1, dtype=torch.int32), torch.full((b,), 700, dtype=torch.int32)
+    kw = dict(kv_granularity=256, block_size=16, max_seqlen_qo=1, uni_seqlen_qo=1, num_cu=num_cu)
+    with pytest.raises(ValueError, match="work_info holds"):
+        get_pa_metadata_v1(sq, i32(b + 1), ctx, 4, hkv, True, ptrs, wi, winfo[:-1].contiguous(), ri, rfm, rpm, **kw)
+    with pytest.raises(ValueError, match="reduce_partial_map holds"):
+        get_pa_metadata_v1(sq, i32(b + 1), ctx, 4, hkv, True, ptrs, wi, winfo, ri, rfm, rpm[:-1].contiguous(), **kw)

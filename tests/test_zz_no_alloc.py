@@ -19,14 +19,15 @@ from tests.pa_testlib import compare_outputs, launch
 pytestmark = pytest.mark.gpu
 
 
-def _noalloc(w, parts, out_dtype=torch.bfloat16):
-    """One call of the allocation-free entry through the C ABI."""
+def _noalloc(w, parts, out_dtype=torch.bfloat16, out=None, sync=True):
+    """One call of the allocation-free entry through the C ABI (into ``out`` when given)."""
     from flydsl_amd import _lib
     from flydsl_amd import pa_decode_fp8 as pdf
 
     cfg = w["config"]
     q = w["query"]
-    out = torch.full(q.shape, float("nan"), dtype=out_dtype, device=q.device)
+    if out is None:
+        out = torch.full(q.shape, float("nan"), dtype=out_dtype, device=q.device)
     a = pdf._decode_args(
         query=q, key_cache=w["key_cache"], value_cache=w["value_cache"], block_tables=w["block_tables"],
         context_lengths=w["context_lengths"], key_scale=w["key_scale"], value_scale=w["value_scale"],
@@ -38,12 +39,13 @@ def _noalloc(w, parts, out_dtype=torch.bfloat16):
     a.output = o5.data_ptr()
     a.stride_o_seq, a.stride_o_len, a.stride_o_head, a.stride_o_group = (o5.stride(i) for i in range(4))
     a.out_dtype = {torch.bfloat16: _lib.PA_FP8_BF16, torch.float16: _lib.PA_FP8_F16,
-                   torch.float32: _lib.PA_FP8_F32}[out_dtype]
+                   torch.float32: _lib.PA_FP8_F32}[out.dtype]
     # the launcher's wave count, so both paths accumulate in the same order
     a.waves_per_slot = pdf._waves_per_slot(q.device, cfg.batch, cfg.num_kv_heads, parts, q.shape[-1])
     stream = torch.cuda.current_stream().cuda_stream
     status = _lib.LIB.pa_fp8_decode_partitions_noalloc(ctypes.byref(a), ctypes.c_void_p(stream))
-    torch.cuda.synchronize()
+    if sync:
+        torch.cuda.synchronize()
     return status, out
 
 
@@ -75,3 +77,34 @@ def test_noalloc_refuses_more_partials_than_the_scratch():
     # 64 x 8 x 128 slots x 4 rows x (8 + 256) bytes = 69 MB > 32 MiB
     status, _ = _noalloc(w, 128)
     assert status == _lib.PA_FP8_ERR_SCRATCH
+
+
+def test_noalloc_replays_in_a_hip_graph():
+    """A call captured into a HIP graph (after one eager call on the device, which
+    looks up the scratch address) replays over new context lengths written into the
+    captured tensor; every replay equals an eager call on the same inputs bit for bit,
+    with eager work between the replays."""
+    import numpy as np
+
+    cfg = scaled(CONFIGS["c3"], name="noalloc_graph", batch=7, ctx_kind="uniform", ctx_a=1, ctx_b=3000)
+    w = build_workload(cfg, "cuda", seed=65)
+    parts = 4
+    max_ctx = list(w["context_list"])
+    status, _ = _noalloc(w, parts)  # the first call on the device, outside the capture
+    assert status == 0
+    out = torch.empty_like(w["query"])
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        status, _ = _noalloc(w, parts, out=out, sync=False)
+    assert status == 0
+    rng = np.random.default_rng(6)
+    for rep in range(4):
+        new_ctx = [int(rng.integers(0, c + 1)) for c in max_ctx]
+        w["context_lengths"].copy_(torch.tensor(new_ctx, dtype=torch.int32))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        status, eager = _noalloc(w, parts)
+        print(f"[noalloc] graph replay {rep}: ctx {new_ctx[:4]}...", flush=True)
+        assert status == 0 and torch.equal(got, eager), f"replay {rep} differs from the eager call"
