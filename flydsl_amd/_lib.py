@@ -13,7 +13,7 @@ from pathlib import Path
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("PA_FP8_LIB", str(_HERE / "libpa_fp8.so")))
 
-PA_FP8_ABI_VERSION = 9
+PA_FP8_ABI_VERSION = 10
 PA_FP8_BF16, PA_FP8_F16, PA_FP8_F32 = 0, 1, 2
 PA_FP8_CACHE_ELEM, PA_FP8_CACHE_FP8_TENSOR, PA_FP8_CACHE_FP8_TOKEN = 0, 1, 2
 PA_FP8_KV_FLASH, PA_FP8_KV_X_PACKED, PA_FP8_KV_X_TRANS = 0, 1, 2
@@ -77,6 +77,7 @@ class DecodeArgs(ctypes.Structure):
         ("stride_o_group", _i64),
         ("waves_per_slot", _i32),
         ("value_layout", _i32),
+        ("slots_per_wave", _i32),
     ]
 
 

@@ -114,4 +114,43 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     return __builtin_bit_cast(uint16_t, h);
 }
 
+// Log-sum-exp merge of the P partials of one query row: lane owns head dims
+// 2*lane, 2*lane+1 of each 128-dim block (a0 / a1 per block; NB blocks).
+// es / ml point at the row's exp_sum / max_logit of slot 0, to at its bf16 partial
+// row of slot 0.  out = sum_z w_z to_z with w_z = s_z e^(m_z - M) / sum_z s_z e^(m_z - M),
+// M = max_z m_z (kernels/pa_decode_swa.py:954-1130).  Both the reduce kernel and the
+// partition kernel's in-workgroup merge run this, so their outputs are identical.
+template <int NB>
+__device__ __forceinline__ void lse_merge_row(const float *es, const float *ml, const uint16_t *to, int64_t s_es_part,
+                                              int64_t s_to_part, int P, int head_dim, int lane, float (&a0)[NB],
+                                              float (&a1)[NB]) {
+    float mloc = -INFINITY;
+    for (int z = lane; z < P; z += 64) mloc = fmaxf(mloc, ml[z * s_es_part]);
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) mloc = fmaxf(mloc, shfl_xor_f(mloc, sh));
+    const float Ms = mloc == -INFINITY ? 0.0f : mloc;
+    float wl = 0.f;
+    for (int z = lane; z < P; z += 64) {
+        const float mz = ml[z * s_es_part];
+        wl += es[z * s_es_part] * fast_exp2((mz - Ms) * kLog2e);
+    }
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) wl += shfl_xor_f(wl, sh);
+    const float inv = wl > 0.f ? 1.0f / wl : 0.0f;
+#pragma unroll
+    for (int k = 0; k < NB; ++k) a0[k] = a1[k] = 0.f;
+    for (int z = 0; z < P; ++z) {
+        const float w = es[z * s_es_part] * fast_exp2((ml[z * s_es_part] - Ms) * kLog2e) * inv;
+        if (w != 0.f) {
+#pragma unroll
+            for (int k = 0; k < NB; ++k) {
+                if (2 * lane + 128 * k >= head_dim) continue;
+                const uint32_t two = *reinterpret_cast<const uint32_t *>(to + z * s_to_part + 128 * k + 2 * lane);
+                a0[k] += w * bf16_bits_to_f32(uint16_t(two & 0xffffu));
+                a1[k] += w * bf16_bits_to_f32(uint16_t(two >> 16));
+            }
+        }
+    }
+}
+
 }  // namespace pa

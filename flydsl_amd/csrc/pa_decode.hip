@@ -280,42 +280,13 @@ __global__ __launch_bounds__(64) void pa_lse_reduce_kernel(const ReduceParams p)
     const int b = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
     const float *es = p.es + b * p.s_es_seq + h * p.s_es_head + r;
     const float *ml = p.ml + b * p.s_es_seq + h * p.s_es_head + r;
-    const uint16_t *to = p.to + b * p.s_to_seq + h * p.s_to_head + r * p.s_to_group + 2 * lane;
-    const int P = p.max_parts;
-
-    float mloc = -INFINITY;
-    for (int z = lane; z < P; z += 64) mloc = fmaxf(mloc, ml[z * p.s_es_part]);
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) mloc = fmaxf(mloc, shfl_xor_f(mloc, sh));
-    const float Ms = mloc == -INFINITY ? 0.0f : mloc;
-    float wl = 0.f;
-    for (int z = lane; z < P; z += 64) {
-        const float mz = ml[z * p.s_es_part];
-        wl += es[z * p.s_es_part] * fast_exp2((mz - Ms) * kLog2e);
-    }
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) wl += shfl_xor_f(wl, sh);
-    const float inv = wl > 0.f ? 1.0f / wl : 0.0f;
-
+    const uint16_t *to = p.to + b * p.s_to_seq + h * p.s_to_head + r * p.s_to_group;
     constexpr int NB = kMaxHeadDim / 128;
     bool live[NB];
 #pragma unroll
     for (int k = 0; k < NB; ++k) live[k] = 2 * lane + 128 * k < p.head_dim;
     float a0[NB], a1[NB];
-#pragma unroll
-    for (int k = 0; k < NB; ++k) a0[k] = a1[k] = 0.f;
-    for (int z = 0; z < P; ++z) {
-        const float w = es[z * p.s_es_part] * fast_exp2((ml[z * p.s_es_part] - Ms) * kLog2e) * inv;
-        if (w != 0.f) {
-#pragma unroll
-            for (int k = 0; k < NB; ++k) {
-                if (!live[k]) continue;
-                const uint32_t two = *reinterpret_cast<const uint32_t *>(to + z * p.s_to_part + 128 * k);
-                a0[k] += w * bf16_bits_to_f32(uint16_t(two & 0xffffu));
-                a1[k] += w * bf16_bits_to_f32(uint16_t(two >> 16));
-            }
-        }
-    }
+    lse_merge_row<NB>(es, ml, to, p.s_es_part, p.s_to_part, p.max_parts, p.head_dim, lane, a0, a1);
     const int qi = r / p.g, gi = r - (r / p.g) * p.g;
     const int64_t off = b * p.s_o_seq + qi * p.s_o_len + h * p.s_o_head + gi * p.s_o_group + 2 * lane;
 #pragma unroll
@@ -410,11 +381,21 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
     if (a->waves_per_slot != 0 && a->waves_per_slot != 1 && a->waves_per_slot != 2 && a->waves_per_slot != 4 &&
         a->waves_per_slot != 8)
         return PA_FP8_ERR_SHAPE;
+    // chained slots: one 16-row group, head_dim 128, the trans_v layout
+    const int spw = a->slots_per_wave;
+    const int wg_waves = a->waves_per_slot > 0 ? a->waves_per_slot : (spw > 0 ? 1 : 4);
+    if (spw < 0 || spw > 65535) return PA_FP8_ERR_SHAPE;
+    if (spw > 0 && (eqgs > 16 || a->head_dim != 128 || a->value_layout != PA_FP8_V_TRANS)) return PA_FP8_ERR_SHAPE;
+    const int P = a->max_context_partition_num;
+    const int64_t slots_per_wg = spw > 0 ? (int64_t)wg_waves * spw : 1;
     if (a->direct_output) {
-        if (a->max_context_partition_num != 1) return PA_FP8_ERR_PARTITIONS;
+        // several slots per sequence: only when one chained workgroup holds them all
+        // (it merges its own partials, which the caller provides)
+        if (P != 1 && (spw == 0 || slots_per_wg < P)) return PA_FP8_ERR_PARTITIONS;
         if (a->out_dtype != PA_FP8_BF16 && a->out_dtype != PA_FP8_F16 && a->out_dtype != PA_FP8_F32)
             return PA_FP8_ERR_DTYPE;
     }
+    const bool partials = !a->direct_output || P > 1;
     const int chunks = (eqgs + kRowChunk - 1) / kRowChunk;
     if ((int64_t)a->batch_size * chunks > 0x7fffffff) return PA_FP8_ERR_SHAPE;
     if (a->batch_size == 0) return PA_FP8_OK;
@@ -427,13 +408,12 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
         if ((reinterpret_cast<uintptr_t>(a->output) & 15) ||
             ((a->stride_o_seq | a->stride_o_len | a->stride_o_head | a->stride_o_group) * esz) & 15)
             return PA_FP8_ERR_SHAPE;
-    } else if (!a->exp_sums || !a->max_logits || !a->tmp_out) {
-        return PA_FP8_ERR_NULL_POINTER;
     }
+    if (partials && (!a->exp_sums || !a->max_logits || !a->tmp_out)) return PA_FP8_ERR_NULL_POINTER;
     if (a->num_blocks <= 0 || a->max_blocks_per_seq <= 0) return PA_FP8_ERR_SHAPE;
     // 16-byte vector accesses: caches, query rows and partial rows must be 16-byte aligned
     if (!aligned16(a->key_cache) || !aligned16(a->value_cache) || !aligned16(a->query) ||
-        (!a->direct_output && !aligned16(a->tmp_out)))
+        (partials && !aligned16(a->tmp_out)))
         return PA_FP8_ERR_SHAPE;
     if ((a->stride_k_block | a->stride_k_head | a->stride_v_block | a->stride_v_head) & 15) return PA_FP8_ERR_SHAPE;
     if ((a->stride_q_seq | a->stride_q_head) & 7) return PA_FP8_ERR_SHAPE;
@@ -488,8 +468,16 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
     p.s_o_head = a->stride_o_head;
     p.s_o_group = a->stride_o_group;
     p.out_dtype = a->out_dtype;
+    p.spw = spw;
+    // a merging workgroup keeps a copy of its partials in LDS when they fit in 48 KiB
+    // (then it reads LDS, not the rows it just stored): P rows of eqgs x (D bf16 + 2 f32)
+    p.merge_lds = 0;
+    if (a->direct_output && P > 1) {
+        const int64_t bytes = (int64_t)P * eqgs * (2 * a->head_dim + 8);
+        if (bytes <= 48 * 1024) p.merge_lds = (int32_t)bytes;
+    }
 
-    const dim3 grid(a->batch_size * chunks, a->num_kv_heads, a->max_context_partition_num);
+    const dim3 grid(a->batch_size * chunks, a->num_kv_heads, (unsigned)((P + slots_per_wg - 1) / slots_per_wg));
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int mtp = (min(eqgs, kRowChunk) + 15) / 16;
     const hipError_t err = run_partition(a->head_dim, p, a->per_token_kv != 0, a->value_layout == PA_FP8_V_4D, mtp,
@@ -526,7 +514,10 @@ int pa_fp8_decode_partitions_noalloc(const pa_fp8_decode_args *a, void *stream) 
     if (st != PA_FP8_OK) return st;
     // partials in the scratch: exp_sums, max_logits [B, Hkv, P, eqgs] f32, tmp_out [B, Hkv, P, eqgs, D] bf16
     const int64_t P = a->max_context_partition_num, D = a->head_dim;
-    d.direct_output = 0;
+    // a chained layout whose workgroups hold every slot of a sequence merges its own
+    // partials (direct_output); otherwise the reduce below does
+    const bool merged = a->direct_output != 0;
+    d.direct_output = merged ? 1 : 0;
     d.exp_sums = reinterpret_cast<float *>(base);
     d.max_logits = reinterpret_cast<float *>(base + es_bytes);
     d.tmp_out = base + 2 * es_bytes;
@@ -538,7 +529,7 @@ int pa_fp8_decode_partitions_noalloc(const pa_fp8_decode_args *a, void *stream) 
     d.stride_to_part = eqgs * D;
     d.stride_to_group = D;
     int status = pa_fp8_decode_partitions(&d, stream);
-    if (status != PA_FP8_OK) return status;
+    if (status != PA_FP8_OK || merged) return status;
     pa_fp8_reduce_args r = {};
     r.output = a->output;
     r.exp_sums = d.exp_sums;

@@ -65,17 +65,23 @@ __device__ __forceinline__ void store_out(void *out, int out_dtype, int64_t off,
 }
 
 // Where the partition kernel puts the result of one slot: the bf16 partial row
-// plus (exp_sum, max_logit), or (direct mode) the final row out[b, qi, h, gi, :].
+// plus (exp_sum, max_logit), or (final: one slot per sequence) the final row
+// out[b, qi, h, gi, :].
 struct SlotSink {
     const DecodeParams &p;
     uint16_t *to;
     float *es;
     float *ml;
     int b, h;
+    bool final_row;
+    // LDS copy of the slot's partial for a merge inside the workgroup (rows of kHeadDim
+    // bf16, then exp_sum / max_logit per row); null when unused
+    uint16_t *lto = nullptr;
+    float *les = nullptr, *lml = nullptr;
 
     template <int N>
     __device__ __forceinline__ void row(int r, int d0, const float (&v)[N]) const {
-        if (!p.direct) {
+        if (!final_row) {
             uint32_t pk[N / 2];
 #pragma unroll
             for (int j = 0; j < N; j += 2)
@@ -83,6 +89,11 @@ struct SlotSink {
             uint16_t *dst = to + r * p.s_to_group + d0;
             if constexpr (N == 8) *reinterpret_cast<uint4 *>(dst) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
             else *reinterpret_cast<uint2 *>(dst) = make_uint2(pk[0], pk[1]);
+            if (lto) {
+                uint16_t *ldst = lto + r * kHeadDim + d0;
+                if constexpr (N == 8) *reinterpret_cast<uint4 *>(ldst) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+                else *reinterpret_cast<uint2 *>(ldst) = make_uint2(pk[0], pk[1]);
+            }
             return;
         }
         const int qi = r / p.g, gi = r - (r / p.g) * p.g;
@@ -90,9 +101,14 @@ struct SlotSink {
     }
     // L = sum of exp2(logit2 - m2) over the slot, m2 = running max in log2 units
     __device__ __forceinline__ void stats(int r, float L, float m2) const {
-        if (!p.direct) {
+        if (!final_row) {
+            const float m = L > 0.f ? m2 * kLn2 : -INFINITY;
             es[r] = L;
-            ml[r] = L > 0.f ? m2 * kLn2 : -INFINITY;
+            ml[r] = m;
+            if (les) {
+                les[r] = L;
+                lml[r] = m;
+            }
         }
     }
 };
@@ -469,10 +485,11 @@ __device__ __forceinline__ void finish_rows(SmState<MTPW, D> &st, const DecodePa
     }
 }
 
-// Rows [row0, row_end) of an empty range (kernels/pa_decode_fp8.py:2591-2598).
+// Rows [row0, row_end) of an empty range (kernels/pa_decode_fp8.py:2591-2598),
+// written by the nthreads threads tid = 0 .. nthreads-1.
 template <int D, class Sink>
-__device__ __forceinline__ void emit_empty(int nthreads, int row0, int row_end, const Sink &sink) {
-    const int tid = threadIdx.x;
+__device__ __forceinline__ void emit_empty(int nthreads, int row0, int row_end, const Sink &sink,
+                                           int tid = threadIdx.x) {
     for (int r = row0 + tid; r < row_end; r += nthreads) sink.stats(r, 0.0f, -INFINITY);
     const float zero8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int i = tid; i < (row_end - row0) * (D / 8); i += nthreads)
@@ -699,6 +716,216 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
                 __syncthreads();
             }
         }
+    }
+}
+
+// Token range [lo, hi) of partition slot z of a sequence of ctx tokens: the 256-token
+// partitions [z*pps, min((z+1)*pps, T)) with T = ceil(ctx/256), pps = ceil(T/P)
+// (kernels/pa_decode_fp8.py:2311-2320); with a sliding window they start at tile
+// max(ctx-ql-sw, 0)/256 (kernels/pa_decode_swa.py:1359-1368) and the first window tile
+// is trimmed to the 16-token group holding the window start.  Empty when lo >= hi.
+// Slot ranges are increasing in z and contiguous: an empty slot has only empty
+// slots after it.
+__device__ __forceinline__ void slot_tokens(const DecodeParams &p, int ctx, int z, int &lo, int &hi) {
+    const int T = (ctx + kPartition - 1) / kPartition;
+    const int seq_start = p.sw > 0 ? max(ctx - p.ql - p.sw, 0) : 0;
+    const int first_tile = seq_start / kPartition;
+    const int vis = T - first_tile;
+    const int pps = vis > 0 ? (vis + p.max_parts - 1) / p.max_parts : 0;
+    const int plo = first_tile + z * pps;
+    const int phi = min(plo + pps, T);
+    lo = plo * kPartition;
+    hi = min(phi * kPartition, ctx);
+    if (lo < seq_start) lo = seq_start & ~(kGroup - 1);
+}
+
+// Single-wave layout over a chain of partition slots [z0, z1) of (sequence b, kv
+// head h), query rows [row0, row0 + 16*MTPW): the wave streams the steps of every
+// slot in turn, its load pipeline (page-table entries two steps ahead, K / V one
+// step ahead) running on across slot boundaries, and writes each slot's partial (or,
+// with one slot per sequence, the output) when that slot's last step is done.  The
+// per-slot state restarts there; each slot's result is exactly what a workgroup of
+// its own would write.  Slots without keys (a suffix of the chain) get the empty
+// partial (kernels/pa_decode_fp8.py:2591-2598).
+template <int MTPW, bool PER_TOKEN, int D, bool V4>
+__device__ __forceinline__ void attend_slots(const DecodeParams &p, const int b, const int h, const int ctx,
+                                             const int z0, const int z1, const int32_t *bt_row, const int row0,
+                                             uint8_t *merge_lds = nullptr) {
+    constexpr int CPL = D / 64;
+    const int lane = threadIdx.x & 63;
+    const int l16 = lane & 15;
+    const int kg = lane >> 4;
+    const int bs = 1 << p.bs_log2;
+    const int row_group0 = row0 >> 4;
+    // one slot per sequence in direct mode: the final rows; otherwise the slot's partial
+    const bool final_row = p.direct && p.max_parts == 1;
+    auto sink_of = [&](int z) {
+        SlotSink sk{p,
+                    p.tmp_out + b * p.s_to_seq + h * p.s_to_head + z * p.s_to_part,
+                    p.exp_sums + b * p.s_es_seq + h * p.s_es_head + z * p.s_es_part,
+                    p.max_logits + b * p.s_es_seq + h * p.s_es_head + z * p.s_es_part,
+                    b,
+                    h,
+                    final_row};
+        if (merge_lds) {  // [P][eqgs][kHeadDim] bf16 rows, then [P][eqgs] exp sums and max logits
+            const int rows = p.max_parts * p.eqgs;
+            sk.lto = reinterpret_cast<uint16_t *>(merge_lds) + z * p.eqgs * kHeadDim;
+            sk.les = reinterpret_cast<float *>(merge_lds + rows * kHeadDim * 2) + z * p.eqgs;
+            sk.lml = sk.les + rows;
+        }
+        return sk;
+    };
+
+    // Slot geometry of the sequence (slot_tokens without its division per slot):
+    // slot z covers [max(base + z * span, trim), min(base + (z + 1) * span, ctx)).
+    const int T = (ctx + kPartition - 1) / kPartition;
+    const int seq_start = p.sw > 0 ? max(ctx - p.ql - p.sw, 0) : 0;
+    const int first_tile = seq_start / kPartition;
+    const int vis = T - first_tile;
+    const int pps = vis > 0 ? (vis + p.max_parts - 1) / p.max_parts : 0;
+    const int base = first_tile * kPartition, span = pps * kPartition;
+    const int trim = seq_start & ~(kGroup - 1);
+    auto slot_lo = [&](int z) { return max(base + z * span, trim); };
+    auto slot_hi = [&](int z) { return min(base + (z + 1) * span, ctx); };
+    // the slots with keys: a prefix [z0, ze) of the chain (slot z has keys iff its
+    // first tile exists, first_tile + z * pps < T)
+    const int ze = pps > 0 ? min(z1, max(z0, (vis + pps - 1) / pps)) : z0;
+    for (int z = ze; z < z1; ++z) emit_empty<D>(64, row0, min(p.eqgs, row0 + kRowChunk), sink_of(z), lane);
+    if (ze == z0) return;
+
+    const float k_fac = PER_TOKEN ? p.qk_scale : p.qk_scale * p.ks[0];
+    const float k_eff = logit_scale(k_fac);
+    RowSet<MTPW, D> rw;
+    // the rows' own key bounds (window start, causal end), clipped per slot below
+    setup_rows(rw, p, b, h, ctx, 0, ctx, row_group0, l16, kg, k_fac < 0.0f);
+    int row_lo[MTPW], row_hi[MTPW];
+#pragma unroll
+    for (int mg = 0; mg < MTPW; ++mg) {
+        row_lo[mg] = rw.lo_n[mg];
+        row_hi[mg] = rw.hi_n[mg];
+    }
+    const int rows_lo_max = rw.lo_max, rows_hi_min = rw.hi_min;
+    const float v_fac = PER_TOKEN ? 1.0f : p.vs[0];
+    SmState<MTPW, D> st;
+    st.init();
+
+    // A step of the chain: its slot z (ze: past the chain), first token t0 and its
+    // slot's end e (page reads clamp to token e - 1, in the slot's last 16-token group).
+    // The slot has a later step iff t0 + 64 < e.  Wave-uniform.
+    struct Cur {
+        int z, t0, e;
+    };
+    auto slot_first = [&](int z) { return z < ze ? Cur{z, slot_lo(z), slot_hi(z)} : Cur{ze, 0, 1}; };
+    auto advance = [&](const Cur &c) {
+        if (c.z >= ze) return c;
+        return c.t0 + kStep < c.e ? Cur{c.z, c.t0 + kStep, c.e} : slot_first(c.z + 1);
+    };
+    auto enter_slot = [&](const Cur &c) {  // the rows' key bounds within the slot
+        const int lo = slot_lo(c.z);
+#pragma unroll
+        for (int mg = 0; mg < MTPW; ++mg) {
+            rw.lo_n[mg] = max(row_lo[mg], lo);
+            rw.hi_n[mg] = min(row_hi[mg], c.e);
+        }
+        rw.lo_max = max(rows_lo_max, lo);
+        rw.hi_min = min(rows_hi_min, c.e);
+    };
+
+    const uint8_t *kc_h = p.kc + (int64_t)h * p.s_k_head;
+    const uint8_t *vc_h = p.vc + (int64_t)h * p.s_v_head;
+    const int kchunk = bs * 16;
+    const int k_lane_off = (l16 & 3) * 16 + (CPL * kg) * kchunk;
+    const int vd = V4 ? bs : 16;
+    const int vsub = V4 ? 16 : D * 16;
+    const int v_lane_off = l16 * vd;
+    auto page_of = [&](const Cur &c, int g) { return bt_row[min(c.t0 + 16 * g, c.e - 1) >> p.bs_log2]; };
+    auto k_ptr = [&](const Cur &c, int e) {
+        const int gs = min(c.t0 + 16 * (l16 >> 2), c.e - 1);
+        const int phys = min(max(e, 0), p.num_blocks - 1);
+        return kc_h + (int64_t)phys * p.s_k_block + ((gs & (bs - 1)) >> 4) * 256 + k_lane_off;
+    };
+    auto v_loc = [&](const Cur &c, int e, int64_t &vofs, int64_t &sofs) {
+        const int gs = min(c.t0 + 16 * kg, c.e - 1);
+        const int phys = min(max(e, 0), p.num_blocks - 1);
+        const int sub = (gs & (bs - 1)) >> 4;
+        vofs = (int64_t)phys * p.s_v_block + sub * vsub + v_lane_off;
+        sofs = (int64_t)phys * p.s_ks_block + (int64_t)h * p.s_ks_head + sub * 16;
+    };
+
+    uint4 kr[4][kKChunks<D>];
+    uint4 vr[D / 16];
+    f32x4 ksl, vsl;  // per-token scale quarters, gathered across the quad at each step
+    auto load_k = [&](const uint8_t *kb) {
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) kr[jt][c] = ld16(kb + c * kchunk + jt * 64);
+    };
+    auto load_v = [&](int64_t vofs) {
+#pragma unroll
+        for (int m = 0; m < D / 16; ++m) vr[m] = ld16(vc_h + vofs + m * 16 * vd);
+    };
+    auto load_scales = [&](int64_t sofs) {
+        ksl = *reinterpret_cast<const f32x4 *>(p.ks + sofs + 4 * (l16 & 3));
+        vsl = *reinterpret_cast<const f32x4 *>(p.vs + sofs + 4 * (l16 & 3));
+    };
+
+    Cur cur = slot_first(z0);
+    Cur c1 = advance(cur);
+    int ek_next = 0, ev_next = 0;  // page-table entries of step c1
+    {
+        const int ek = page_of(cur, l16 >> 2), ev = page_of(cur, kg);
+        if (c1.z < ze) {
+            ek_next = page_of(c1, l16 >> 2);
+            ev_next = page_of(c1, kg);
+        }
+        int64_t vofs, sofs;
+        v_loc(cur, ev, vofs, sofs);
+        load_k(k_ptr(cur, ek));
+        if constexpr (PER_TOKEN) load_scales(sofs);
+        load_v(vofs);
+    }
+    enter_slot(cur);
+    while (cur.z < ze) {
+        const Cur c2 = advance(c1);
+        const bool has_nxt = c1.z < ze;
+        int ek_after = 0, ev_after = 0;
+        if (c2.z < ze) {
+            ek_after = page_of(c2, l16 >> 2);
+            ev_after = page_of(c2, kg);
+        }
+        const uint8_t *nkb = nullptr;
+        int64_t nvofs = 0, nsofs = 0;
+        if (has_nxt) {
+            nkb = k_ptr(c1, ek_next);
+            v_loc(c1, ev_next, nvofs, nsofs);
+        }
+        ek_next = ek_after;
+        ev_next = ev_after;
+        f32x4 ksc[4], vsc[4];
+        if constexpr (PER_TOKEN) {
+            quad_gather(ksl, ksc);
+            quad_gather(vsl, vsc);
+        }
+        bf16x8 pop[MTPW][2];
+        step_qk_softmax<MTPW, D, PER_TOKEN>(st, rw, kr, [&](int jt) { return ksc[jt]; },
+                                            [&](int jt) { return vsc[jt]; }, k_eff, cur.t0, kg, pop, [&] {
+                                                if (has_nxt) {
+                                                    load_k(nkb);
+                                                    if constexpr (PER_TOKEN) load_scales(nsofs);
+                                                }
+                                            });
+        step_pv<MTPW, D>(st, vr, pop);
+        if (has_nxt) load_v(nvofs);
+        if (c1.z != cur.z) {  // the slot's last step: its result, then a fresh state for the next slot
+            finish_rows<MTPW, D>(st, p, row_group0, l16, kg, v_fac, sink_of(cur.z));
+            if (has_nxt) {
+                st.init();
+                enter_slot(c1);
+            }
+        }
+        cur = c1;
+        c1 = c2;
     }
 }
 
@@ -980,33 +1207,87 @@ __global__ __launch_bounds__((kThreads<RS, NS>), (kWavesFor<MTPW, NS, D>)) void 
         row0 = (blockIdx.x - b * p.chunks) * kRowChunk;
     }
     const int h = blockIdx.y;
-    const int z = blockIdx.z;
 
-    // ---- slot -> token range (integer planner, bit-exact with the oracle)
     int64_t ctx64 = p.ctx[b];
     const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
     ctx64 = ctx64 < 0 ? 0 : (ctx64 > cap ? cap : ctx64);
     const int ctx = (int)ctx64;
-    const int T = (ctx + kPartition - 1) / kPartition;
-    int seq_start = 0;
-    if (p.sw > 0) seq_start = max(ctx - p.ql - p.sw, 0);
-    const int first_tile = seq_start / kPartition;
-    const int vis = T - first_tile;
-    const int pps = vis > 0 ? (vis + p.max_parts - 1) / p.max_parts : 0;
-    const int plo = first_tile + z * pps;
-    const int phi = min(plo + pps, T);
-    int tok_lo = plo * kPartition;
-    const int tok_hi = min(phi * kPartition, ctx);
-    if (tok_lo < seq_start) tok_lo = seq_start & ~(kGroup - 1);
+    const int z = blockIdx.z;
+
+    // ---- slot -> token range (integer planner, bit-exact with the oracle)
+    int tok_lo, tok_hi;
+    slot_tokens(p, ctx, z, tok_lo, tok_hi);
 
     const SlotSink sink{p,
                         p.tmp_out + b * p.s_to_seq + h * p.s_to_head + z * p.s_to_part,
                         p.exp_sums + b * p.s_es_seq + h * p.s_es_head + z * p.s_es_part,
                         p.max_logits + b * p.s_es_seq + h * p.s_es_head + z * p.s_es_part,
                         b,
-                        h};
+                        h,
+                        p.direct != 0};
     attend<MTPW, RS, NS, PER_TOKEN, D, V4>(p, b, h, ctx, tok_lo, tok_hi, p.bt + (int64_t)b * p.s_bt_seq,
                                            p.max_blocks, row0, sink);
+}
+
+// Chained-slot layout: workgroup (b, h, zc) has NW waves; wave w runs the slots
+// [(zc * NW + w) * spw, (zc * NW + w + 1) * spw) of (sequence b, kv head h) in turn
+// (attend_slots), each writing its slots' partials.  When one workgroup holds every
+// slot of its (sequence, kv head) and p.direct is set, its waves then merge those
+// partials into the final output themselves (the reduce's arithmetic, lse_merge_row),
+// and no reduce launch follows.  Query rows: one 16-row group (ql * g <= 16).
+template <int NW, bool PER_TOKEN, int D, bool V4>
+__global__ __launch_bounds__(NW * 64, (kWavesPerSimd<1, D>)) void pa_decode_chain_kernel(const DecodeParams p) {
+    const int b = blockIdx.x;
+    const int h = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int64_t ctx64 = p.ctx[b];
+    const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
+    ctx64 = ctx64 < 0 ? 0 : (ctx64 > cap ? cap : ctx64);
+    const int ctx = (int)ctx64;
+    const int64_t zb = ((int64_t)blockIdx.z * NW + wave) * p.spw;
+    const int z0 = (int)min(zb, (int64_t)p.max_parts);
+    const int z1 = (int)min(zb + p.spw, (int64_t)p.max_parts);
+    // the merge's copy of the partials, when the host sized the dynamic LDS for it
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_merge[];
+    const bool lds_merge = p.direct && p.max_parts > 1 && p.merge_lds;
+    attend_slots<1, PER_TOKEN, D, V4>(p, b, h, ctx, z0, z1, p.bt + (int64_t)b * p.s_bt_seq, 0,
+                                      lds_merge ? s_merge : nullptr);
+    if (!p.direct || p.max_parts == 1) return;
+    // every slot's partial is written (in LDS, or in global memory: a workgroup-scope
+    // release and acquire, the waves sharing a CU and none of them having read these
+    // rows before)
+    __syncthreads();
+    constexpr int NB = (D + 127) / 128;
+    const int rows = p.max_parts * p.eqgs;
+    for (int r = wave; r < p.eqgs; r += NW) {
+        const int64_t e0 = b * p.s_es_seq + h * p.s_es_head + r;
+        float a0[NB], a1[NB];
+        if (lds_merge) {
+            const float *les = reinterpret_cast<const float *>(s_merge + rows * kHeadDim * 2);
+            lse_merge_row<NB>(les + r, les + rows + r, reinterpret_cast<const uint16_t *>(s_merge) + r * kHeadDim,
+                              p.eqgs, p.eqgs * kHeadDim, p.max_parts, D, lane, a0, a1);
+        } else {
+            lse_merge_row<NB>(p.exp_sums + e0, p.max_logits + e0, p.tmp_out + b * p.s_to_seq + h * p.s_to_head +
+                              r * p.s_to_group, p.s_es_part, p.s_to_part, p.max_parts, D, lane, a0, a1);
+        }
+        const int qi = r / p.g, gi = r - (r / p.g) * p.g;
+        const int64_t off = b * p.s_o_seq + qi * p.s_o_len + h * p.s_o_head + gi * p.s_o_group + 2 * lane;
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            if (2 * lane + 128 * k >= D) continue;
+            if (p.out_dtype == PA_FP8_F32) {
+                float *o = reinterpret_cast<float *>(p.out) + off + 128 * k;
+                *reinterpret_cast<float2 *>(o) = make_float2(a0[k], a1[k]);
+            } else {
+                uint16_t *o = reinterpret_cast<uint16_t *>(p.out) + off + 128 * k;
+                *reinterpret_cast<uint32_t *>(o) =
+                    p.out_dtype == PA_FP8_F16
+                        ? uint32_t(f32_to_f16_bits(a0[k])) | (uint32_t(f32_to_f16_bits(a1[k])) << 16)
+                        : uint32_t(f32_to_bf16_bits(a0[k])) | (uint32_t(f32_to_bf16_bits(a1[k])) << 16);
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------- worklist path
@@ -1133,8 +1414,24 @@ hipError_t launch_partition(const DecodeParams &p, dim3 grid, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <int NW, bool PT, int D, bool V4>
+hipError_t launch_chain(const DecodeParams &p, dim3 grid, hipStream_t s) {
+    hipLaunchKernelGGL((pa_decode_chain_kernel<NW, PT, D, V4>), grid, dim3(NW * 64), p.merge_lds, s, p);
+    return hipGetLastError();
+}
+
 template <bool PT, int D, bool V4>
 hipError_t dispatch_partition_pt(const DecodeParams &p, int mtp, int waves, dim3 grid, hipStream_t s) {
+    if constexpr (D == 128 && !V4) {
+        if (p.spw > 0) {  // chained slots (the C ABI admits them for one row group only)
+            switch (waves) {
+            case 2: return launch_chain<2, PT, D, V4>(p, grid, s);
+            case 4: return launch_chain<4, PT, D, V4>(p, grid, s);
+            case 8: return launch_chain<8, PT, D, V4>(p, grid, s);
+            default: return launch_chain<1, PT, D, V4>(p, grid, s);
+            }
+        }
+    }
     switch (mtp) {
     case 1:
         if constexpr (D == 128) {

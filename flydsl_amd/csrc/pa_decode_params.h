@@ -40,6 +40,8 @@ struct DecodeParams {
     int64_t s_o_seq, s_o_len, s_o_head, s_o_group;
     int32_t out_dtype;
     int32_t direct;
+    int32_t spw;        // chained layout: partition slots one wave runs in turn (0: one slot per workgroup)
+    int32_t merge_lds;  // bytes of dynamic LDS holding the partials a merging workgroup reads (0: global)
 };
 
 struct WorklistParams {

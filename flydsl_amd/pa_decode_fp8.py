@@ -332,11 +332,59 @@ def _auto_layout(dev, batch_size, num_kv_heads, max_tokens, sliding_window, quer
     return max(1, min(max(fill, least), tiles)), 4
 
 
+# Resident waves per CU of the register-streaming layout (two per SIMD), and the
+# most steps a chain of slots may give one wave (it bounds the longest wave of a
+# ragged batch, whose slots the host cannot see).
+_WAVES_PER_CU = 8
+_CHAIN_MAX_STEPS = 32
+
+
+def _slot_layout(dev, batch_size, num_kv_heads, max_parts, head_dim=HEAD_DIM, eqgs=1, v4=False,
+                 max_slot_tokens=None):
+    """(waves per workgroup, slots per wave, merged) of the partition kernel.
+
+    One-row-group layouts take the fewest waves per slot (1, 2, 4 or 8) whose grid
+    fills the GPU at eight resident waves per CU: a wave then streams more steps and
+    a slot needs no merge of its waves' states.  Measured on c2 at 8 slots per
+    sequence, 99.7 / 101.8 / 106.6 / 136.0 us per step at 1 / 2 / 4 / 8 waves; c4 at
+    17 slots, 61.3 / 63.2 / 73.8 / 97.2 us.
+
+    When one wave per slot fills the GPU, and workgroups of W <= 8 waves, one per
+    (sequence, kv head), fill it too, each wave of such a workgroup runs consecutive
+    slots in turn (the chained layout, slots per wave > 0), its loads running on
+    across slot boundaries, and the workgroup merges its own partials into the output
+    (``merged``: no reduce launch) -- as long as a wave's chain stays within
+    _CHAIN_MAX_STEPS steps of the longest possible slot (``max_slot_tokens``).  c2 at
+    8 slots: 94.0 us (99.6 with one slot per one-wave workgroup and the reduce); c4 at
+    17 slots: 54.3 us (62.2).  Otherwise slots that may be long (ragged batches, whose
+    lengths the host cannot see) get one wave per _CHAIN_MAX_STEPS steps, up to 8:
+    c3 at 8 slots (up to 64 steps each) 302.1 us with two waves, 308.1 with one."""
+    if head_dim != HEAD_DIM or eqgs > 16:
+        return 4, 0, False
+    target = _WAVES_PER_CU * _device_cu_count(dev)
+    pairs = max(1, batch_size * num_kv_heads)
+    slots = pairs * max_parts
+    choices = (4, 8) if v4 else (1, 2, 4, 8)
+    waves = next((c for c in choices if slots * c >= target), choices[-1])
+    if v4 or waves > 1 or max_parts == 1:
+        return waves, 0, False
+    steps = max(1, _cdiv(max_slot_tokens, 64)) if max_slot_tokens else 1
+    wg = next((c for c in (1, 2, 4, 8) if pairs * c >= target), None)
+    if wg is not None and _cdiv(max_parts, wg) * steps <= _CHAIN_MAX_STEPS:
+        return wg, _cdiv(max_parts, wg), True
+    return next((c for c in (1, 2, 4, 8) if c * _CHAIN_MAX_STEPS >= steps), 8), 0, False
+
+
 def _waves_per_slot(dev, batch_size, num_kv_heads, max_parts, head_dim=HEAD_DIM):
-    """Eight waves per slot when the grid fits one workgroup per CU (head_dim 128), else four."""
-    if head_dim != HEAD_DIM:
-        return 4
-    return 8 if batch_size * num_kv_heads * max_parts <= _device_cu_count(dev) else 4
+    """Waves per workgroup of the one-row-group layout (see _slot_layout)."""
+    return _slot_layout(dev, batch_size, num_kv_heads, max_parts, head_dim)[0]
+
+
+def _max_slot_tokens(max_tokens, max_parts, sliding_window, query_length):
+    """Tokens of the longest slot any sequence of at most max_tokens tokens can have."""
+    span = min(max_tokens, sliding_window + query_length) if sliding_window > 0 else max_tokens
+    tiles = _cdiv(span, KV_COMPUTE_BLOCK) + (1 if sliding_window > 0 else 0)
+    return _cdiv(tiles, max_parts) * KV_COMPUTE_BLOCK
 
 
 _PLAN_CACHE: "OrderedDict[tuple, _Plan]" = OrderedDict()
@@ -386,6 +434,10 @@ def _partitioned_plan(
             f"and `temporary_output` for the {path_name} path."
         )
     output_5d = output.view(batch_size, query_length, num_kv_heads, query_group_size, head_size)
+    max_tokens = block_tables.shape[1] * key_cache.shape[-2]
+    waves, spw, merged = _slot_layout(dev, batch_size, num_kv_heads, max_parts, head_size, eqgs,
+                                      value_cache.dim() != 5,
+                                      _max_slot_tokens(max_tokens, max_parts, sliding_window, query_length))
     given_es, given_ml, given_to = exp_sums is not None, max_logits is not None, temporary_output is not None
     # One slot per sequence: the kernel writes the output itself.  On the small-block
     # path the reference fills caller-passed partials even at one slot (its reduce
@@ -425,8 +477,10 @@ def _partitioned_plan(
         softmax_scale=softmax_scale,
     )
     out_dtype = _get_output_dtype_str(output)
-    dargs.waves_per_slot = _waves_per_slot(dev, batch_size, num_kv_heads, max_parts, head_size)
-    if direct:
+    dargs.waves_per_slot, dargs.slots_per_wave = waves, spw
+    if direct or merged:
+        # the kernel writes the output: one slot per sequence, or workgroups that hold
+        # every slot of their (sequence, kv head) and merge the partials they wrote
         dargs.direct_output = 1
         dargs.out_dtype = {"bf16": _lib.PA_FP8_BF16, "f16": _lib.PA_FP8_F16, "f32": _lib.PA_FP8_F32}[out_dtype]
         dargs.output = output_5d.data_ptr()

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define PA_FP8_ABI_VERSION 9
+#define PA_FP8_ABI_VERSION 10
 
 enum pa_fp8_status {
     PA_FP8_OK = 0,
@@ -105,19 +105,34 @@ typedef struct pa_fp8_decode_args {
     int32_t per_token_kv;        /* 0 = per-tensor scales, 1 = per-token */
     int32_t query_dtype;         /* PA_FP8_BF16 or PA_FP8_F16 */
     float softmax_scale;
-    /* direct_output = 1 (only with max_context_partition_num == 1): each workgroup
-     * holds the whole sequence, so it writes the final rows to
-     * output[b, qi, h, gi, :] (5-D view [B, ql, Hkv, g, D], dtype out_dtype) as
-     * pa_fp8_lse_reduce would, and exp_sums / max_logits / tmp_out are not used. */
+    /* direct_output = 1: the kernel writes the final rows to output[b, qi, h, gi, :]
+     * (5-D view [B, ql, Hkv, g, D], dtype out_dtype) as pa_fp8_lse_reduce would.
+     * With max_context_partition_num == 1 each workgroup holds the whole sequence
+     * and exp_sums / max_logits / tmp_out are not used.  With more slots it needs
+     * the chained layout below with waves_per_slot * slots_per_wave >= the slot
+     * count (one workgroup per sequence and kv head): the workgroup writes every
+     * slot's partial, then merges them into the output with pa_fp8_lse_reduce's
+     * arithmetic (the same bits), so no reduce launch follows. */
     int32_t direct_output;
     int32_t out_dtype;
     void *output;
     int64_t stride_o_seq, stride_o_len, stride_o_head, stride_o_group;
-    /* waves per workgroup when ql * query_group_size <= 16 (the waves split a slot's
-     * steps): 0 = 4, or 1, 2, 4, 8.  Eight suits grids of at most one workgroup per CU.
-     * Head dims other than 128 and 256 always run four. */
+    /* waves per workgroup when ql * query_group_size <= 16: 0 = 4, or 1, 2, 4, 8.
+     * With slots_per_wave == 0 the waves split one slot's steps (eight suit grids of
+     * at most one workgroup per CU; head dims other than 128 always run four);
+     * with slots_per_wave > 0 each wave runs its own chain of slots. */
     int32_t waves_per_slot;
     int32_t value_layout;        /* pa_fp8_value_layout */
+    /* 0: one slot per workgroup.  slots_per_wave > 0 (only with
+     * ql * query_group_size <= 16, head_dim 128 and the trans_v layout): the chained
+     * layout -- wave w of workgroup (b, h, zc) runs the slots
+     * [(zc * W + w) * slots_per_wave, (zc * W + w + 1) * slots_per_wave) of its
+     * (sequence, kv head) in turn (W = waves_per_slot, 0 meaning 1), its K / V loads
+     * running on across slot boundaries, and writes each slot's partial as that slot
+     * ends; the grid's third dimension is ceil(max_context_partition_num /
+     * (W * slots_per_wave)).  A slot's partial is the same whichever layout runs
+     * with one wave per slot. */
+    int32_t slots_per_wave;
 } pa_fp8_decode_args;
 
 int pa_fp8_decode_partitions(const pa_fp8_decode_args *args, void *hip_stream);

@@ -122,6 +122,18 @@ def _decode_args(lib, **over):
         ({"direct_output": 1}, 7),
         ({"waves_per_slot": 3}, 5),
         ({"batch_size": 3}, 1),  # null pointers
+        # the chained layout: one 16-row group, head_dim 128, the trans_v layout
+        ({"slots_per_wave": 2}, 0),
+        ({"slots_per_wave": 2, "waves_per_slot": 4}, 0),
+        ({"slots_per_wave": -1}, 5),
+        ({"slots_per_wave": 2, "query_group_size": 32}, 5),
+        ({"slots_per_wave": 2, "head_dim": 64}, 5),
+        ({"slots_per_wave": 2, "value_layout": 1}, 5),
+        # several slots written to the output: only workgroups that hold every slot
+        ({"direct_output": 1, "slots_per_wave": 2, "waves_per_slot": 4}, 0),
+        ({"direct_output": 1, "slots_per_wave": 2, "waves_per_slot": 2}, 7),
+        ({"direct_output": 1, "slots_per_wave": 0, "waves_per_slot": 8}, 7),
+        ({"direct_output": 1, "slots_per_wave": 8, "waves_per_slot": 1, "batch_size": 3}, 1),  # null pointers
     ],
 )
 def test_decode_validation_codes(lib, over, status):

@@ -177,3 +177,50 @@ def test_caller_partials_with_metadata_on_a_ragged_batch(parts):
     assert tag == "ps_small_block"
     compare_outputs(w, out, range(cfg.batch))
     check_partials(w, partials, parts, _spread(cfg.batch, 16))
+
+
+CHAIN_CASES = {
+    "bs16_pt_g4": dict(base="c2", batch=5, ctx_kind="uniform", ctx_a=1, ctx_b=3000),
+    "bs16_tok_g4": dict(base="c3", batch=6, ctx_kind="uniform", ctx_a=1, ctx_b=3000),
+    "sw_small": dict(base="c4", batch=4, sliding_window=300, ctx_kind="uniform", ctx_a=1, ctx_b=2000),
+    "sw_mtp": dict(base="c4", batch=4, sliding_window=100, query_length=3, ctx_kind="uniform", ctx_a=3, ctx_b=900),
+    "bs64_ql2_g8_tok": dict(base="c3", batch=4, num_q_heads=16, num_kv_heads=2, block_size=64, query_length=2,
+                            ctx_kind="uniform", ctx_a=2, ctx_b=2500),
+}
+
+
+def _bits(t):
+    return t.view(torch.int32) if t.dtype == torch.float32 else t.view(torch.int16)
+
+
+@pytest.mark.parametrize("case", sorted(CHAIN_CASES))
+@pytest.mark.parametrize("parts,spw,wg", [(3, 2, 2), (8, 3, 4), (8, 8, 1), (5, 4, 2), (17, 3, 8)])
+def test_chained_slots_equal_one_slot_per_wave(case, parts, spw, wg, monkeypatch):
+    """One wave running several consecutive slots (its loads running on across the
+    slot boundaries) writes exactly what one wave per slot writes; and workgroups of
+    wg such waves that hold every slot of their (sequence, kv head) and merge their
+    own partials write the output the reduce kernel writes.  Partials and outputs
+    bit-identical across the three layouts, every slot checked against the oracle's
+    token range, empty slots (0, -inf, 0) included."""
+    from flydsl_amd import pa_decode_fp8 as pdf
+
+    kw = dict(CHAIN_CASES[case])
+    cfg = scaled(CONFIGS[kw.pop("base")], name=case, **kw)
+    print(f"[parity] chained slots {case} P={parts} spw={spw} wg={wg}", flush=True)
+    w = build_workload(cfg, "cuda", seed=8)
+    results = []
+    for layout in ((1, 1, False), (1, spw, False), (wg, spw, True)):
+        monkeypatch.setattr(pdf, "_slot_layout", lambda *a, layout=layout, **k: layout)
+        pdf._PLAN_CACHE.clear()
+        out, _, part = launch(w, max_parts=parts, with_partials=True)
+        plan = next(reversed(pdf._PLAN_CACHE.values()))
+        assert (plan.rargs is None) == layout[2]
+        results.append((out, part))
+    pdf._PLAN_CACHE.clear()
+    out1, part1 = results[0]
+    for out2, part2 in results[1:]:
+        assert torch.equal(out1, out2)
+        for k in part1:
+            assert torch.equal(_bits(part1[k]), _bits(part2[k])), k
+    compare_outputs(w, out1, range(cfg.batch))
+    check_partials(w, part1, parts, range(cfg.batch))

@@ -491,3 +491,49 @@ def test_metadata_v1_refuses_buffers_below_the_schedule_bound():
         get_pa_metadata_v1(sq, i32(b + 1), ctx, 4, hkv, True, ptrs, wi, winfo[:-1].contiguous(), ri, rfm, rpm, **kw)
     with pytest.raises(ValueError, match="reduce_partial_map holds"):
         get_pa_metadata_v1(sq, i32(b + 1), ctx, 4, hkv, True, ptrs, wi, winfo, ri, rfm, rpm[:-1].contiguous(), **kw)
+
+
+def _shaped(batch, hq, hkv, ctx_tokens, bs=16, nb=None):
+    t = make(batch=batch, hq=hq, hkv=hkv, bs=bs, nb=nb or 8, max_blocks=ctx_tokens // bs)
+    return t
+
+
+@pytest.mark.parametrize("batch,hkv,ctx,parts,sw,expect", [
+    # c2 at the harness's 8 slots: 4 waves x 2 slots hold a (sequence, head), merged in the workgroup
+    (64, 8, 4096, 8, 0, (4, 2, True)),
+    (64, 8, 4096, 4, 0, (4, 1, True)),
+    # c4's window at 17 slots: 8 waves x 3 slots (a slot spans at most two tiles)
+    (32, 8, 32768, 17, 4096, (8, 3, True)),
+    # c3-like pages (a slot of up to 64 steps): two waves per slot, then the reduce
+    (128, 8, 32768, 8, 0, (2, 0, False)),
+    # a small batch with many short slots: workgroups per (sequence, head) would not
+    # fill the GPU, so one wave per slot
+    (8, 8, 16384, 64, 0, (1, 0, False)),
+    # too few slots for one wave each: waves split a slot's steps
+    (64, 8, 4096, 2, 0, (2, 0, False)),
+    (64, 8, 4096, 1, 0, (4, 0, False)),
+    (32, 8, 32768, 1, 4096, (8, 0, False)),
+])
+def test_slot_layout(batch, hkv, ctx, parts, sw, expect):
+    """The partition kernel's layout: the fewest waves per slot that fill 256 CUs at eight
+    waves each; chained slots when one wave per slot fills them, merged in the workgroup
+    when it holds every slot of its (sequence, kv head) within 32 steps per wave."""
+    got = pdf._slot_layout(None, batch, hkv, parts, 128, 4, False, pdf._max_slot_tokens(ctx, parts, sw, 1))
+    assert got == expect
+
+
+def test_merged_layout_plan_writes_partials_and_output():
+    """With the merged layout the partition kernel writes the caller's partials and the
+    output; no reduce launch follows."""
+    t = make(batch=64, hq=32, hkv=8, nb=20, max_blocks=256)
+    shape = (64, 8, 8, 4)
+    es, ml = torch.empty(shape), torch.empty(shape)
+    to = torch.empty(shape + (128,), dtype=torch.bfloat16)
+    p = plan(t, max_parts=8, exp_sums=es, max_logits=ml, temporary_output=to)
+    a = p.dargs
+    assert (a.waves_per_slot, a.slots_per_wave, a.direct_output) == (4, 2, 1)
+    assert p.rargs is None and [fn.__name__ for fn, _ in p.launches] == ["decode_partitions"]
+    assert a.exp_sums == es.data_ptr() and a.tmp_out == to.data_ptr() and a.output == t["output"].data_ptr()
+    # without caller partials the launcher allocates them (the workgroups merge from them)
+    p = plan(t, max_parts=8)
+    assert p.dargs.direct_output == 1 and p.rargs is None and len(p.keepalive) == 3

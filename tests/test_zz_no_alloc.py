@@ -40,8 +40,14 @@ def _noalloc(w, parts, out_dtype=torch.bfloat16, out=None, sync=True):
     a.stride_o_seq, a.stride_o_len, a.stride_o_head, a.stride_o_group = (o5.stride(i) for i in range(4))
     a.out_dtype = {torch.bfloat16: _lib.PA_FP8_BF16, torch.float16: _lib.PA_FP8_F16,
                    torch.float32: _lib.PA_FP8_F32}[out.dtype]
-    # the launcher's wave count, so both paths accumulate in the same order
-    a.waves_per_slot = pdf._waves_per_slot(q.device, cfg.batch, cfg.num_kv_heads, parts, q.shape[-1])
+    # the launcher's layout, so both paths accumulate in the same order (a merged
+    # layout's workgroups merge their own partials: direct_output with several slots)
+    max_slot = pdf._max_slot_tokens(w["block_tables"].shape[1] * cfg.block_size, parts, cfg.sliding_window,
+                                    cfg.query_length)
+    a.waves_per_slot, a.slots_per_wave, merged = pdf._slot_layout(
+        q.device, cfg.batch, cfg.num_kv_heads, parts, q.shape[-1], cfg.query_length * cfg.group_size,
+        w["value_cache"].dim() != 5, max_slot)
+    a.direct_output = 1 if merged else 0
     stream = torch.cuda.current_stream().cuda_stream
     status = _lib.LIB.pa_fp8_decode_partitions_noalloc(ctypes.byref(a), ctypes.c_void_p(stream))
     if sync:
