@@ -61,6 +61,24 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// max(a, b) as one v_max_f32 (the compiler's fmaxf adds a NaN-quieting move per
+// operand that comes from another lane; the values here are finite or -inf).
+__device__ __forceinline__ float max_raw(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// max of v over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows), with
+// the gfx950 row swaps (v_permlane16_swap / v_permlane32_swap: no lane-index
+// arithmetic, no LDS): each swap hands every lane its partner row's value.
+__device__ __forceinline__ float rows4_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float m = max_raw(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return max_raw(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // Lane J of each quad of lanes (4q .. 4q+3) to the whole quad: a DPP quad_perm
 // broadcast (a VALU move, no LDS).
 template <int J>

@@ -298,6 +298,9 @@ __device__ __forceinline__ void setup_rows(RW &rw, const DecodeParams &p, int b,
 template <int MTPW, int D>
 struct SmState {
     float m_run[MTPW], l_run[MTPW], m_top[MTPW];
+    // derived from m_run, updated only when it is raised: the exponent offset
+    // (-m_run, 0 while the row has seen no key) and the raise threshold m_run + kSlack
+    float m_neg[MTPW], m_raise[MTPW];
     f32x4 o[MTPW][D / 16];
 
     __device__ __forceinline__ void init() {
@@ -305,6 +308,8 @@ struct SmState {
         for (int mg = 0; mg < MTPW; ++mg) {
             m_run[mg] = -INFINITY;
             m_top[mg] = -INFINITY;
+            m_neg[mg] = 0.0f;
+            m_raise[mg] = -INFINITY;
             l_run[mg] = 0.0f;
 #pragma unroll
             for (int m = 0; m < D / 16; ++m) o[mg][m] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -397,40 +402,45 @@ __device__ __forceinline__ void step_qk_softmax(SmState<MTPW, D> &st, const RW &
 
 #pragma unroll
     for (int mg = 0; mg < MTPW; ++mg) {
-        float mx = -INFINITY;
+        if constexpr (PER_TOKEN) {
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-            if constexpr (PER_TOKEN) sc[mg][jt] *= kf[jt];
-            if (!interior) {
+            for (int jt = 0; jt < 4; ++jt) sc[mg][jt] *= kf[jt];
+        }
+        if (!interior) {  // one wave-uniform branch for the whole step
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int t = trow + 4 * jt + i;
                     sc[mg][jt][i] = (t >= rw.lo_n[mg] && t < rw.hi_n[mg]) ? sc[mg][jt][i] : -INFINITY;
                 }
-            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[mg][jt][i]);
         }
-        mx = fmaxf(mx, shfl_xor_f(mx, 16));
-        mx = fmaxf(mx, shfl_xor_f(mx, 32));
-        mx *= k_eff;  // k_eff > 0: the max of the scaled logits (-inf stays -inf)
-        st.m_top[mg] = fmaxf(st.m_top[mg], mx);
-        const bool raise = mx > st.m_run[mg] + kSlack;  // false while the row has seen no key
-        if (__any(raise)) {                              // wave-uniform
+        mx = rows4_max(mx) * k_eff;  // k_eff > 0: the max of the scaled logits (-inf stays -inf)
+        st.m_top[mg] = max_raw(st.m_top[mg], mx);
+        const bool raise = mx > st.m_raise[mg];  // m_run + kSlack; false while the row has seen no key
+        if (__any(raise)) {                      // wave-uniform
             const float alpha = raise ? fast_exp2(st.m_run[mg] - mx) : 1.0f;  // 0 on a row's first keys
             st.m_run[mg] = raise ? mx : st.m_run[mg];
+            st.m_neg[mg] = st.m_run[mg] == -INFINITY ? 0.0f : -st.m_run[mg];
+            st.m_raise[mg] = st.m_run[mg] + kSlack;
             st.l_run[mg] *= alpha;
 #pragma unroll
             for (int m = 0; m < D / 16; ++m) st.o[mg][m] *= alpha;
         }
-        const float m_use = st.m_run[mg] == -INFINITY ? 0.0f : st.m_run[mg];
-        float psum = 0.0f;
+        const float m_neg = st.m_neg[mg];
+        float psum;
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float pv = fast_exp2(fmaf(sc[mg][jt][i], k_eff, -m_use));
-                psum += pv;
+                const float pv = fast_exp2(fmaf(sc[mg][jt][i], k_eff, m_neg));
+                psum = (jt | i) ? psum + pv : pv;
                 sc[mg][jt][i] = pv;
             }
             if constexpr (PER_TOKEN) sc[mg][jt] *= vsr(jt);
@@ -983,6 +993,19 @@ __device__ __forceinline__ void dma16(const void *gptr, uint32_t lds_base) {
 #endif
 }
 
+// 16 bytes from sbase + voff (sbase wave-uniform, in scalar registers; voff a 32-bit
+// per-lane offset) to LDS byte address lds_base + 16 * lane: the SADDR form, whose
+// address needs no vector arithmetic.
+__device__ __forceinline__ void dma16_s(const void *sbase, uint32_t voff, uint32_t lds_base) {
+#if PA_FP8_NT_KV
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "s"(lds_base)
+                 : "memory", "m0");
+#else
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
+                 : "memory", "m0");
+#endif
+}
+
 // Wait until at most N of this wave's vector memory loads are outstanding and
 // its LDS operations are done, then meet the other waves.
 template <int N>
@@ -1013,9 +1036,13 @@ struct KvStager {
     int32_t *pages;
     const int32_t *bt_row;
     const uint8_t *kc_h, *vc_h;
-    int64_t kchunk;
+    int kchunk;
     uint32_t ring_addr;
     int h, row_len, tok_lo, last_group, last_page, nsteps, wbase, bs, tid, lane, wave;
+    bool one_page;  // every step lies in one page (issue_one_page)
+    // loop-invariant lane offsets of the one-page loads: K rows j and V rows j from the
+    // step's sub-row 0 of the page, and the lane's scale piece (in floats)
+    int k_lane[KROWS], v_lane[VROWS], s_lane;
 
     __device__ __forceinline__ void load_window(int base) {  // every wave is past its last use of the window
         wbase = base;
@@ -1030,7 +1057,43 @@ struct KvStager {
         phys = min(max(e, 0), p.num_blocks - 1);
         sub = (gs & (bs - 1)) >> 4;
     }
+    // Steps inside one page (pages of 64 tokens or more, the range starting on a step
+    // boundary) whose four groups all hold keys: one page-window read and one scalar
+    // base per cache for the step, the lanes' parts being loop-invariant offsets.
+    __device__ __forceinline__ bool issue_one_page(int q) {
+        const int t = tok_lo + q * kStep;
+        if (!one_page || t + 3 * kGroup > last_group) return false;
+        const int pg = t >> p.bs_log2;
+        if (pg - wbase >= kPageWin) load_window(pg);
+        const uint32_t sb = ring_addr + (uint32_t)((q % STAGES) * kStageBytes<D>);
+        const int e = __builtin_amdgcn_readfirstlane(pages[pg - wbase]);
+        const int64_t phys = min(max(e, 0), p.num_blocks - 1);
+        const int sub0 = (t & (bs - 1)) >> 4;  // 16-token sub-row of the step's group 0
+        const uint8_t *kb = kc_h + phys * p.s_k_block + sub0 * 256;
+        const uint8_t *vb = vc_h + phys * p.s_v_block + sub0 * (V4 ? 16 : 16 * D);
+#pragma unroll
+        for (int j = 0; j < KROWS; ++j) {
+            const int r = wave + NW * j;
+            const int g = r / CPL, c4 = r % CPL;
+            dma16_s(kb, k_lane[j], __builtin_amdgcn_readfirstlane(sb + g * kKGroupStride<D> + c4 * 1024));
+        }
+#pragma unroll
+        for (int j = 0; j < VROWS; ++j) {
+            const int r = wave + NW * j;
+            const int g = r / CPL, c4 = r % CPL;
+            dma16_s(vb, v_lane[j], __builtin_amdgcn_readfirstlane(sb + kStageV<D> + g * (16 * D) + c4 * 1024));
+        }
+        if constexpr (PER_TOKEN) {
+            if (lane < SLANES) {
+                const float *sbase = (wave * SLANES < 16 ? p.ks : p.vs) + phys * p.s_ks_block +
+                                     (int64_t)h * p.s_ks_head + sub0 * 16;
+                dma16_s(sbase, 4 * s_lane, __builtin_amdgcn_readfirstlane(sb + kStageS<D> + wave * SLANES * 16));
+            }
+        }
+        return true;
+    }
     __device__ __forceinline__ void issue(int q) {
+        if (issue_one_page(q)) return;
         const int lastg_page = min(tok_lo + q * kStep + 48, last_group) >> p.bs_log2;
         if (lastg_page - wbase >= kPageWin) load_window((tok_lo + q * kStep) >> p.bs_log2);
         const uint32_t sb = ring_addr + (uint32_t)((q % STAGES) * kStageBytes<D>);
@@ -1104,7 +1167,7 @@ __device__ __forceinline__ void init_stager(KvStager<NW, STAGES, PER_TOKEN, D, V
     sg.kc_h = p.kc + (int64_t)h * p.s_k_head;
     sg.vc_h = p.vc + (int64_t)h * p.s_v_head;
     sg.bs = 1 << p.bs_log2;
-    sg.kchunk = (int64_t)sg.bs * 16;
+    sg.kchunk = sg.bs * 16;
     sg.tok_lo = tok_lo;
     const int ngroups = (tok_hi - tok_lo + kGroup - 1) / kGroup;
     sg.nsteps = (ngroups + 3) / 4;
@@ -1113,6 +1176,17 @@ __device__ __forceinline__ void init_stager(KvStager<NW, STAGES, PER_TOKEN, D, V
     sg.tid = threadIdx.x;
     sg.lane = threadIdx.x & 63;
     sg.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    using S = KvStager<NW, STAGES, PER_TOKEN, D, V4>;
+    sg.one_page = sg.bs >= kStep && (tok_lo & (kStep - 1)) == 0;
+#pragma unroll
+    for (int j = 0; j < S::KROWS; ++j) {
+        const int r = sg.wave + NW * j;
+        const int g = r / S::CPL, c4 = r % S::CPL;
+        sg.k_lane[j] = (4 * c4 + (sg.lane >> 4)) * sg.kchunk + g * 256 + (sg.lane & 15) * 16;
+        sg.v_lane[j] = g * (V4 ? 16 : 16 * D) + (64 * c4 + sg.lane) * (V4 ? sg.bs : 16);
+    }
+    const int piece = sg.wave * S::SLANES + min(sg.lane, S::SLANES - 1);
+    sg.s_lane = ((piece & 15) >> 2) * 16 + 4 * (piece & 3);
     sg.load_window(tok_lo >> p.bs_log2);
 }
 
@@ -1370,11 +1444,15 @@ __global__ __launch_bounds__((kThreads<RS, NS>), (kWavesFor<MTPW, NS, D>)) void 
         r.pbase = ((const cint *)w.partition_indptr)[bb];
         return r;
     };
+    // (The LDS-staged layout reads each work's fields when it starts: the next work's
+    // fields would stay live in scalar registers through every step, where that
+    // layout's step has none to spare.)
+    constexpr bool kAhead = NS > 0;
     Fields nxt{};
-    if (wbeg < wend) nxt = fields(wbeg);
+    if (kAhead && wbeg < wend) nxt = fields(wbeg);
     for (int wi = wbeg; wi < wend; ++wi) {
-        const Fields f = nxt;
-        if (wi + 1 < wend) nxt = fields(wi + 1);
+        const Fields f = kAhead ? nxt : fields(wi);
+        if (kAhead && wi + 1 < wend) nxt = fields(wi + 1);
         const int b = f.b, pidx = f.pidx, qo_start = f.qo_start;
         const int h = f.qh_start / p.g;
         if (b < 0 || b >= w.batch || h >= w.num_kv_heads) continue;
