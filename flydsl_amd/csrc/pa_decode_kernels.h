@@ -1228,7 +1228,8 @@ __device__ __forceinline__ void attend_range_staged(const DecodeParams &p, const
         __builtin_amdgcn_s_setprio(3);
         if (n + kStages - 1 < sg.nsteps) sg.issue(n + kStages - 1);
         __builtin_amdgcn_s_setprio(0);
-        const uint8_t *sk = sg.stage(n);
+        // the stage's byte offset as one scalar, so each LDS address below is one add
+        const uint8_t *sk = s_ring + __builtin_amdgcn_readfirstlane((n % kStages) * kStageBytes<D>);
         uint4 kr[4][kKChunks<D>];
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
