@@ -18,8 +18,8 @@ are rotated step to step so the working set (>= 1.5 GiB for c2) defeats the
                    back-to-back launches of it alone), never longer than the step
   cpu_baseline   = the reference's torch path (restated with torch CPU ops) timed
                    on this host's cores over 3 full steps of the workload (median)
-  configs        = c3, c4 and c5 measured the same way in the same run, with
-                   --config-steps timed steps each
+  configs        = c3, c4 and c5 measured the same way in the same run (the
+                   same warmup, --config-steps or --steps timed steps each)
 """
 
 from __future__ import annotations
@@ -60,7 +60,8 @@ def _parse():
     ap.add_argument("--rope-tokens", type=int, default=16384, help="tokens per writer launch (--path rope_cache)")
     ap.add_argument("--configs", default="c3,c4,c5",
                     help="other configurations measured in the same run (the line's `configs` block; '' for none)")
-    ap.add_argument("--config-steps", type=int, default=50, help="timed steps of each configuration in --configs")
+    ap.add_argument("--config-steps", type=int, default=0,
+                    help="timed steps of each configuration in --configs (0: as many as --steps)")
     return ap.parse_args()
 
 
@@ -631,9 +632,10 @@ def main():
     # budget (inputs resident in HBM, metadata outside the timed steps, as above)
     configs = {}
     extra = [c for c in (args.configs.split(",") if args.configs else []) if c and c != cfg.name]
+    config_steps = args.config_steps or args.steps
     for name in extra:
         c = CONFIGS[name]
-        o = measure_decode(torch, c, dev, args.config_steps, min(args.warmup, 10), copies=args.copies,
+        o = measure_decode(torch, c, dev, config_steps, args.warmup, copies=args.copies,
                            use_metadata=not args.no_metadata, extras=False)
         o.pop("works")
         torch.cuda.empty_cache()
@@ -661,7 +663,7 @@ def main():
                 "us_per_step": round(o["ref_us"], 2),
                 "kv_gbs": round(o["kvb"] / (o["ref_us"] * 1e-6) / 1e9, 1),
             },
-            "steps": args.config_steps,
+            "steps": config_steps,
         }
 
     us_step = r["us_step"]
