@@ -132,42 +132,124 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     return __builtin_bit_cast(uint16_t, h);
 }
 
-// Log-sum-exp merge of the P partials of one query row: lane owns head dims
-// 2*lane, 2*lane+1 of each 128-dim block (a0 / a1 per block; NB blocks).
-// es / ml point at the row's exp_sum / max_logit of slot 0, to at its bf16 partial
-// row of slot 0.  out = sum_z w_z to_z with w_z = s_z e^(m_z - M) / sum_z s_z e^(m_z - M),
-// M = max_z m_z (kernels/pa_decode_swa.py:954-1130).  Both the reduce kernel and the
-// partition kernel's in-workgroup merge run this, so their outputs are identical.
+// Log-sum-exp merge of the P partials of R query rows (the first nrows <= R of them):
+// lane owns head dims 2*lane, 2*lane+1 of each 128-dim block (a0 / a1 per row and
+// block; NB blocks).  es / ml point at row 0's exp_sum / max_logit of slot 0 (row q at
+// + q * s_es_row), to at row 0's bf16 partial row of slot 0 (row q at + q * s_to_row).
+// out = sum_z w_z to_z with w_z = s_z e^(m_z - M) / sum_z s_z e^(m_z - M), M = max_z m_z
+// (kernels/pa_decode_swa.py:954-1130).  Both the reduce kernel and the chained
+// kernel's in-workgroup merge run this, so their outputs are identical; each row's
+// arithmetic is the same whatever R and nrows are, the rows only share the memory
+// round trips.  Each slot's weight is computed in its own lane and broadcast with
+// readlane; the rows of kMergeChunk slots with nonzero weights are loaded together
+// (one memory round trip per chunk) and added in slot order.  A slot of weight 0 (an
+// empty slot, whose row may hold anything) is neither loaded nor added.
+constexpr int kMergeChunk = 8;
+template <int NB, int R>
+__device__ __forceinline__ void lse_merge_rows(const float *es, const float *ml, const uint16_t *to, int64_t s_es_row,
+                                               int64_t s_to_row, int64_t s_es_part, int64_t s_to_part, int P,
+                                               int head_dim, int lane, int nrows, float (&a0)[R][NB],
+                                               float (&a1)[R][NB]) {
+    constexpr int CH = R > 1 ? kMergeChunk / 2 : kMergeChunk;  // slots per chunk (registers: R * CH * NB)
+    // the first 64 slots' exp_sums and max_logits, one per lane, loaded once for all
+    // three passes (later slots are read again where a pass needs them)
+    float es0[R], ml0[R], Ms[R], inv[R];
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+        const bool in = q < nrows && lane < P;
+        es0[q] = in ? es[q * s_es_row + lane * s_es_part] : 0.f;
+        ml0[q] = in ? ml[q * s_es_row + lane * s_es_part] : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+        Ms[q] = 0.f;
+        if (q >= nrows) continue;
+        const float *mq = ml + q * s_es_row;
+        float mloc = -INFINITY;
+        if (lane < P) mloc = fmaxf(mloc, ml0[q]);
+        for (int z = lane + 64; z < P; z += 64) mloc = fmaxf(mloc, mq[z * s_es_part]);
+#pragma unroll
+        for (int sh = 32; sh >= 1; sh >>= 1) mloc = fmaxf(mloc, shfl_xor_f(mloc, sh));
+        Ms[q] = mloc == -INFINITY ? 0.0f : mloc;
+    }
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+        inv[q] = 0.f;
+        if (q >= nrows) continue;
+        const float *eq = es + q * s_es_row, *mq = ml + q * s_es_row;
+        float wl = 0.f;
+        if (lane < P) wl += es0[q] * fast_exp2((ml0[q] - Ms[q]) * kLog2e);
+        for (int z = lane + 64; z < P; z += 64) {
+            const float mz = mq[z * s_es_part];
+            wl += eq[z * s_es_part] * fast_exp2((mz - Ms[q]) * kLog2e);
+        }
+#pragma unroll
+        for (int sh = 32; sh >= 1; sh >>= 1) wl += shfl_xor_f(wl, sh);
+        inv[q] = wl > 0.f ? 1.0f / wl : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < R; ++q)
+#pragma unroll
+        for (int k = 0; k < NB; ++k) a0[q][k] = a1[q][k] = 0.f;
+    for (int z0 = 0; z0 < P; z0 += 64) {
+        const int z = z0 + lane, n = min(P - z0, 64);
+        float wz[R];
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+            const float *eq = es + q * s_es_row, *mq = ml + q * s_es_row;
+            const float ez = z0 == 0 ? es0[q] : (z < P ? eq[z * s_es_part] : 0.f);
+            const float mz = z0 == 0 ? ml0[q] : (z < P ? mq[z * s_es_part] : 0.f);
+            wz[q] = q < nrows && z < P ? ez * fast_exp2((mz - Ms[q]) * kLog2e) * inv[q] : 0.f;
+        }
+        for (int j0 = 0; j0 < n; j0 += CH) {
+            float w[R][CH];
+            uint32_t two[R][CH][NB];
+#pragma unroll
+            for (int q = 0; q < R; ++q)
+#pragma unroll
+                for (int j = 0; j < CH; ++j)
+                    w[q][j] = q < nrows && j0 + j < n
+                                  ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wz[q]),
+                                                                                        j0 + j))
+                                  : 0.f;
+#pragma unroll
+            for (int q = 0; q < R; ++q)
+#pragma unroll
+                for (int j = 0; j < CH; ++j)
+#pragma unroll
+                    for (int k = 0; k < NB; ++k)
+                        two[q][j][k] = w[q][j] != 0.f && 2 * lane + 128 * k < head_dim
+                                           ? *reinterpret_cast<const uint32_t *>(to + q * s_to_row +
+                                                                                 (z0 + j0 + j) * s_to_part + 128 * k +
+                                                                                 2 * lane)
+                                           : 0u;
+#pragma unroll
+            for (int q = 0; q < R; ++q)
+#pragma unroll
+                for (int j = 0; j < CH; ++j) {
+                    if (w[q][j] == 0.f) continue;
+#pragma unroll
+                    for (int k = 0; k < NB; ++k) {
+                        if (2 * lane + 128 * k >= head_dim) continue;
+                        a0[q][k] += w[q][j] * bf16_bits_to_f32(uint16_t(two[q][j][k] & 0xffffu));
+                        a1[q][k] += w[q][j] * bf16_bits_to_f32(uint16_t(two[q][j][k] >> 16));
+                    }
+                }
+        }
+    }
+}
+
+// One row of lse_merge_rows.
 template <int NB>
 __device__ __forceinline__ void lse_merge_row(const float *es, const float *ml, const uint16_t *to, int64_t s_es_part,
                                               int64_t s_to_part, int P, int head_dim, int lane, float (&a0)[NB],
                                               float (&a1)[NB]) {
-    float mloc = -INFINITY;
-    for (int z = lane; z < P; z += 64) mloc = fmaxf(mloc, ml[z * s_es_part]);
+    float r0[1][NB], r1[1][NB];
+    lse_merge_rows<NB, 1>(es, ml, to, 0, 0, s_es_part, s_to_part, P, head_dim, lane, 1, r0, r1);
 #pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) mloc = fmaxf(mloc, shfl_xor_f(mloc, sh));
-    const float Ms = mloc == -INFINITY ? 0.0f : mloc;
-    float wl = 0.f;
-    for (int z = lane; z < P; z += 64) {
-        const float mz = ml[z * s_es_part];
-        wl += es[z * s_es_part] * fast_exp2((mz - Ms) * kLog2e);
-    }
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) wl += shfl_xor_f(wl, sh);
-    const float inv = wl > 0.f ? 1.0f / wl : 0.0f;
-#pragma unroll
-    for (int k = 0; k < NB; ++k) a0[k] = a1[k] = 0.f;
-    for (int z = 0; z < P; ++z) {
-        const float w = es[z * s_es_part] * fast_exp2((ml[z * s_es_part] - Ms) * kLog2e) * inv;
-        if (w != 0.f) {
-#pragma unroll
-            for (int k = 0; k < NB; ++k) {
-                if (2 * lane + 128 * k >= head_dim) continue;
-                const uint32_t two = *reinterpret_cast<const uint32_t *>(to + z * s_to_part + 128 * k + 2 * lane);
-                a0[k] += w * bf16_bits_to_f32(uint16_t(two & 0xffffu));
-                a1[k] += w * bf16_bits_to_f32(uint16_t(two >> 16));
-            }
-        }
+    for (int k = 0; k < NB; ++k) {
+        a0[k] = r0[0][k];
+        a1[k] = r1[0][k];
     }
 }
 

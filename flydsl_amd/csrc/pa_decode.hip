@@ -60,6 +60,9 @@ struct ReduceParams {
     int64_t s_es_seq, s_es_head, s_es_part;
     int64_t s_to_seq, s_to_head, s_to_part, s_to_group;
     int32_t g, max_parts, head_dim;
+    int32_t eqgs;        // query rows per (sequence, kv head): ql * g
+    int32_t rpw;         // rows per wave
+    int32_t row_groups;  // workgroups per (sequence, kv head): ceil(eqgs / (waves per workgroup * rpw))
 };
 
 struct ReduceV1Params {
@@ -271,39 +274,66 @@ __global__ __launch_bounds__(256) void pa_reduce_v1_rows_kernel(const ReduceV1Pa
         p.final_lse[orow * p.s_lse_row + hd * p.s_lse_head] = wl > 0.f ? Ms + __logf(wl) : -INFINITY;
 }
 
-// Log-sum-exp merge of the P partials of one (sequence, kv head, query row):
-// one wave, lane owns head dims 2*lane and 2*lane+1 of each 128-dim block
-// (kernels/pa_decode_swa.py:954-1130).
-template <int OUT>
-__global__ __launch_bounds__(64) void pa_lse_reduce_kernel(const ReduceParams p) {
-    const int lane = threadIdx.x;
-    const int b = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
-    const float *es = p.es + b * p.s_es_seq + h * p.s_es_head + r;
-    const float *ml = p.ml + b * p.s_es_seq + h * p.s_es_head + r;
-    const uint16_t *to = p.to + b * p.s_to_seq + h * p.s_to_head + r * p.s_to_group;
-    constexpr int NB = kMaxHeadDim / 128;
+// Log-sum-exp merge of the P partials of each (sequence, kv head, query row)
+// (kernels/pa_decode_swa.py:954-1130): one wave merges p.rpw consecutive rows
+// (lse_merge_rows, their loads in flight together; R = p.rpw, 1 or kReduceMaxRows),
+// lane owning head dims 2*lane and 2*lane+1 of each of the NB 128-dim blocks.  A workgroup holds kReduceWaves such waves of one
+// (sequence, kv head), and consecutive workgroups hold consecutive rows (grid x =
+// sequence * row groups + row group), so the workgroups resident together read
+// neighbouring pieces of each slot's partial block.  rpw > 1 when the rows outnumber
+// what the GPU holds at once: fewer waves, each with several rows' loads in flight.
+constexpr int kReduceWaves = 4;
+constexpr int kReduceMaxRows = 2;  // rows per wave, at most
+// waves the GPU keeps resident at once for this kernel, about (256 CUs x 32)
+constexpr int64_t kReduceResidentWaves = 8192;
+template <int OUT, int NB, int R>
+__global__ __launch_bounds__(kReduceWaves * 64) void pa_lse_reduce_kernel(const ReduceParams p) {
+    const int lane = threadIdx.x & 63;
+    const int b = blockIdx.x / p.row_groups, h = blockIdx.y;
+    const int r0 = ((blockIdx.x - b * p.row_groups) * kReduceWaves + (threadIdx.x >> 6)) * p.rpw;
+    if (r0 >= p.eqgs) return;  // the last group's spare waves (no barrier follows)
+    const int nrows = min(R, p.eqgs - r0);
+    const float *es = p.es + b * p.s_es_seq + h * p.s_es_head + r0;
+    const float *ml = p.ml + b * p.s_es_seq + h * p.s_es_head + r0;
+    const uint16_t *to = p.to + b * p.s_to_seq + h * p.s_to_head + r0 * p.s_to_group;
     bool live[NB];
 #pragma unroll
     for (int k = 0; k < NB; ++k) live[k] = 2 * lane + 128 * k < p.head_dim;
-    float a0[NB], a1[NB];
-    lse_merge_row<NB>(es, ml, to, p.s_es_part, p.s_to_part, p.max_parts, p.head_dim, lane, a0, a1);
-    const int qi = r / p.g, gi = r - (r / p.g) * p.g;
-    const int64_t off = b * p.s_o_seq + qi * p.s_o_len + h * p.s_o_head + gi * p.s_o_group + 2 * lane;
+    float a0[R][NB], a1[R][NB];
+    lse_merge_rows<NB, R>(es, ml, to, 1, p.s_to_group, p.s_es_part, p.s_to_part, p.max_parts, p.head_dim, lane,
+                          nrows, a0, a1);
 #pragma unroll
-    for (int k = 0; k < NB; ++k) {
-        if (!live[k]) continue;
-        if constexpr (OUT == PA_FP8_F32) {
-            float *o = reinterpret_cast<float *>(p.out) + off + 128 * k;
-            *reinterpret_cast<float2 *>(o) = make_float2(a0[k], a1[k]);
-        } else if constexpr (OUT == PA_FP8_F16) {
-            uint16_t *o = reinterpret_cast<uint16_t *>(p.out) + off + 128 * k;
-            *reinterpret_cast<uint32_t *>(o) = uint32_t(f32_to_f16_bits(a0[k])) | (uint32_t(f32_to_f16_bits(a1[k])) << 16);
-        } else {
-            uint16_t *o = reinterpret_cast<uint16_t *>(p.out) + off + 128 * k;
-            *reinterpret_cast<uint32_t *>(o) =
-                uint32_t(f32_to_bf16_bits(a0[k])) | (uint32_t(f32_to_bf16_bits(a1[k])) << 16);
+    for (int q = 0; q < R; ++q) {
+        if (q >= nrows) break;
+        const int r = r0 + q;
+        const int qi = r / p.g, gi = r - (r / p.g) * p.g;
+        const int64_t off = b * p.s_o_seq + qi * p.s_o_len + h * p.s_o_head + gi * p.s_o_group + 2 * lane;
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            if (!live[k]) continue;
+            if constexpr (OUT == PA_FP8_F32) {
+                float *o = reinterpret_cast<float *>(p.out) + off + 128 * k;
+                *reinterpret_cast<float2 *>(o) = make_float2(a0[q][k], a1[q][k]);
+            } else if constexpr (OUT == PA_FP8_F16) {
+                uint16_t *o = reinterpret_cast<uint16_t *>(p.out) + off + 128 * k;
+                *reinterpret_cast<uint32_t *>(o) =
+                    uint32_t(f32_to_f16_bits(a0[q][k])) | (uint32_t(f32_to_f16_bits(a1[q][k])) << 16);
+            } else {
+                uint16_t *o = reinterpret_cast<uint16_t *>(p.out) + off + 128 * k;
+                *reinterpret_cast<uint32_t *>(o) =
+                    uint32_t(f32_to_bf16_bits(a0[q][k])) | (uint32_t(f32_to_bf16_bits(a1[q][k])) << 16);
+            }
         }
     }
+}
+
+// The instance for the head dim's 128-dim blocks (two: above 128) and the rows per wave.
+template <int OUT>
+void launch_lse_reduce(bool two, bool many, dim3 grid, dim3 block, hipStream_t s, const ReduceParams &p) {
+    if (two && many) hipLaunchKernelGGL((pa_lse_reduce_kernel<OUT, 2, kReduceMaxRows>), grid, block, 0, s, p);
+    else if (two) hipLaunchKernelGGL((pa_lse_reduce_kernel<OUT, 2, 1>), grid, block, 0, s, p);
+    else if (many) hipLaunchKernelGGL((pa_lse_reduce_kernel<OUT, 1, kReduceMaxRows>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((pa_lse_reduce_kernel<OUT, 1, 1>), grid, block, 0, s, p);
 }
 
 bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
@@ -593,12 +623,22 @@ int pa_fp8_lse_reduce(const pa_fp8_reduce_args *a, void *stream) {
     p.g = a->query_group_size;
     p.max_parts = a->max_context_partition_num;
     p.head_dim = a->head_dim;
-    const dim3 grid(a->batch_size, a->num_kv_heads, (unsigned)eqgs);
+    p.eqgs = (int)eqgs;
+    // one row per wave while the rows fit in about two rounds of resident waves
+    // (kReduceResidentWaves), else kReduceMaxRows rows per wave
+    const int64_t rows = (int64_t)a->batch_size * a->num_kv_heads * eqgs;
+    p.rpw = rows > 2 * kReduceResidentWaves ? kReduceMaxRows : 1;
+    const int per_group = kReduceWaves * p.rpw;
+    p.row_groups = (int)((eqgs + per_group - 1) / per_group);
+    if ((int64_t)a->batch_size * p.row_groups > 0x7fffffffLL) return PA_FP8_ERR_SHAPE;
+    const dim3 grid((unsigned)(a->batch_size * p.row_groups), a->num_kv_heads);
+    const dim3 block(kReduceWaves * 64);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const bool two = a->head_dim > 128, many = p.rpw > 1;
     switch (a->out_dtype) {
-    case PA_FP8_F32: hipLaunchKernelGGL(pa_lse_reduce_kernel<PA_FP8_F32>, grid, dim3(64), 0, s, p); break;
-    case PA_FP8_F16: hipLaunchKernelGGL(pa_lse_reduce_kernel<PA_FP8_F16>, grid, dim3(64), 0, s, p); break;
-    default: hipLaunchKernelGGL(pa_lse_reduce_kernel<PA_FP8_BF16>, grid, dim3(64), 0, s, p); break;
+    case PA_FP8_F32: launch_lse_reduce<PA_FP8_F32>(two, many, grid, block, s, p); break;
+    case PA_FP8_F16: launch_lse_reduce<PA_FP8_F16>(two, many, grid, block, s, p); break;
+    default: launch_lse_reduce<PA_FP8_BF16>(two, many, grid, block, s, p); break;
     }
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + (int)err;
