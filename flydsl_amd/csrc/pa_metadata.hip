@@ -460,19 +460,17 @@ __device__ bool pack_schedule(const MetaParams &p, const int S, const bool equal
     if (t == 0) s_WI[nspk] = W;
     __syncthreads();
     if ((long long)p.nhk * W > p.max_work || T > p.max_split_tiles) return give_up();  // within bounds by construction
-    // work_info rows of every head
-    auto put = [&](int row, int b, int ploc, int k0, int k1) {
-        const int qs = s_sq[b], qe = s_sq[b + 1];
-        const int4 lo = make_int4(b, ploc, qs, qe);
-        for (int kh = 0; kh < p.nhk; ++kh) {
-            const int32_t qhr = (int32_t)((((unsigned)(kh + 1) * (unsigned)p.gqa) << 16) |
-                                          (((unsigned)kh * (unsigned)p.gqa) & 0xFFFFu));
+    // work_info rows: one thread per (head, bin rank), so the heads' rows are written in
+    // parallel rather than one after another
+    for (int i = t; i < p.nhk * nspk; i += kParThreads) {
+        const int kh = i / nspk, j = i - kh * nspk;
+        const int32_t qhr = (int32_t)((((unsigned)(kh + 1) * (unsigned)p.gqa) << 16) |
+                                      (((unsigned)kh * (unsigned)p.gqa) & 0xFFFFu));
+        auto put = [&](int row, int b, int ploc, int k0, int k1) {
             int4 *w = reinterpret_cast<int4 *>(p.work_info) + 2 * ((long long)kh * W + row);
-            w[0] = lo;
+            w[0] = make_int4(b, ploc, s_sq[b], s_sq[b + 1]);
             w[1] = make_int4(s_P[b] + k0, s_P[b] + k1, 0, qhr);
-        }
-    };
-    for (int j = t; j < nspk; j += kParThreads) {
+        };
         int row = s_WI[s_bo[j]];
         if (j < m) {
             const int b = s_ord[j];
@@ -675,20 +673,23 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
         }
         return lo;
     };
-    // first bin and works of each batch, then the works, split works and split
-    // batches before each batch (block scans)
+    // first bin and works of each batch, one batch per thread (the bin searches of all
+    // batches run side by side; s_W holds the work counts until the scan below
+    // replaces them), then the works, split works and split batches before each batch
+    // (block scans over four consecutive batches per thread)
+    for (int b = t; b < p.nb; b += kParThreads) {
+        const int pb = s_P[b], pe = s_P[b + 1];
+        const int fb = pe > pb ? bin_of(pb) : (pb == 0 ? 0 : bin_of(pb - 1));
+        s_F[b] = fb;
+        s_W[b] = pe > pb ? bin_of(pe - 1) - fb + 1 : 1;
+    }
+    __syncthreads();
     int w4[4], l4[4], g4[4];
     int wl = 0, ll = 0, gl = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int b = 4 * t + i;
-        int nw = 0;
-        if (b < p.nb) {
-            const int pb = s_P[b], pe = s_P[b + 1];
-            const int fb = pe > pb ? bin_of(pb) : (pb == 0 ? 0 : bin_of(pb - 1));
-            nw = pe > pb ? bin_of(pe - 1) - fb + 1 : 1;
-            s_F[b] = fb;
-        }
+        const int nw = b < p.nb ? s_W[b] : 0;  // read by every thread before scan_quad's first barrier
         w4[i] = nw;
         l4[i] = nw > 1 ? nw : 0;
         g4[i] = nw > 1 ? 1 : 0;
@@ -721,26 +722,26 @@ __global__ __launch_bounds__(kParThreads) void pa_metadata_par_kernel(const Meta
     auto works_of = [&](int b) { return min(max(s_W[b + 1] - s_W[b], 0), nspk); };
     const bool overflow = (long long)p.nhk * W > p.max_work || Lt > p.max_split_tiles;
 
-    // work_info rows of every head
-    for (int b = t; b < p.nb; b += kParThreads) {
+    // work_info rows: one thread per (head, batch), so the heads' rows are written in
+    // parallel rather than one after another
+    for (int i = t; i < p.nhk * p.nb; i += kParThreads) {
+        const int k = i / p.nb, b = i - k * p.nb;
         const int pb = s_P[b], pe = s_P[b + 1];
         const int c0 = s_F[b], nw = works_of(b);
         const int wb = s_W[b], lb = s_L[b];
         const int qs = sq_at(p, b), qe = sq_at(p, b + 1);
+        const int32_t qhr = (int32_t)((((unsigned)(k + 1) * (unsigned)p.gqa) << 16) |
+                                      (((unsigned)k * (unsigned)p.gqa) & 0xFFFFu));
         for (int j = 0; j < nw; ++j) {
+            const long long row = (long long)k * W + wb + j;
+            if (row >= p.max_work) continue;
             const int c = c0 + j;
             const int ks = pe > pb ? max(pb, Qs(c)) : pb;
             const int ke = pe > pb ? min(pe, Qs(c + 1)) : pb;
             const int ploc = nw > 1 ? p.ql * (lb + j) : -1;
-            for (int k = 0; k < p.nhk; ++k) {
-                const long long row = (long long)k * W + wb + j;
-                if (row >= p.max_work) continue;
-                const int32_t qhr = (int32_t)((((unsigned)(k + 1) * (unsigned)p.gqa) << 16) |
-                                              (((unsigned)k * (unsigned)p.gqa) & 0xFFFFu));
-                int4 *w = reinterpret_cast<int4 *>(p.work_info) + 2 * row;
-                w[0] = make_int4(b, ploc, qs, qe);
-                w[1] = make_int4(ks, ke, 0, qhr);
-            }
+            int4 *w = reinterpret_cast<int4 *>(p.work_info) + 2 * row;
+            w[0] = make_int4(b, ploc, qs, qe);
+            w[1] = make_int4(ks, ke, 0, qhr);
         }
     }
     // work_indptr: entry k*nspk + c + 1 = k*W + works of head 0 in bins <= c
