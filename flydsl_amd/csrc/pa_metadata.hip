@@ -313,9 +313,6 @@ __device__ bool pack_schedule(const MetaParams &p, const int S, const bool equal
         for (int i = tid; i < n; i += kParThreads / 2) v[i] = (v[i] << 12) | (4095 - i);
         for (int i = tid; i < 16; i += kParThreads / 2) v[n + i] = -1;  // the padding never counts
     };
-    if (t < kParThreads / 2) make_keys(s_Pv, nb, t);
-    else make_keys(s_Qv, nspk, t - kParThreads / 2);
-    __syncthreads();
     auto count = [&](const int32_t *v, int n, int32_t *out, int tid) {
         int tpe = 1;
         while (tpe < 64 && tpe * 2 * n <= kParThreads / 2) tpe <<= 1;
@@ -338,12 +335,28 @@ __device__ bool pack_schedule(const MetaParams &p, const int S, const bool equal
             if (part == 0 && e < n) out[r] = e;
         }
     };
-    if (t < kParThreads / 2) count(s_Pv, nb, s_ord, t);
-    else count(s_Qv, nspk, s_bo, t - kParThreads / 2);
-    __syncthreads();
-    for (int i = t; i < nb; i += kParThreads) s_Pv[i] >>= 12;  // the values again
-    for (int i = t; i < nspk; i += kParThreads) s_Qv[i] >>= 12;
-    __syncthreads();
+    auto rank_all = [&]() {
+        if (t < kParThreads / 2) make_keys(s_Pv, nb, t);
+        else make_keys(s_Qv, nspk, t - kParThreads / 2);
+        __syncthreads();
+        if (t < kParThreads / 2) count(s_Pv, nb, s_ord, t);
+        else count(s_Qv, nspk, s_bo, t - kParThreads / 2);
+        __syncthreads();
+        for (int i = t; i < nb; i += kParThreads) s_Pv[i] >>= 12;  // the values again
+        for (int i = t; i < nspk; i += kParThreads) s_Qv[i] >>= 12;
+        __syncthreads();
+    };
+    if (equal_ctx) {
+        // every sequence has the same partitions and the quotas are even (no weights
+        // apply to equal contexts), bins [0, S % bins) one partition above the rest:
+        // both orders are the identity, so nothing is ranked
+        for (int i = t; i < nb; i += kParThreads) s_ord[i] = i;
+        for (int i = t; i < nspk; i += kParThreads) s_bo[i] = i;
+        __syncthreads();
+    } else {
+        rank_all();
+    }
+
     const int m = min(nspk, nb);
     for (int k = t; k < m; k += kParThreads)  // every rank k < m fits its bin
         if (s_Pv[s_ord[k]] > s_Qv[s_bo[k]]) s_flag[0] = 1;

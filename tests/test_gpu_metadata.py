@@ -235,6 +235,25 @@ def test_device_packing_schedule_matches_oracle(seed):
         np.testing.assert_array_equal(op.metadata_valid_prefixes(got0)[key], val, err_msg=key)
 
 
+@pytest.mark.parametrize("b", [1, 24, 48, 97, 700])
+def test_device_packing_schedule_equal_contexts(b):
+    """Equal context lengths through the packing schedule with dispatch-round weights set
+    (the scheduler then knows the lengths are equal, keeps even quotas and takes both
+    rank orders as the identity): bit-exact with the oracle's packing schedule, with
+    fewer, as many and more sequences than bins per head."""
+    nhk, nspk, weights, ql, gqa = 4, 48, [115, 107, 100], 2, 4
+    ctx = [3000 + 7 * b] * b
+    sq = [i * ql for i in range(b + 1)]
+    ref = op.get_pa_metadata_packed(sq, ctx, gqa, nhk, nhk * nspk, 256, ql, quota_of=None)
+    if ref is None:
+        ref = op.get_pa_metadata_v1(sq, ctx, gqa, nhk, nhk * nspk, 256, ql, quota_of=None)
+    got, count = run_device_schedule(ctx, ql, gqa, nhk, nspk, 256, weights, True)
+    got["num_reduce_groups"] = ref["num_reduce_groups"]
+    for key, val in op.metadata_valid_prefixes(ref).items():
+        np.testing.assert_array_equal(op.metadata_valid_prefixes(got)[key], val, err_msg=key)
+    assert count == int(ref["reduce_indptr"][-1])
+
+
 def _metadata_for(name):
     from flydsl_amd import get_pa_metadata
     from flydsl_amd.workloads import CONFIGS, context_lengths_for
