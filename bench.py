@@ -439,6 +439,20 @@ def _kernel_alone_ms(torch, plans, j, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
+def _reference_entry(o):
+    """The ``reference_default_partitions`` object of one measured configuration."""
+    return {
+        "max_context_partition_num": o["ref_parts"],
+        "call": "the reference harness's call: get_pa_metadata's schedule (none with a sliding window), "
+                "max_context_partition_num from get_recommended_splits, partials passed only with a "
+                "sliding window (tests/kernels/test_pa.py:838-895)",
+        "path": o["ref_tag"],
+        "us_per_step": round(o["ref_us"], 2),
+        "kv_gbs": round(o["kvb"] / (o["ref_us"] * 1e-6) / 1e9, 1),
+        "without_metadata_us_per_step": round(o["ref_nomd_us"], 2),
+    }
+
+
 def _reference_parts(cfg):
     """The partition count the reference harness passes (tests/kernels/test_pa.py:852-856
     calls get_recommended_splits; 8 for the small-block configs, 17 for c4's window)."""
@@ -520,10 +534,34 @@ def measure_decode(torch, cfg, dev, steps, warmup, copies=3, max_parts=0, use_me
         kbytes = _partition_kernel_bytes(cfg, ctx, used_parts)
     achieved = kbytes / (k_us * 1e-6) / 1e9
 
-    # ---- the reference harness's explicit partition count on the partition kernel
-    # (no metadata: the reference's small-block route ignores it)
+    # ---- the reference harness's own call (tests/kernels/test_pa.py:838-895): the
+    # get_pa_metadata schedule, max_context_partition_num from get_recommended_splits,
+    # and caller-allocated partials only with a sliding window.  Beside it, the same
+    # partition count without metadata: the partition route, which is what the
+    # reference's small-block launcher itself runs (it ignores the metadata).
     ref_parts = _reference_parts(cfg)
-    ref_us = _timed(torch, lambda i: step(i, md=None, parts=ref_parts), steps, warmup)[0] * 1e3
+    ref_partials = {}
+    if cfg.sliding_window:
+        eqgs = cfg.query_length * cfg.group_size
+        shape = (cfg.batch, cfg.num_kv_heads, ref_parts, eqgs)
+        ref_partials = {"exp_sums": torch.empty(shape, dtype=torch.float32, device=dev),
+                        "max_logits": torch.empty(shape, dtype=torch.float32, device=dev),
+                        "temporary_output": torch.empty(*shape, cfg.head_dim, dtype=out.dtype, device=dev)}
+
+    def harness_step(i):
+        w = works[i % len(works)]
+        return pa_decode_ps_launch(
+            out, w["query"], w["key_cache"], w["value_cache"], w["context_lengths"], w["kv_page_indices"],
+            w["kv_indptr"], scale, w["key_scale"], w["value_scale"], sliding_window=cfg.sliding_window,
+            metadata=metadata, block_tables=w["block_tables"], max_context_partition_num=ref_parts, **ref_partials,
+        )
+
+    ref_tag = harness_step(0)
+    ref_us = _timed(torch, harness_step, steps, warmup)[0] * 1e3
+    ref_nomd_us = ref_us
+    if metadata is not None:
+        ref_nomd_us = _timed(torch, lambda i: step(i, md=None, parts=ref_parts), steps, warmup)[0] * 1e3
+    del ref_partials
 
     others = {}
     if extras:
@@ -563,6 +601,8 @@ def measure_decode(torch, cfg, dev, steps, warmup, copies=3, max_parts=0, use_me
         "traffic": traffic,
         "ref_parts": ref_parts,
         "ref_us": ref_us,
+        "ref_tag": ref_tag,
+        "ref_nomd_us": ref_nomd_us,
         "others": others,
     }
     return res
@@ -658,11 +698,7 @@ def main():
                 "frac": round(o["achieved"] / HBM_PEAK_GBS, 4),
                 "traffic": o["traffic"],
             },
-            "reference_default_partitions": {
-                "max_context_partition_num": o["ref_parts"],
-                "us_per_step": round(o["ref_us"], 2),
-                "kv_gbs": round(o["kvb"] / (o["ref_us"] * 1e-6) / 1e9, 1),
-            },
+            "reference_default_partitions": _reference_entry(o),
             "steps": config_steps,
         }
 
@@ -704,11 +740,7 @@ def main():
         "metadata_us": round(r["metadata_us"], 2) if r["metadata_us"] is not None else None,
         "host_us_per_step": round(r["host_s"] * 1e6, 2),
         "other_paths_us_per_step": {k: round(v, 2) for k, v in r["others"].items()},
-        "reference_default_partitions": {
-            "max_context_partition_num": r["ref_parts"],
-            "us_per_step": round(r["ref_us"], 2),
-            "kv_gbs": round(r["kvb"] / (r["ref_us"] * 1e-6) / 1e9, 1),
-        },
+        "reference_default_partitions": _reference_entry(r),
         "roofline": {
             "bound": "hbm",
             "achieved": round(r["achieved"], 1),
