@@ -499,6 +499,10 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
     p.s_o_group = a->stride_o_group;
     p.out_dtype = a->out_dtype;
     p.spw = spw;
+    // several workgroups per (sequence, kv head) of the partition kernel: spread each
+    // sequence over the XCDs (slot_item)
+    const unsigned zg = (unsigned)((P + slots_per_wg - 1) / slots_per_wg);
+    p.spread = zg > 1 && spw == 0 ? 1 : 0;
     // a merging workgroup keeps a copy of its partials in LDS when they fit in 48 KiB
     // (then it reads LDS, not the rows it just stored): P rows of eqgs x (D bf16 + 2 f32)
     p.merge_lds = 0;
@@ -507,7 +511,7 @@ int pa_fp8_decode_partitions(const pa_fp8_decode_args *a, void *stream) {
         if (bytes <= 48 * 1024) p.merge_lds = (int32_t)bytes;
     }
 
-    const dim3 grid(a->batch_size * chunks, a->num_kv_heads, (unsigned)((P + slots_per_wg - 1) / slots_per_wg));
+    const dim3 grid(a->batch_size * chunks, a->num_kv_heads, zg);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int mtp = (min(eqgs, kRowChunk) + 15) / 16;
     const hipError_t err = run_partition(a->head_dim, p, a->per_token_kv != 0, a->value_layout == PA_FP8_V_4D, mtp,

@@ -1269,25 +1269,49 @@ __device__ __forceinline__ void attend(const DecodeParams &p, int b, int h, int 
         attend_range<MTPW, RS, NS, PER_TOKEN, D, V4>(p, b, h, ctx, tok_lo, tok_hi, bt_row, row0, sink);
 }
 
-// Split-context decode: workgroup (x, h, z) runs partition slot z of kv head h of
-// sequence b = x / chunks, query rows [64 c, 64 c + 64) with c = x % chunks (the
-// row chunks of a slot are adjacent in dispatch order, so they read its K / V at
-// about the same time).
+// The work item of a split-context workgroup.  The grid is (B * chunks, Hkv, Z), and
+// the workgroups go to the XCDs round-robin in dispatch order (x fastest).  With
+// several slot groups per sequence (Z > 1, p.spread) the linear dispatch index is
+// read with the row chunk fastest, then the kv head, then the slot group, then the
+// sequence: one sequence's items are consecutive and spread over every XCD.  Read as
+// the grid's (x, y, z), every item of sequence b goes to XCD b mod 8 (B * Hkv is a
+// multiple of 8 in practice), and a ragged batch loads the XCDs as unevenly as its
+// lengths: c3 at 8 slots took 300 us that way, 204 us spread.  One workgroup per
+// (sequence, kv head) keeps the grid's order, where a sequence's kv heads share their
+// XCD's L2 for its page-table row (equal-length batches 0.3-0.8% faster).  The
+// chained kernel keeps the grid's order (its layouts hold whole sequences or equal
+// slots, and the remap cost it 1-2%).
+struct SlotItem {
+    int b, h, z, row0;
+};
+__device__ __forceinline__ SlotItem slot_item(const DecodeParams &p) {
+    if (!p.spread) {
+        const int b = p.chunks > 1 ? (int)(blockIdx.x / p.chunks) : (int)blockIdx.x;
+        return SlotItem{b, (int)blockIdx.y, (int)blockIdx.z, ((int)blockIdx.x - b * max(p.chunks, 1)) * kRowChunk};
+    }
+    const uint64_t nh = gridDim.y, nz = gridDim.z, nc = p.chunks > 1 ? (uint64_t)p.chunks : 1u;
+    uint64_t r = blockIdx.x + (uint64_t)gridDim.x * (blockIdx.y + nh * blockIdx.z);
+    const int c = (int)(r % nc);
+    r /= nc;
+    const int h = (int)(r % nh);
+    r /= nh;
+    const int z = (int)(r % nz);
+    return SlotItem{(int)(r / nz), h, z, c * kRowChunk};
+}
+
+// Split-context decode: a workgroup runs partition slot z of kv head h of sequence b,
+// query rows [row0, row0 + 64) (slot_item; the row chunks of a slot are adjacent in
+// dispatch order, so they read its K / V at about the same time).
 template <int MTPW, int RS, int NS, bool PER_TOKEN, int D, bool V4>
 __global__ __launch_bounds__((kThreads<RS, NS>), (kWavesFor<MTPW, NS, D>)) void pa_decode_partition_kernel(
     const DecodeParams p) {
-    int b = blockIdx.x, row0 = 0;
-    if (p.chunks > 1) {
-        b = blockIdx.x / p.chunks;
-        row0 = (blockIdx.x - b * p.chunks) * kRowChunk;
-    }
-    const int h = blockIdx.y;
+    const SlotItem it = slot_item(p);
+    const int b = it.b, h = it.h, z = it.z, row0 = it.row0;
 
     int64_t ctx64 = p.ctx[b];
     const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
     ctx64 = ctx64 < 0 ? 0 : (ctx64 > cap ? cap : ctx64);
     const int ctx = (int)ctx64;
-    const int z = blockIdx.z;
 
     // ---- slot -> token range (integer planner, bit-exact with the oracle)
     int tok_lo, tok_hi;

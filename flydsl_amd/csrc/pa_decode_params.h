@@ -42,6 +42,7 @@ struct DecodeParams {
     int32_t direct;
     int32_t spw;        // chained layout: partition slots one wave runs in turn (0: one slot per workgroup)
     int32_t merge_lds;  // bytes of dynamic LDS holding the partials a merging workgroup reads (0: global)
+    int32_t spread;     // several slots per sequence: spread each sequence's items over the XCDs (slot_item)
 };
 
 struct WorklistParams {

@@ -82,11 +82,12 @@ def test_small_cases_with_partials(case, max_parts):
         check_partials(w, partials, max_parts, range(cfg.batch))
 
 
-@pytest.mark.parametrize("name", ["c2", "c4"])
+@pytest.mark.parametrize("name", ["c2", "c3", "c4"])
 @pytest.mark.parametrize("max_parts", [1, 8])
 def test_baseline_config_partition_counts(name, max_parts):
     """Full-size configs at the direct-output and the reference-default partition
-    counts, every sequence against the oracle."""
+    counts, every sequence against the oracle (c3: a ragged batch on the partition
+    route, as a caller without metadata gets it)."""
     cfg = CONFIGS[name]
     print(f"[parity] {name} P={max_parts}", flush=True)
     w = build_workload(cfg, "cuda")
