@@ -18,8 +18,9 @@ are rotated step to step so the working set (>= 1.5 GiB for c2) defeats the
                    back-to-back launches of it alone), never longer than the step
   cpu_baseline   = the reference's torch path (restated with torch CPU ops) timed
                    on this host's cores over 3 full steps of the workload (median)
-  configs        = c3, c4 and c5 measured the same way in the same run (the
-                   same warmup, --config-steps or --steps timed steps each)
+  configs        = c3, c4 and c5 measured the same way in the same run
+                   (--config-steps or --steps timed steps each, after at least
+                   CONFIG_WARMUP untimed steps, so the clocks have settled)
 """
 
 from __future__ import annotations
@@ -40,6 +41,7 @@ if str(ROOT) not in sys.path:
 
 METRIC = "KV-read HBM GB/s (% of peak) + µs/decode step, 8B-shaped fp8 paged decode"
 HBM_PEAK_GBS = 8000.0
+CONFIG_WARMUP = 200  # untimed steps before each configuration of the `configs` block, at least
 
 
 def _parse():
@@ -402,23 +404,25 @@ def rope_main(args):
 
 def _timed(torch, fn, steps, warmup):
     """ms per call of fn(i) over ``steps`` calls between two HIP events on the
-    launch stream (torch's current stream), after ``warmup`` calls; also the host
-    wall time per call.  Python's garbage collector is paused over the timed calls
-    (as timeit does), so a collection cannot stall the launches."""
-    for i in range(warmup):
-        fn(i)
+    launch stream (torch's current stream), after ``warmup`` calls queued right
+    before them (no idle gap between the two, which would let the clocks boost and
+    then overshoot down under the power limit); also the host's time per call to
+    queue the timed calls.  Python's garbage collector is paused over the calls (as
+    timeit does), so a collection cannot stall the launches."""
     e0, e1 = _events(torch, 2)
     torch.cuda.synchronize()
     gc.collect()
     gc.disable()
     try:
-        t0 = time.perf_counter()
+        for i in range(warmup):
+            fn(i)
         e0.record()
+        t0 = time.perf_counter()
         for i in range(steps):
             fn(i)
+        host = (time.perf_counter() - t0) / steps
         e1.record()
         torch.cuda.synchronize()
-        host = (time.perf_counter() - t0) / steps
     finally:
         gc.enable()
     return e0.elapsed_time(e1) / steps, host
@@ -428,19 +432,21 @@ def _kernel_alone_ms(torch, plans, j, steps, warmup):
     """ms per launch of the plans' j-th kernel alone: ``steps`` back-to-back launches
     of only that kernel (the plans of the rotated KV copies in turn) between two HIP
     events on the launch stream.  A GPU-side sleep holds the stream until every
-    launch is queued, so host submission never gaps the launches.  The interval per
-    launch is the kernel's duration plus the dependency gap to the next launch; it
-    cannot exceed the step that runs this kernel and the others."""
+    launch is queued, so host submission never gaps the launches; the warmup launches
+    are queued behind the sleep too, so the clocks settle again after the idle sleep
+    before the timed ones run.  The interval per launch is the kernel's duration plus
+    the dependency gap to the next launch; it cannot exceed the step that runs this
+    kernel and the others."""
     handle = torch.cuda.current_stream().cuda_stream
-    for i in range(warmup):
-        fn, a = plans[i % len(plans)].launches[j]
-        fn(a, handle)
     e0, e1 = _events(torch, 2)
     torch.cuda.synchronize()
     gc.collect()
     gc.disable()
     try:
-        torch.cuda._sleep(int(2.5e6 + 2e4 * steps))  # cycles: several ms of queue head start
+        torch.cuda._sleep(int(2.5e6 + 2e4 * (steps + warmup)))  # cycles: several ms of queue head start
+        for i in range(warmup):
+            fn, a = plans[i % len(plans)].launches[j]
+            fn(a, handle)
         e0.record()
         for i in range(steps):
             fn, a = plans[i % len(plans)].launches[j]
@@ -690,10 +696,15 @@ def main():
     configs = {}
     extra = [c for c in (args.configs.split(",") if args.configs else []) if c and c != cfg.name]
     config_steps = args.config_steps or args.steps
+    # at least CONFIG_WARMUP steps before each configuration's timed ones: after the
+    # idle gaps between measurements the clocks boost, overshoot down under the power
+    # limit and settle over about a hundred c5 steps (c5's worklist kernel ran 280 us,
+    # then 460 us, then settled near 305-320 us in kernel traces)
+    config_warmup = max(args.warmup, CONFIG_WARMUP)
     for name in extra:
         c = CONFIGS[name]
         try:
-            o = measure_decode(torch, c, dev, config_steps, args.warmup, copies=args.copies,
+            o = measure_decode(torch, c, dev, config_steps, config_warmup, copies=args.copies,
                                use_metadata=not args.no_metadata, extras=False)
         except ValueError as e:  # a configuration the launcher refuses leaves the headline line intact
             print(f"[bench] {name} refused: {e}", file=sys.stderr, flush=True)
@@ -722,6 +733,7 @@ def main():
             },
             "reference_default_partitions": _reference_entry(o),
             "steps": config_steps,
+            "warmup": config_warmup,
         }
 
     us_step = r["us_step"]
