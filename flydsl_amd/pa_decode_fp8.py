@@ -797,18 +797,22 @@ def _build_plan_checked(
     small = block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES
     # Block sizes other than 16 / 64 take the persistent path, as in the reference.
     # The small-block path also runs the worklist kernel when the caller hands
-    # in get_pa_metadata's schedule with the flat page list, the batch is ragged
-    # and no split-context partials are passed: the schedule balances ragged
-    # batches across CUs, which fixed partition slots cannot (equal-length batches
-    # keep the partition kernel, whose slots are balanced already and which skips
-    # the worklist reads).  The tag stays "ps_small_block".  A caller that passes
+    # in get_pa_metadata's schedule with the flat page list and no split-context
+    # partials, and the batch is ragged or the caller asks for several slots: the
+    # schedule balances ragged batches across CUs, which fixed partition slots
+    # cannot, and on an equal-length batch it holds whole sequences, as one slot
+    # does (c2 at the harness's 8 slots: 87.6-88.3 us on the worklist against 93.9 us
+    # on the chained slots).  Equal-length batches at one slot or the automatic
+    # count keep the partition kernel, which skips the worklist reads.  The tag stays
+    # "ps_small_block".  A caller that passes
     # exp_sums / max_logits / temporary_output gets them filled in the reference's
     # partition-slot format, as the reference's small-block route (which ignores
     # metadata) fills them: that call runs the partition kernel at the caller's
     # partition count (kernels/pa_decode_fp8.py:3010-3121).
     caller_partials = exp_sums is not None or max_logits is not None or temporary_output is not None
     balanced_worklist = (metadata is not None and kv_page_indices is not None and kv_indptr is not None
-                         and not metadata.get("uniform_context", False) and not caller_partials)
+                         and not caller_partials
+                         and (not metadata.get("uniform_context", False) or max_context_partition_num > 1))
     if small and sliding_window <= 0 and not trans_v:
         # the reference's small-block kernel reads trans_v only (kernels/pa_decode_fp8.py:2082-2083)
         raise NotImplementedError("compile_pa_decode_ps: trans_v=False not yet supported.")

@@ -326,9 +326,14 @@ def test_small_block_with_metadata_runs_the_worklist(bs):
     p = plan(t, max_parts=4)
     assert p.tag == "ps_small_block" and p.wargs is not None and p.dargs is None
     assert p.wargs.block_size == bs and p.wargs.num_cu == 3
-    # without the flat page list, with a window, or for a uniform batch, the partition kernel runs
+    # without the flat page list, with a window, or for a uniform batch at one slot or the
+    # automatic count, the partition kernel runs; a uniform batch at several slots keeps the
+    # worklist (whole sequences per bin, no slot boundaries)
     assert plan(t, max_parts=4, kv_indptr=None).dargs is not None
-    assert plan(t, max_parts=4, metadata=dict(t["metadata"], uniform_context=True)).dargs is not None
+    uniform = dict(t["metadata"], uniform_context=True)
+    assert plan(t, max_parts=1, metadata=uniform).dargs is not None
+    assert plan(t, max_parts=0, metadata=uniform).dargs is not None
+    assert plan(t, max_parts=4, metadata=uniform).wargs is not None
     assert plan(t, sliding_window=300, max_parts=4).dargs is not None
     # the worklist route allocates nothing, so it is capturable without partials; the
     # partition route keeps the reference's graph-capture rule
