@@ -981,6 +981,35 @@ def get_pa_metadata(
     args[0].partition_indptr = partition_indptr.data_ptr()
     args[0].uniform_context = counts[1:2].data_ptr()
     _lib.metadata_multi(args, torch.cuda.current_stream(dev).cuda_stream)
+
+    # the dicts are built while the scheduler runs; only the partial buffers wait for
+    # the host read below
+    def entry(k):
+        wi, winfo, ri, rfm, rpm = sched_bufs[k]
+        return {
+            "work_indptr": wi,
+            "work_info_flat": winfo,
+            "reduce_indptr": ri,
+            "reduce_final_map": rfm.view(batch_size, 2),
+            "reduce_partial_map": rpm,
+            "num_sm": schedules[k][0],
+        }
+
+    entries = [entry(k) for k in range(len(schedules))]
+    md = entries[0]
+    md.update({
+        "partition_indptr": partition_indptr,
+        "stride_po_partial": query_length * num_query_heads * head_size,
+        "stride_pl_partial": query_length * num_query_heads,
+        "stride_po_ql": num_query_heads * head_size,
+        "stride_pl_ql": num_query_heads,
+        "query_length": query_length,
+    })
+    if tuned:
+        t = entries[1]
+        t["bin_groups"] = schedules[1][1]
+        t["bin_weight"] = _BIN_WEIGHTS.get(schedules[1][1])
+        md["tuned"] = t
     if graph_safe:
         # no host read: room for every partial a schedule can emit
         nparts = [int(b[4].numel()) for b in sched_bufs]
@@ -991,43 +1020,13 @@ def get_pa_metadata(
         host = counts[:3].cpu().tolist()
         nparts = [host[0], host[2]][: len(schedules)]
         uniform = bool(host[1])
-
-    def partials(n):
+    for e, n in zip(entries, nparts):
         rows = (n + 1) * query_length
-        return (torch.empty((rows, 1, num_query_heads, head_size), dtype=torch.float32, device=dev),
-                torch.empty((rows, 1, num_query_heads, 1), dtype=torch.float32, device=dev))
-
-    def entry(k):
-        wi, winfo, ri, rfm, rpm = sched_bufs[k]
-        po, pl = partials(nparts[k])
-        return {
-            "work_indptr": wi,
-            "work_info_flat": winfo,
-            "reduce_indptr": ri,
-            "reduce_final_map": rfm.view(batch_size, 2),
-            "reduce_partial_map": rpm,
-            "num_sm": schedules[k][0],
-            "partial_output": po,
-            "partial_lse": pl,
-        }
-
-    md = entry(0)
-    md.update({
-        "partition_indptr": partition_indptr,
-        "stride_po_partial": query_length * num_query_heads * head_size,
-        "stride_pl_partial": query_length * num_query_heads,
-        "stride_po_ql": num_query_heads * head_size,
-        "stride_pl_ql": num_query_heads,
-        "query_length": query_length,
-        # equal context lengths: fixed partition slots are already balanced, so the
-        # small-block path keeps its partition kernel instead of the worklist
-        "uniform_context": uniform,
-    })
-    if tuned:
-        t = entry(1)
-        t["bin_groups"] = schedules[1][1]
-        t["bin_weight"] = _BIN_WEIGHTS.get(schedules[1][1])
-        md["tuned"] = t
+        e["partial_output"] = torch.empty((rows, 1, num_query_heads, head_size), dtype=torch.float32, device=dev)
+        e["partial_lse"] = torch.empty((rows, 1, num_query_heads, 1), dtype=torch.float32, device=dev)
+    # equal context lengths: at one slot or the automatic count the small-block path
+    # keeps its partition kernel (one balanced slot per sequence) instead of the worklist
+    md["uniform_context"] = uniform
     return md
 
 
