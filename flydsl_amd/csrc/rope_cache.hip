@@ -7,6 +7,8 @@
 // needed for the rotation (the reference gives each lane a contiguous slice and
 // fetches the partner with ds_bpermute, kernels/fused_rope_cache_kernel.py:150-177).
 // Every load and store of Q/K/V/outputs/cos/sin is one 16-byte vector access.
+// Flash-layout head dims that are not a multiple of 16 go to
+// rope_cache_narrow_kernel instead (element-wise accesses, same arithmetic).
 // Rows of token t are laid out [Q heads..., K heads...] in the flat row index,
 // so consecutive lanes stream consecutive bytes of Q then K.  A K row also
 // reads V and writes the two cache entries of its token.
@@ -537,6 +539,175 @@ __global__ __launch_bounds__(kRopeThreads) void rope_cache_kernel(RopeParams p) 
     }
 }
 
+// Flash-layout rows of head dims that are not a multiple of 16 (the reference
+// writer takes any head dim its vector-width rule admits,
+// kernels/fused_rope_cache_kernel.py:79-96).  Rows are numbered as in
+// rope_cache_kernel's Q range, Q rows t * QH + h then K rows t * KH + h; a row
+// is handled by an aligned group of L = 2^lpr_log2 lanes (L = next_pow2(D/2),
+// at most 64), lane c taking the rotation pairs (j, j + D/2) for j = c, c + L,
+// ... < D/2, one 16-bit element per access (consecutive lanes, consecutive
+// elements).  Same arithmetic as rotate() and finish_kv_row(), element by element.
+constexpr int kNarrowPairs = 8;  // pairs per lane: D/2 <= 8 * 64
+
+template <int ELEM>
+__device__ __forceinline__ void rotate1(float &x1, float &x2, float c1, float s1, float c2, float s2) {
+#pragma clang fp contract(off)
+    if constexpr (ELEM == PA_FP8_F16) {
+        const _Float16 a = (_Float16)x1, b = (_Float16)x2;
+        const _Float16 p1 = a * (_Float16)c1, p2 = b * (_Float16)s1;
+        const _Float16 p3 = b * (_Float16)c2, p4 = a * (_Float16)s2;
+        x1 = (float)(_Float16)(p1 - p2);
+        x2 = (float)(_Float16)(p3 + p4);
+    } else {
+        float p1 = x1 * c1, p2 = x2 * s1, p3 = x2 * c2, p4 = x1 * s2;
+        round_pair_bf16(p1, p2);
+        round_pair_bf16(p3, p4);
+        float o1 = p1 - p2, o2 = p3 + p4;
+        round_pair_bf16(o1, o2);
+        x1 = o1;
+        x2 = o2;
+    }
+}
+
+template <int ELEM, int FMT>
+__global__ __launch_bounds__(kRopeThreads) void rope_cache_narrow_kernel(RopeParams p) {
+    const int lpr_log2 = p.lpr_log2;
+    const int c = int(threadIdx.x & ((1u << lpr_log2) - 1));
+    const int64_t row = int64_t(blockIdx.x) * (kRopeThreads >> lpr_log2) + (threadIdx.x >> lpr_log2);
+    // whole rows leave together, so the amax exchange below stays among live lanes
+    if (row >= p.q_rows + int64_t(p.T) * p.KH) return;
+    const int half = p.D >> 1;
+    const bool is_k = row >= p.q_rows;
+    int t, h;
+    if (!is_k) {
+        t = fdiv(int(row), p.div_qh);
+        h = int(row - int64_t(t) * p.QH);
+    } else {
+        const int kr = int(row - p.q_rows);
+        t = fdiv(kr, p.div_kh);
+        h = kr - t * p.KH;
+    }
+    const int pos = min(max(p.pos[int64_t(t) << p.pos_shift], 0), p.max_pos - 1);
+    const uint16_t *x = is_k ? p.k + int64_t(t) * p.sk_t + int64_t(h) * p.sk_h
+                             : p.q + int64_t(t) * p.sq_t + int64_t(h) * p.sq_h;
+    uint16_t *out = is_k ? p.ko + int64_t(t) * p.sko_t + int64_t(h) * p.sko_h
+                         : p.qo + int64_t(t) * p.sqo_t + int64_t(h) * p.sqo_h;
+    const uint16_t *crow = p.cos + int64_t(pos) * p.scos;
+    const uint16_t *srow = p.sin + int64_t(pos) * p.ssin;
+    const int coff = p.reuse ? 0 : half;  // column of the second half's cos / sin
+    float x1[kNarrowPairs], x2[kNarrowPairs];
+#pragma unroll
+    for (int i = 0; i < kNarrowPairs; ++i) {
+        const int j = c + (i << lpr_log2);
+        x1[i] = x2[i] = 0.0f;
+        if (j < half) {
+            x1[i] = to_f<ELEM>(x[j]);
+            x2[i] = to_f<ELEM>(x[j + half]);
+            rotate1<ELEM>(x1[i], x2[i], to_f<ELEM>(crow[j]), to_f<ELEM>(srow[j]), to_f<ELEM>(crow[j + coff]),
+                          to_f<ELEM>(srow[j + coff]));
+            out[j] = (uint16_t)from_f<ELEM>(x1[i]);
+            out[j + half] = (uint16_t)from_f<ELEM>(x2[i]);
+        }
+    }
+    if (!is_k) return;
+
+    const int slot = p.slot[int64_t(t) << p.slot_shift];
+    const bool write = slot >= 0 && fdiv(slot, p.div_bs) < p.nb;  // uniform over the row's lanes
+    const int blk = write ? fdiv(slot, p.div_bs) : 0;
+    const int bpos = write ? slot - blk * p.bs : 0;
+    const uint16_t *vr = p.v + int64_t(t) * p.sv_t + int64_t(h) * p.sv_h;
+    float v1[kNarrowPairs], v2[kNarrowPairs];
+#pragma unroll
+    for (int i = 0; i < kNarrowPairs; ++i) {
+        const int j = c + (i << lpr_log2);
+        v1[i] = v2[i] = 0.0f;
+        if (write && j < half) {
+            v1[i] = to_f<ELEM>(vr[j]);
+            v2[i] = to_f<ELEM>(vr[j + half]);
+        }
+    }
+    float sk = 1.0f, sv = 1.0f;
+    if constexpr (FMT == PA_FP8_CACHE_FP8_TENSOR) {
+        sk = __builtin_amdgcn_rcpf(p.ks[0]);  // applied as x * rcp(scale)
+        sv = __builtin_amdgcn_rcpf(p.vs[0]);
+    } else if constexpr (FMT == PA_FP8_CACHE_FP8_TOKEN) {
+        float ak = 0.0f, av = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kNarrowPairs; ++i) {
+            x1[i] = clean448(x1[i]);
+            x2[i] = clean448(x2[i]);
+            v1[i] = clean448(v1[i]);
+            v2[i] = clean448(v2[i]);
+            ak = fmaxf(ak, fmaxf(fabsf(x1[i]), fabsf(x2[i])));
+            av = fmaxf(av, fmaxf(fabsf(v1[i]), fabsf(v2[i])));
+        }
+        for (int m = (1 << lpr_log2) >> 1; m >= 1; m >>= 1) {
+            ak = fmaxf(ak, __shfl_xor(ak, m, 64));
+            av = fmaxf(av, __shfl_xor(av, m, 64));
+        }
+        sk = ak / 448.0f;
+        sv = av / 448.0f;
+        if (sk == 0.0f) sk = 1.0f;
+        if (sv == 0.0f) sv = 1.0f;
+        if (write && c == 0) {
+            const int64_t so = int64_t(blk) * p.sks_b + int64_t(h) * p.sks_h + bpos;
+            p.ks[so] = sk;
+            p.vs[so] = sv;
+        }
+    }
+    if (!write) return;
+    constexpr int esz = FMT == PA_FP8_CACHE_ELEM ? 2 : 1;
+    uint8_t *kt = p.kc + (int64_t(blk) * p.skc_b + int64_t(bpos) * p.skc_t + int64_t(h) * p.skc_h) * esz;
+    uint8_t *vt = p.vc + (int64_t(blk) * p.svc_b + int64_t(bpos) * p.svc_t + int64_t(h) * p.svc_h) * esz;
+#pragma unroll
+    for (int i = 0; i < kNarrowPairs; ++i) {
+        const int j = c + (i << lpr_log2);
+        if (j >= half) continue;
+        float k1 = x1[i], k2 = x2[i], w1 = v1[i], w2 = v2[i];
+        if constexpr (FMT == PA_FP8_CACHE_FP8_TENSOR) {
+            k1 *= sk;
+            k2 *= sk;
+            w1 *= sv;
+            w2 *= sv;
+        } else if constexpr (FMT == PA_FP8_CACHE_FP8_TOKEN) {
+            k1 = k1 / sk;
+            k2 = k2 / sk;
+            w1 = w1 / sv;
+            w2 = w2 / sv;
+        }
+        if constexpr (FMT == PA_FP8_CACHE_ELEM) {
+            uint16_t *k16 = reinterpret_cast<uint16_t *>(kt), *v16 = reinterpret_cast<uint16_t *>(vt);
+            k16[j] = (uint16_t)from_f<ELEM>(k1);
+            k16[j + half] = (uint16_t)from_f<ELEM>(k2);
+            v16[j] = (uint16_t)from_f<ELEM>(w1);
+            v16[j + half] = (uint16_t)from_f<ELEM>(w2);
+        } else {
+            kt[j] = (uint8_t)cache_bits<FMT, ELEM>(k1);
+            kt[j + half] = (uint8_t)cache_bits<FMT, ELEM>(k2);
+            vt[j] = (uint8_t)cache_bits<FMT, ELEM>(w1);
+            vt[j + half] = (uint8_t)cache_bits<FMT, ELEM>(w2);
+        }
+    }
+}
+
+template <int ELEM>
+hipError_t launch_narrow(const RopeParams &p, int fmt, dim3 grid, hipStream_t s) {
+    switch (fmt) {
+    case PA_FP8_CACHE_ELEM:
+        hipLaunchKernelGGL((rope_cache_narrow_kernel<ELEM, PA_FP8_CACHE_ELEM>), grid, dim3(kRopeThreads), 0, s, p);
+        break;
+    case PA_FP8_CACHE_FP8_TENSOR:
+        hipLaunchKernelGGL((rope_cache_narrow_kernel<ELEM, PA_FP8_CACHE_FP8_TENSOR>), grid, dim3(kRopeThreads), 0, s,
+                           p);
+        break;
+    default:
+        hipLaunchKernelGGL((rope_cache_narrow_kernel<ELEM, PA_FP8_CACHE_FP8_TOKEN>), grid, dim3(kRopeThreads), 0, s,
+                           p);
+        break;
+    }
+    return hipGetLastError();
+}
+
 template <int ELEM, int FMT>
 hipError_t launch_layout(const RopeParams &p, int layout, dim3 grid, hipStream_t s) {
     switch (layout) {
@@ -564,6 +735,90 @@ hipError_t launch_format(const RopeParams &p, int fmt, int layout, dim3 grid, hi
 
 inline bool aligned(const void *ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; }
 
+// pa_fp8_rope_cache for flash-layout head dims that are not a multiple of 16 (the
+// caller has checked the head dim, shape and layout fields): 16-bit tensors
+// need only 2-byte alignment and any non-negative strides.
+int rope_cache_narrow(const pa_fp8_rope_cache_args *a, void *hip_stream) {
+    const void *p16[] = {a->query, a->key, a->value, a->cos_cache, a->sin_cache, a->query_out, a->key_out};
+    for (const void *ptr : p16)
+        if (!aligned(ptr, 2)) return PA_FP8_ERR_SHAPE;
+    const int64_t st[] = {a->stride_q_token,  a->stride_q_head,   a->stride_k_token,  a->stride_k_head,
+                          a->stride_v_token,  a->stride_v_head,   a->stride_qo_token, a->stride_qo_head,
+                          a->stride_ko_token, a->stride_ko_head,  a->stride_cos_pos,  a->stride_sin_pos,
+                          a->stride_kc_block, a->stride_kc_head,  a->stride_kc_token, a->stride_vc_block,
+                          a->stride_vc_head,  a->stride_vc_token};
+    for (int64_t s : st)
+        if (s < 0) return PA_FP8_ERR_SHAPE;
+    if (a->cache_format == PA_FP8_CACHE_ELEM && (!aligned(a->key_cache, 2) || !aligned(a->value_cache, 2)))
+        return PA_FP8_ERR_SHAPE;
+    if (a->cache_format == PA_FP8_CACHE_FP8_TOKEN && (a->stride_ks_block < 0 || a->stride_ks_head < 0))
+        return PA_FP8_ERR_SHAPE;
+    if (a->num_tokens == 0) return PA_FP8_OK;
+    const int half = a->head_dim / 2;
+    int lpr_log2 = 0;
+    while ((1 << lpr_log2) < half && lpr_log2 < 6) ++lpr_log2;
+    RopeParams p{};
+    p.q = static_cast<const uint16_t *>(a->query);
+    p.k = static_cast<const uint16_t *>(a->key);
+    p.v = static_cast<const uint16_t *>(a->value);
+    p.cos = static_cast<const uint16_t *>(a->cos_cache);
+    p.sin = static_cast<const uint16_t *>(a->sin_cache);
+    p.pos = static_cast<const int32_t *>(a->positions);
+    p.slot = static_cast<const int32_t *>(a->slot_mapping);
+    p.qo = static_cast<uint16_t *>(a->query_out);
+    p.ko = static_cast<uint16_t *>(a->key_out);
+    p.kc = static_cast<uint8_t *>(a->key_cache);
+    p.vc = static_cast<uint8_t *>(a->value_cache);
+    p.ks = a->key_scale;
+    p.vs = a->value_scale;
+    p.sq_t = a->stride_q_token;
+    p.sq_h = a->stride_q_head;
+    p.sk_t = a->stride_k_token;
+    p.sk_h = a->stride_k_head;
+    p.sv_t = a->stride_v_token;
+    p.sv_h = a->stride_v_head;
+    p.sqo_t = a->stride_qo_token;
+    p.sqo_h = a->stride_qo_head;
+    p.sko_t = a->stride_ko_token;
+    p.sko_h = a->stride_ko_head;
+    p.scos = a->stride_cos_pos;
+    p.ssin = a->stride_sin_pos;
+    p.skc_b = a->stride_kc_block;
+    p.skc_h = a->stride_kc_head;
+    p.skc_t = a->stride_kc_token;
+    p.svc_b = a->stride_vc_block;
+    p.svc_h = a->stride_vc_head;
+    p.svc_t = a->stride_vc_token;
+    p.sks_b = a->stride_ks_block;
+    p.sks_h = a->stride_ks_head;
+    p.QH = a->num_q_heads;
+    p.KH = a->num_kv_heads;
+    p.D = a->head_dim;
+    p.bs = a->block_size;
+    p.nb = a->num_blocks;
+    p.max_pos = a->max_pos;
+    p.pos_shift = a->positions_i64 ? 1 : 0;
+    p.slot_shift = a->slots_i64 ? 1 : 0;
+    p.reuse = a->reuse_freqs_front_part ? 1 : 0;
+    p.lpr_log2 = lpr_log2;
+    p.T = a->num_tokens;
+    p.q_rows = int64_t(a->num_tokens) * a->num_q_heads;
+    const int64_t rows = p.q_rows + int64_t(a->num_tokens) * a->num_kv_heads;
+    const int64_t rpp = kRopeThreads >> lpr_log2;
+    const int64_t blocks = (rows + rpp - 1) / rpp;
+    // rows, K rows and slots are divided as 31-bit values
+    if (blocks > 0x7fffffffLL || blocks * rpp > 0x7fffffffLL) return PA_FP8_ERR_SHAPE;
+    p.div_qh = make_fastdiv(a->num_q_heads);
+    p.div_kh = make_fastdiv(a->num_kv_heads);
+    p.div_bs = make_fastdiv(a->block_size);
+    p.div_d = make_fastdiv(a->head_dim);
+    const dim3 grid((unsigned)blocks);
+    hipStream_t s = static_cast<hipStream_t>(hip_stream);
+    const hipError_t e = a->elem_dtype == PA_FP8_BF16 ? launch_narrow<PA_FP8_BF16>(p, a->cache_format, grid, s)
+                                                      : launch_narrow<PA_FP8_F16>(p, a->cache_format, grid, s);
+    return e == hipSuccess ? PA_FP8_OK : PA_FP8_ERR_HIP + int(e);
+}
+
 __global__ __launch_bounds__(256) void hw_reciprocal_kernel(const float *x, float *y, int64_t n) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i < n) y[i] = __builtin_amdgcn_rcpf(x[i]);
@@ -585,12 +840,15 @@ extern "C" int pa_fp8_rope_cache(const pa_fp8_rope_cache_args *a, void *hip_stre
     if (a->kv_layout < PA_FP8_KV_FLASH || a->kv_layout > PA_FP8_KV_X_TRANS) return PA_FP8_ERR_LAYOUT;
     if (a->cache_format != PA_FP8_CACHE_ELEM && (!a->key_scale || !a->value_scale)) return PA_FP8_ERR_NULL_POINTER;
     const int D = a->head_dim;
-    if (D < 16 || D > 1024 || D % 16 != 0) return PA_FP8_ERR_HEAD_DIM;
+    // head dims off the 16-dim grid: flash layout only, element-wise accesses
+    const bool narrow = a->kv_layout == PA_FP8_KV_FLASH && D % 16 != 0;
+    if (narrow ? (D < 2 || D > 1024 || D % 2 != 0) : (D < 16 || D > 1024 || D % 16 != 0)) return PA_FP8_ERR_HEAD_DIM;
     if (a->num_tokens < 0 || a->num_q_heads < 1 || a->num_kv_heads < 1 || a->block_size < 1 || a->num_blocks < 1 ||
         a->max_pos < 1)
         return PA_FP8_ERR_SHAPE;
     if (int64_t(a->num_q_heads) + a->num_kv_heads > (1 << 20)) return PA_FP8_ERR_SHAPE;
     if (a->kv_layout == PA_FP8_KV_X_TRANS && a->block_size % 16 != 0) return PA_FP8_ERR_LAYOUT;
+    if (narrow) return rope_cache_narrow(a, hip_stream);
     // 16-byte vector rows for every 16-bit tensor
     const void *p16[] = {a->query, a->key, a->value, a->cos_cache, a->sin_cache, a->query_out, a->key_out};
     for (const void *ptr : p16)

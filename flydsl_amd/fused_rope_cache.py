@@ -32,8 +32,13 @@ Cache formats:
   in the scale tensor at the token's slot and writes the codes of
   ``x / scale`` (the quantiser of tests/kernels/test_pa.py:334-376).
 
+Head dims: those the reference admits (its vector-width rule, and a multiple
+of 16 without the flash layout), up to 1024.  Multiples of 16 run one kernel
+over 16-byte vectors; other (flash-layout) head dims a kernel that reads and
+writes element by element, with the same arithmetic.
+
 Differences from the reference, each an error where the reference would
-silently misbehave: head_dim must be a multiple of 16; Positions / SlotMapping
+silently misbehave: Positions / SlotMapping
 must have the dtype ``pos_dtype`` names; every tensor is checked for shape,
 dtype, device and alignment before the launch.  Positions outside
 ``[0, CosCache.shape[0])`` are clamped into it and slots past the cache are
@@ -62,8 +67,10 @@ def _tkey(t):
     return ("obj", id(t))
 
 
-def _rows(name, t, tokens, heads, head_dim, dtype):
-    """A [>= tokens, heads, head_dim] tensor with contiguous rows -> (token stride, head stride)."""
+def _rows(name, t, tokens, heads, head_dim, dtype, vec16=True):
+    """A [>= tokens, heads, head_dim] tensor with contiguous rows -> (token stride, head stride).
+
+    ``vec16``: rows read and written as 16-byte vectors must be 16-byte aligned."""
     if not isinstance(t, torch.Tensor) or t.dim() != 3:
         raise ValueError(f"{name} must be a 3-D tensor [tokens, heads, head_dim]")
     if t.shape[0] < tokens or t.shape[1] != heads or t.shape[2] != head_dim:
@@ -72,7 +79,7 @@ def _rows(name, t, tokens, heads, head_dim, dtype):
         raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
     if t.stride(2) != 1:
         raise ValueError(f"{name} must be contiguous along head_dim")
-    if t.data_ptr() % 16 or t.stride(0) % 8 or t.stride(1) % 8:
+    if vec16 and (t.data_ptr() % 16 or t.stride(0) % 8 or t.stride(1) % 8):
         raise ValueError(f"{name} rows must be 16-byte aligned (pointer and strides)")
     return t.stride(0), t.stride(1)
 
@@ -109,12 +116,14 @@ def _pack_args(spec, Q, K, V, Positions, CosCache, SinCache, SlotMapping, KeyCac
     if T < 0:
         raise ValueError(f"num_tokens must be >= 0, got {num_tokens}")
     D, QH, KH, bs = spec.head_dim, spec.num_q_heads, spec.num_kv_heads, spec.block_size
+    # head dims off the 16-dim grid (flash layout only) are read and written element by element
+    vec16 = D % 16 == 0
     a = _lib.RopeCacheArgs()
-    a.stride_q_token, a.stride_q_head = _rows("Q", Q, T, QH, D, spec.dtype)
-    a.stride_k_token, a.stride_k_head = _rows("K", K, T, KH, D, spec.dtype)
-    a.stride_v_token, a.stride_v_head = _rows("V", V, T, KH, D, spec.dtype)
-    a.stride_qo_token, a.stride_qo_head = _rows("Q_out", Q_out, T, QH, D, spec.dtype)
-    a.stride_ko_token, a.stride_ko_head = _rows("K_out", K_out, T, KH, D, spec.dtype)
+    a.stride_q_token, a.stride_q_head = _rows("Q", Q, T, QH, D, spec.dtype, vec16)
+    a.stride_k_token, a.stride_k_head = _rows("K", K, T, KH, D, spec.dtype, vec16)
+    a.stride_v_token, a.stride_v_head = _rows("V", V, T, KH, D, spec.dtype, vec16)
+    a.stride_qo_token, a.stride_qo_head = _rows("Q_out", Q_out, T, QH, D, spec.dtype, vec16)
+    a.stride_ko_token, a.stride_ko_head = _rows("K_out", K_out, T, KH, D, spec.dtype, vec16)
     pos_dt = _POS_DTYPES[spec.pos_dtype]
     _index("Positions", Positions, T, pos_dt)
     _index("SlotMapping", SlotMapping, T, pos_dt)
@@ -126,7 +135,7 @@ def _pack_args(spec, Q, K, V, Positions, CosCache, SinCache, SlotMapping, KeyCac
             raise ValueError(f"{name} must be [max_pos, {cols}] (reuse_freqs_front_part={spec.reuse}), got {shape}")
         if t.dtype != spec.dtype:
             raise ValueError(f"{name} must be {spec.dtype} (the element dtype), got {t.dtype}")
-        if t.stride(1) != 1 or t.data_ptr() % 16 or t.stride(0) % 8:
+        if t.stride(1) != 1 or (vec16 and (t.data_ptr() % 16 or t.stride(0) % 8)):
             raise ValueError(f"{name} rows must be contiguous and 16-byte aligned")
     if CosCache.shape[0] != SinCache.shape[0]:
         raise ValueError("CosCache and SinCache must have the same number of positions")
@@ -206,7 +215,7 @@ def _pack_args(spec, Q, K, V, Positions, CosCache, SinCache, SlotMapping, KeyCac
     esize = 2 if fmt == _lib.PA_FP8_CACHE_ELEM else 1
     used = 3 if spec.flash_layout else 2  # block, (token,) head strides
     for name, c in (("KeyCache", KeyCache), ("ValueCache", ValueCache)):
-        if c.data_ptr() % (8 * esize) or any(st % 8 for st in c.stride()[:used]):
+        if vec16 and (c.data_ptr() % (8 * esize) or any(st % 8 for st in c.stride()[:used])):
             raise ValueError(f"{name} must be aligned to 8 elements (pointer and block / head strides)")
 
     a.query, a.key, a.value = Q.data_ptr(), K.data_ptr(), V.data_ptr()
@@ -249,10 +258,19 @@ def build_fused_rope_cache_module(
         raise NotImplementedError("Partial rotation not yet supported")
     if dtype_str not in _ELEM:
         raise ValueError(f"dtype_str must be 'bf16' or 'f16', got {dtype_str!r}")
+    # the reference's vector-width rule (:79-96): one wave of 64 lanes covers a head
+    # vector, ceil(head_dim / 64) elements per lane, in both halves
+    vec = max(1, (head_dim + 63) // 64)
+    if head_dim % vec != 0:
+        raise ValueError(f"head_dim must be a multiple of the vector width {vec}, got {head_dim}")
     if rotary_dim % 2 != 0:
         raise ValueError(f"rotary_dim must be even, got {rotary_dim}")
-    if head_dim % 16 != 0 or not 16 <= head_dim <= 1024:
-        raise ValueError(f"head_dim must be a multiple of 16 in [16, 1024] (16-byte rotation halves), got {head_dim}")
+    if (head_dim // 2) % vec != 0:
+        raise ValueError(f"head_dim / 2 must be a multiple of the vector width {vec}, got {head_dim // 2}")
+    if not flash_layout and head_dim % _X != 0:
+        raise ValueError(f"head_dim must be a multiple of the x-pack factor {_X} without the flash layout, got {head_dim}")
+    if not 2 <= head_dim <= 1024:
+        raise ValueError(f"head_dim must be in [2, 1024], got {head_dim}")
     if pos_dtype not in _POS_DTYPES:
         raise ValueError(f"pos_dtype must be 'i32' or 'i64', got {pos_dtype!r}")
     if num_q_heads < 1 or num_kv_heads < 1 or block_size < 1:

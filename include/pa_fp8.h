@@ -410,6 +410,9 @@ enum pa_fp8_kv_layout {
  * (inner dim contiguous, 16-byte aligned rows); cos / sin [max_pos, cols]
  * with a free row stride; caches contiguous inside a (block, head) tile with
  * free block and head strides (and token stride for the flash layout).
+ * head_dim: a multiple of 16 in [16, 1024]; with PA_FP8_KV_FLASH also any even
+ * head_dim in [2, 1024], read and written element by element (2-byte aligned
+ * 16-bit tensors, any non-negative strides).
  * Per-token scales [nb, Hkv, bs, 1] f32: element blk*stride_ks_block +
  * h*stride_ks_head + slot % block_size.
  *

@@ -475,6 +475,61 @@ def test_prefill_runs_other_head_dims(D, QH, KH):
     run_case(80, D, QH, KH, layout="x5", fmt="fp8_token", bs=16, num_blocks=12, slots=_runs("aligned", 80, 16, 12, 0))
 
 
+# ---- head dims off the 16-dim grid (flash layout) ----------------------------------------------
+# The reference admits any head dim its vector-width rule passes in the flash layout
+# (kernels/fused_rope_cache_kernel.py:79-96): 72, 100, 200, 900, ... as well as the
+# multiples of 16.  These run the element-wise kernel; same bit-exact bar.
+
+NARROW_DIMS = [2, 8, 20, 40, 72, 100, 120, 200, 300, 900]
+
+
+@pytest.mark.parametrize("D", NARROW_DIMS)
+@pytest.mark.parametrize("fmt", ["elem", "fp8_tensor", "fp8_token"])
+def test_flash_head_dims_off_the_16_grid(D, fmt):
+    run_case(37, D, 6, 2, fmt=fmt, negative_slots=True)
+
+
+@pytest.mark.parametrize("D", [20, 72, 200])
+def test_flash_off_grid_f16_full_tables_i64(D):
+    run_case(25, D, 4, 2, elem="f16", reuse=False, pos_dtype="i64", fmt="fp8_token", bs=24,
+             slots=torch.randperm(8 * 24, generator=torch.Generator().manual_seed(D))[:25].int(), num_blocks=8)
+
+
+@pytest.mark.parametrize("D", [20, 40, 72])
+def test_flash_off_grid_strided_views(D):
+    # Q / K / V as views of one projection output: token strides of (QH + 2 KH) * D
+    # elements, not 16-byte multiples
+    run_case(19, D, 6, 2, fused_qkv=True, fmt="fp8_tensor")
+
+
+@pytest.mark.parametrize("D", [8, 72, 120])
+def test_flash_off_grid_decode_tolerances(D):
+    r = run_case(1, D, 8, 1)
+    _reference_tolerances(r, 1e-2)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_flash_off_grid_case(seed):
+    """Random flash-layout launches at head dims off the 16-dim grid, bit-exact against
+    the oracle: every element dtype and cache format, half / full tables, i32 / i64
+    indices, page sizes 1-1024, strided views and skipped slots."""
+    import random
+
+    rnd = random.Random(7100 + seed)
+    D = rnd.choice(NARROW_DIMS)
+    bs = rnd.choice([1, 2, 8, 16, 24, 64, 256, 1024])
+    KH = rnd.choice([1, 2, 4, 8])
+    QH = KH * rnd.choice([1, 2, 4, 8])
+    T = rnd.choice([1, 3, 16, 64, 200])
+    nb = max(4, (T + bs - 1) // bs + rnd.randint(0, 4))
+    g = torch.Generator().manual_seed(7100 + seed)
+    slots = torch.randperm(nb * bs, generator=g)[:T].to(torch.int32)
+    slots[torch.rand(T, generator=g) < 0.1] = -1
+    run_case(T, D, QH, KH, elem=rnd.choice(["bf16", "f16"]), fmt=rnd.choice(["elem", "fp8_tensor", "fp8_token"]),
+             reuse=rnd.random() < 0.5, pos_dtype=rnd.choice(["i32", "i64"]), bs=bs, num_blocks=nb, slots=slots,
+             fused_qkv=rnd.random() < 0.3, seed=7100 + seed)
+
+
 @pytest.mark.parametrize(
     "layout,bs,fmt,kind",
     [("flash", 24, "fp8_token", "random"), ("x4", 24, "elem", "random"), ("x5", 48, "fp8_tensor", "random"),

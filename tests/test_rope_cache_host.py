@@ -49,10 +49,49 @@ def test_build_time_checks_follow_the_reference():
     with pytest.raises(ValueError):
         frc.build_fused_rope_cache_module(dtype_str="f32")
     with pytest.raises(ValueError):
-        frc.build_fused_rope_cache_module(head_dim=72)
-    with pytest.raises(ValueError):
         frc.build_fused_rope_cache_module(pos_dtype="i16")
     assert callable(frc.build_fused_rope_cache_module(head_dim=64))
+
+
+# head dims the reference's vector-width rule admits (kernels/fused_rope_cache_kernel.py:79-96):
+# width w = ceil(D / 64); D and D / 2 multiples of w; D a multiple of 16 without the flash layout
+@pytest.mark.parametrize("D,flash,ok", [
+    (2, True, True), (8, True, True), (20, True, True), (62, True, True), (72, True, True),
+    (100, True, True), (200, True, True), (900, True, True), (1024, True, True), (1024, False, True),
+    (72, False, False),   # not a multiple of 16 without the flash layout
+    (66, True, False),    # w = 2, D / 2 = 33
+    (130, True, False),   # w = 3, 130 % 3
+    (160, True, False),   # w = 3, 160 % 3, although a multiple of 16
+    (1008, True, False),  # w = 16, D / 2 = 504
+    (63, True, False),    # rotary_dim odd
+    (1040, True, False),  # past 1024
+])
+def test_head_dim_rule(D, flash, ok):
+    if ok:
+        assert callable(frc.build_fused_rope_cache_module(head_dim=D, flash_layout=flash))
+    else:
+        with pytest.raises(ValueError):
+            frc.build_fused_rope_cache_module(head_dim=D, flash_layout=flash)
+
+
+def test_off_grid_head_dim_takes_element_alignment():
+    """Head dims off the 16-dim grid are read element by element: rows, tables and
+    caches need only element alignment (a 16-dim head keeps the 16-byte rule)."""
+    D, QH, KH, T = 20, 5, 2, 5
+    launch = frc.build_fused_rope_cache_module(head_dim=D, num_q_heads=QH, num_kv_heads=KH)
+    qkv = torch.zeros(T, (QH + 2 * KH) * D, dtype=torch.bfloat16)
+    q = qkv[:, : QH * D].view(T, QH, D)
+    k = qkv[:, QH * D: (QH + KH) * D].view(T, KH, D)
+    v = qkv[:, (QH + KH) * D:].view(T, KH, D)
+    t = dict(Q=q, K=k, V=v, Positions=torch.zeros(T, dtype=torch.int32),
+             CosCache=torch.zeros(16, D // 2, dtype=torch.bfloat16), SinCache=torch.zeros(16, D // 2, dtype=torch.bfloat16),
+             SlotMapping=torch.arange(T, dtype=torch.int32),
+             KeyCache=torch.zeros(4, 16, KH, D, dtype=torch.bfloat16), ValueCache=torch.zeros(4, 16, KH, D, dtype=torch.bfloat16),
+             Q_out=torch.zeros(T, QH, D, dtype=torch.bfloat16), K_out=torch.zeros(T, KH, D, dtype=torch.bfloat16),
+             num_tokens=T, KScale=None, VScale=None)
+    a = _pack(launch.spec, t)
+    assert (a.head_dim, a.stride_q_token, a.kv_layout) == (D, (QH + 2 * KH) * D, frc._lib.PA_FP8_KV_FLASH)
+    assert a.stride_q_token % 8 != 0 and a.stride_q_head % 8 != 0  # 180 and 20 elements
 
 
 @pytest.mark.parametrize(
