@@ -439,6 +439,14 @@ def _partitioned_plan(
                                       value_cache.dim() != 5,
                                       _max_slot_tokens(max_tokens, max_parts, sliding_window, query_length))
     given_es, given_ml, given_to = exp_sums is not None, max_logits is not None, temporary_output is not None
+    if merged and not (given_es or given_ml or given_to):
+        # Workgroups would hold every slot of their (sequence, kv head) and merge
+        # partials nobody reads: one slot per sequence on the same workgroups gives the
+        # output (to rounding: no bf16 slot rows in between) without the slot
+        # boundaries and the merge.  c2 at the harness's 8 slots: 84 us against 92.
+        max_parts = 1
+        waves, spw, merged = _slot_layout(dev, batch_size, num_kv_heads, 1, head_size, eqgs, value_cache.dim() != 5)
+        shape = (batch_size, num_kv_heads, 1, eqgs)
     # One slot per sequence: the kernel writes the output itself.  On the small-block
     # path the reference fills caller-passed partials even at one slot (its reduce
     # then reads them), so those calls keep the partials; its fused sliding-window
@@ -801,18 +809,26 @@ def _build_plan_checked(
     # partials, and the batch is ragged or the caller asks for several slots: the
     # schedule balances ragged batches across CUs, which fixed partition slots
     # cannot, and on an equal-length batch it holds whole sequences, as one slot
-    # does (c2 at the harness's 8 slots: 87.6-88.3 us on the worklist against 93.9 us
-    # on the chained slots).  Equal-length batches at one slot or the automatic
-    # count keep the partition kernel, which skips the worklist reads.  The tag stays
-    # "ps_small_block".  A caller that passes
+    # does.  Equal-length batches keep the partition kernel at one slot or the
+    # automatic count, and at a larger count when workgroups of one (sequence, kv
+    # head) each fill the GPU (the partition route then runs one slot per sequence,
+    # see _partitioned_plan): it skips the worklist reads (c2 at the harness's 8
+    # slots: 84.0 us against 85.7 on the worklist).  The tag stays "ps_small_block".
+    # A caller that passes
     # exp_sums / max_logits / temporary_output gets them filled in the reference's
     # partition-slot format, as the reference's small-block route (which ignores
     # metadata) fills them: that call runs the partition kernel at the caller's
     # partition count (kernels/pa_decode_fp8.py:3010-3121).
     caller_partials = exp_sums is not None or max_logits is not None or temporary_output is not None
+    uniform = metadata is not None and bool(metadata.get("uniform_context", False))
+    one_slot = max_context_partition_num <= 1
+    if uniform and not one_slot and not caller_partials and block_tables is not None and block_tables.dim() == 2:
+        one_slot = _slot_layout(dev, batch_size, num_kv_heads, max_context_partition_num, head_size,
+                                query_length * query_group_size, not trans_v,
+                                _max_slot_tokens(block_tables.shape[1] * block_size, max_context_partition_num,
+                                                 sliding_window, query_length))[2]
     balanced_worklist = (metadata is not None and kv_page_indices is not None and kv_indptr is not None
-                         and not caller_partials
-                         and (not metadata.get("uniform_context", False) or max_context_partition_num > 1))
+                         and not caller_partials and not (uniform and one_slot))
     if small and sliding_window <= 0 and not trans_v:
         # the reference's small-block kernel reads trans_v only (kernels/pa_decode_fp8.py:2082-2083)
         raise NotImplementedError("compile_pa_decode_ps: trans_v=False not yet supported.")

@@ -342,6 +342,26 @@ def test_small_block_with_metadata_runs_the_worklist(bs):
         plan(t, capturing=True, metadata=None)
 
 
+def test_uniform_batch_at_several_slots_runs_one_slot_when_workgroups_fill_the_gpu():
+    """c2's shape at the harness's 8 slots, no caller partials: workgroups of one
+    (sequence, kv head) fill 256 CUs, so the partition route runs one slot per sequence
+    (four waves, the output written directly), with or without a uniform batch's
+    metadata; with caller partials it keeps the caller's 8 slots on the chained layout."""
+    t = make(batch=64, hq=32, hkv=8, bs=16, nb=20, max_blocks=256)
+    t["kv_indptr"] = torch.arange(65, dtype=torch.int32) * 256
+    t["kv_page_indices"] = torch.zeros(64 * 256, dtype=torch.int32)
+    for md in (None, {"uniform_context": True}):
+        p = plan(t, max_parts=8, metadata=md)
+        a = p.dargs
+        assert p.tag == "ps_small_block" and p.wargs is None and p.rargs is None
+        assert (p.max_parts, a.max_context_partition_num, a.waves_per_slot, a.slots_per_wave, a.direct_output) == (
+            1, 1, 4, 0, 1)
+    shape = (64, 8, 8, 4)
+    p = plan(t, max_parts=8, metadata={"uniform_context": True}, exp_sums=torch.empty(shape),
+             max_logits=torch.empty(shape), temporary_output=torch.empty(shape + (128,), dtype=torch.bfloat16))
+    assert (p.max_parts, p.dargs.waves_per_slot, p.dargs.slots_per_wave, p.dargs.direct_output) == (8, 4, 2, 1)
+
+
 @pytest.mark.parametrize("bs", [16, 64])
 @pytest.mark.parametrize("parts", [1, 3, 8])
 def test_caller_partials_get_the_partition_slot_format(bs, parts):
@@ -539,6 +559,10 @@ def test_merged_layout_plan_writes_partials_and_output():
     assert (a.waves_per_slot, a.slots_per_wave, a.direct_output) == (4, 2, 1)
     assert p.rargs is None and [fn.__name__ for fn, _ in p.launches] == ["decode_partitions"]
     assert a.exp_sums == es.data_ptr() and a.tmp_out == to.data_ptr() and a.output == t["output"].data_ptr()
-    # without caller partials the launcher allocates them (the workgroups merge from them)
+    # without caller partials nobody reads them: one slot per sequence on the same
+    # four-wave workgroups, the output written directly
     p = plan(t, max_parts=8)
-    assert p.dargs.direct_output == 1 and p.rargs is None and len(p.keepalive) == 3
+    a = p.dargs
+    assert (p.max_parts, a.max_context_partition_num, a.waves_per_slot, a.slots_per_wave, a.direct_output) == (
+        1, 1, 4, 0, 1)
+    assert p.rargs is None and len(p.keepalive) == 0
