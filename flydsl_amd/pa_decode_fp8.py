@@ -882,28 +882,56 @@ def _schedule_layout(batch_size: int, num_kv_heads: int, num_sm: int) -> list:
     return [int(torch.Size(shape).numel()) for shape, _ in infos[1:]]
 
 
-def _schedule_args(a, bufs, ctx, batch_size, gqa, num_kv_heads, num_sm, partition_size,
-                   query_length, bin_groups, partial_count):
-    work_indptr, work_info, reduce_indptr, reduce_final_map, reduce_partial_map = bufs
-    a.seqlens_qo_indptr = None  # the scheduler's b * query_length: no offsets tensor to build
-    a.context_lens = ctx.data_ptr()
-    a.work_indptr = work_indptr.data_ptr()
-    a.work_info = work_info.data_ptr()
-    a.reduce_indptr = reduce_indptr.data_ptr()
-    a.reduce_final_map = reduce_final_map.data_ptr()
-    a.reduce_partial_map = reduce_partial_map.data_ptr()
-    a.partial_count = partial_count.data_ptr()
-    a.num_batches = batch_size
-    a.gqa = gqa
-    a.num_heads_k = num_kv_heads
-    a.num_cu = num_sm
-    a.kv_granularity = partition_size
-    a.query_length = query_length
-    a.max_work = work_info.numel() // 8
-    a.max_split_tiles = reduce_partial_map.numel()
-    a.bin_groups = bin_groups
-    for g, wgt in enumerate(_BIN_WEIGHTS.get(bin_groups, ())):
-        a.bin_weight[g] = wgt
+@functools.lru_cache(maxsize=64)
+def _metadata_layout(batch_size, num_kv_heads, gqa, query_length, head_size, cus, partition_size, tuned):
+    """What get_pa_metadata's launches share for one shape: the schedules (num_sm,
+    bin groups), the int32 element counts and 16-byte aligned offsets of the pieces
+    of its one allocation, and the scheduler argument blocks with every field but the
+    pointers filled (as bytes, copied per call)."""
+    num_sm = (cus * _REFERENCE_BINS_PER_CU // num_kv_heads) * num_kv_heads  # kernels/pa_decode_fp8.py:1769-1771
+    if num_sm <= 0 or partition_size <= 0 or partition_size & (partition_size - 1):
+        raise ValueError(
+            f"get_pa_metadata needs num_kv_heads <= {_REFERENCE_BINS_PER_CU} * CUs and a power-of-two partition_size"
+        )
+    schedules = [(num_sm, 0)]
+    if tuned:
+        bins_per_cu = _metadata_bins_per_cu(query_length, gqa, head_size)
+        t_sm = (cus * bins_per_cu // num_kv_heads) * num_kv_heads
+        # quotas weighted by dispatch round, when every round holds whole groups of bins
+        # and the parallel scheduler runs (the serial one, past 4096 batches, splits evenly)
+        t_groups = bins_per_cu if (t_sm == cus * bins_per_cu and t_sm % (bins_per_cu * num_kv_heads) == 0
+                                   and batch_size <= 4096 and bins_per_cu in _BIN_WEIGHTS) else 0
+        if t_sm > 0:
+            schedules.append((t_sm, t_groups))
+    # Every int32 output in one allocation: four counters first (the reference
+    # schedule's split partials, uniform_context, the tuned schedule's split
+    # partials), so one three-int read returns what the host needs; then each
+    # schedule's buffers and partition_indptr, in 16-byte aligned pieces.
+    sizes = [4]
+    for s_sm, _ in schedules:
+        sizes += _schedule_layout(batch_size, num_kv_heads, s_sm)
+    sizes.append(batch_size + 1)  # partition_indptr
+    offs = [0]
+    for n in sizes:
+        offs.append(offs[-1] + (n + 3) // 4 * 4)
+    args = (_lib.MetadataArgs * len(schedules))()
+    for k, (s_sm, s_groups) in enumerate(schedules):
+        a = args[k]
+        a.seqlens_qo_indptr = None  # the scheduler's b * query_length: no offsets tensor to build
+        a.num_batches = batch_size
+        a.gqa = gqa
+        a.num_heads_k = num_kv_heads
+        a.num_cu = s_sm
+        a.kv_granularity = partition_size
+        a.query_length = query_length
+        a.max_work = sizes[2 + 5 * k] // 8
+        a.max_split_tiles = sizes[5 + 5 * k]
+        a.bin_groups = s_groups
+        for g, wgt in enumerate(_BIN_WEIGHTS.get(s_groups, ())):
+            a.bin_weight[g] = wgt
+    if len(schedules) > 1:
+        args[1].pack = 1  # this build's packing schedule where it applies (the reference's stays sequential)
+    return tuple(schedules), tuple(sizes), tuple(offs), bytes(args)
 
 
 def get_pa_metadata(
@@ -950,53 +978,33 @@ def get_pa_metadata(
     query_length = query.shape[0] // batch_size
     head_size = query.shape[-1]
     gqa = num_query_heads // num_kv_heads
-    cus = _device_cu_count(dev)
-    num_sm = (cus * _REFERENCE_BINS_PER_CU // num_kv_heads) * num_kv_heads  # kernels/pa_decode_fp8.py:1769-1771
-    if num_sm <= 0 or partition_size <= 0 or partition_size & (partition_size - 1):
-        raise ValueError(
-            f"get_pa_metadata needs num_kv_heads <= {_REFERENCE_BINS_PER_CU} * CUs and a power-of-two partition_size"
-        )
-    schedules = [(num_sm, 0)]
-    if tuned:
-        bins_per_cu = _metadata_bins_per_cu(query_length, gqa, head_size)
-        t_sm = (cus * bins_per_cu // num_kv_heads) * num_kv_heads
-        # quotas weighted by dispatch round, when every round holds whole groups of bins
-        # and the parallel scheduler runs (the serial one, past 4096 batches, splits evenly)
-        t_groups = bins_per_cu if (t_sm == cus * bins_per_cu and t_sm % (bins_per_cu * num_kv_heads) == 0
-                                   and batch_size <= 4096 and bins_per_cu in _BIN_WEIGHTS) else 0
-        if t_sm <= 0:
-            tuned = False
-        else:
-            schedules.append((t_sm, t_groups))
+    schedules, sizes, offs, template = _metadata_layout(
+        batch_size, num_kv_heads, gqa, query_length, head_size, _device_cu_count(dev), partition_size, bool(tuned))
+    tuned = len(schedules) > 1
     ctx = context_lengths if context_lengths.dtype == torch.int32 else context_lengths.to(torch.int32)
     ctx = ctx.contiguous()
-    # Every int32 output in one allocation: four counters first (the reference
-    # schedule's split partials, uniform_context, the tuned schedule's split
-    # partials), so one three-int read returns what the host needs; then each
-    # schedule's buffers and partition_indptr, in 16-byte aligned pieces.
-    sizes = [4]
-    for s_sm, _ in schedules:
-        sizes += _schedule_layout(batch_size, num_kv_heads, s_sm)
-    sizes.append(batch_size + 1)  # partition_indptr
-    offs = [0]
-    for n in sizes:
-        offs.append(offs[-1] + (n + 3) // 4 * 4)
     buf = torch.empty(offs[-1], dtype=torch.int32, device=dev)
+    # The launch goes out first: its pointers are the pieces' offsets into the one
+    # allocation, and the pieces' tensors are made while the scheduler runs.
+    base = buf.data_ptr()
+    args = (_lib.MetadataArgs * len(schedules)).from_buffer_copy(template)
+    ctx_ptr = ctx.data_ptr()
+    for k in range(len(schedules)):
+        a, o = args[k], offs[1 + 5 * k: 6 + 5 * k]
+        a.context_lens = ctx_ptr
+        a.work_indptr = base + 4 * o[0]
+        a.work_info = base + 4 * o[1]
+        a.reduce_indptr = base + 4 * o[2]
+        a.reduce_final_map = base + 4 * o[3]
+        a.reduce_partial_map = base + 4 * o[4]
+        a.partial_count = base + 4 * (2 * k)  # counts[2k]
+    # the first schedule also writes the derived per-batch values
+    args[0].partition_indptr = base + 4 * offs[-2]
+    args[0].uniform_context = base + 4  # counts[1]
+    _lib.metadata_multi(args, torch.cuda.current_stream(dev).cuda_stream)
     piece = [buf[offs[k]: offs[k] + sizes[k]] for k in range(len(sizes))]
     counts, partition_indptr = piece[0], piece[-1]
-    args = (_lib.MetadataArgs * len(schedules))()
-    sched_bufs = []
-    for k, (s_sm, s_groups) in enumerate(schedules):
-        bufs = piece[1 + 5 * k: 6 + 5 * k]
-        _schedule_args(args[k], bufs, ctx, batch_size, gqa, num_kv_heads, s_sm, partition_size,
-                       query_length, s_groups, counts[2 * k: 2 * k + 1])
-        sched_bufs.append(bufs)
-    if tuned:
-        args[1].pack = 1  # this build's packing schedule where it applies (the reference's stays sequential)
-    # the first schedule also writes the derived per-batch values
-    args[0].partition_indptr = partition_indptr.data_ptr()
-    args[0].uniform_context = counts[1:2].data_ptr()
-    _lib.metadata_multi(args, torch.cuda.current_stream(dev).cuda_stream)
+    sched_bufs = [piece[1 + 5 * k: 6 + 5 * k] for k in range(len(schedules))]
 
     # the dicts are built while the scheduler runs; only the partial buffers wait for
     # the host read below
