@@ -614,7 +614,10 @@ __device__ __forceinline__ void attend_range(const DecodeParams &p, const int b,
         sofs = (int64_t)phys * p.s_ks_block + (int64_t)h * p.s_ks_head + sub * 16;
     };
 
-    uint4 kr[4][kKChunks<D>];  // K of the step: [tile][chunk], 16 fp8 each (the bf16 products skip the padding)
+    // K of the step: [tile][chunk], 16 fp8 each, tile jt the step's group jt (the
+    // page-per-tile layout of step_qk_softmax<..., KT = true>; the bf16 products skip
+    // the padding chunk)
+    uint4 kr[4][kKChunks<D>];
     uint4 vr[D / 16];  // V of the step: [dim tile], 16 tokens of one head dim
     // Per-token scales: a lane needs the 16 K and 16 V scales of its group kg, and
     // loads a quarter of each (tokens 4 (l16 & 3) .. +3, 16 bytes); the quad of
