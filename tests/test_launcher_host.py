@@ -566,3 +566,57 @@ def test_merged_layout_plan_writes_partials_and_output():
     assert (p.max_parts, a.max_context_partition_num, a.waves_per_slot, a.slots_per_wave, a.direct_output) == (
         1, 1, 4, 0, 1)
     assert p.rargs is None and len(p.keepalive) == 0
+
+
+def test_get_pa_metadata_argument_blocks(monkeypatch):
+    """get_pa_metadata's scheduler argument blocks (shape fields from a per-shape template,
+    pointers as offsets into its one allocation) point at the tensors of the returned dict,
+    on CPU tensors with the scheduler launch replaced by a recorder."""
+    import ctypes
+
+    calls = []
+
+    def record(args, stream):
+        calls.append([{f: getattr(a, f) for f, _ in _lib.MetadataArgs._fields_ if f != "bin_weight"}
+                      | {"bin_weight": list(a.bin_weight)} for a in args])
+        for a in args:  # the counters the host reads: no split partials, not uniform
+            ctypes.memset(a.partial_count, 0, 4)
+        ctypes.memset(args[0].uniform_context, 0, 4)
+
+    class _Stream:
+        cuda_stream = 0
+
+    monkeypatch.setattr(_lib, "metadata_multi", record)
+    monkeypatch.setattr(pdf, "_device_cu_count", lambda dev: 256)
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda *a, **k: _Stream())
+    pdf._metadata_layout.cache_clear()
+    B, hq, hkv = 64, 32, 8
+    q = torch.zeros(B, hq, 128, dtype=torch.bfloat16)
+    kc = torch.zeros(4, hkv, 8, 16, 16, dtype=torch.uint8)
+    kv = torch.zeros(B + 1, dtype=torch.int32)
+    for call in range(2):  # the second call reuses the cached layout with new pointers
+        ctx = torch.full((B,), 4096 + call, dtype=torch.int32)
+        md = pdf.get_pa_metadata(q, kc, ctx, kv, hq, hkv, graph_safe=False)
+        blocks = calls[-1]
+        assert len(blocks) == 2
+        for k, sched in enumerate((md, md["tuned"])):
+            a = blocks[k]
+            assert a["context_lens"] == ctx.data_ptr() and a["seqlens_qo_indptr"] is None
+            for field, key in (("work_indptr", "work_indptr"), ("work_info", "work_info_flat"),
+                               ("reduce_indptr", "reduce_indptr"), ("reduce_final_map", "reduce_final_map"),
+                               ("reduce_partial_map", "reduce_partial_map")):
+                assert a[field] == sched[key].data_ptr(), field
+            assert (a["num_batches"], a["gqa"], a["num_heads_k"], a["num_cu"], a["query_length"]) == (
+                B, hq // hkv, hkv, sched["num_sm"], 1)
+            assert a["max_work"] == sched["work_info_flat"].numel() // 8
+            assert a["max_split_tiles"] == sched["reduce_partial_map"].numel()
+            assert a["kv_granularity"] == 256
+        assert blocks[0]["pack"] == 0 and blocks[1]["pack"] == 1
+        assert blocks[0]["bin_groups"] == 0 and blocks[1]["bin_groups"] == md["tuned"]["bin_groups"] == 2
+        assert blocks[1]["bin_weight"][:2] == list(md["tuned"]["bin_weight"])
+        assert blocks[0]["partition_indptr"] == md["partition_indptr"].data_ptr()
+        assert blocks[1]["partition_indptr"] is None and blocks[1]["uniform_context"] is None
+        assert md["uniform_context"] is False and md["partial_output"].shape == (1, 1, hq, 128)
+    assert pdf._metadata_layout.cache_info().hits >= 1
+    with pytest.raises(ValueError, match="power-of-two partition_size"):
+        pdf.get_pa_metadata(q, kc, ctx, kv, hq, hkv, partition_size=96)
