@@ -483,11 +483,13 @@ def _reference_parts(cfg):
     return get_recommended_splits(cfg.batch, cfg.num_kv_heads, split_kv_blocks=max(1, 256 // cfg.block_size))
 
 
-def measure_decode(torch, cfg, dev, steps, warmup, copies=3, max_parts=0, use_metadata=True, extras=True):
+def measure_decode(torch, cfg, dev, steps, warmup, copies=3, max_parts=0, use_metadata=True, extras=True,
+                   graph=False):
     """One configuration through ``pa_decode_ps_launch``: the step time (events around
     ``steps`` steps, ``copies`` KV caches rotated), the dominant kernel's time alone,
     its algorithmic bytes and the reference harness's partition count.  Returns a
-    dict; ``extras`` adds the partition-kernel and graph-captured variants."""
+    dict; ``extras`` adds the partition-kernel and graph-captured variants, ``graph``
+    the graph-captured one alone."""
     from flydsl_amd import get_pa_metadata, pa_decode_ps_launch
     from flydsl_amd.pa_decode_fp8 import _PLAN_CACHE
     from flydsl_amd.workloads import build_workload_copies, kv_bytes
@@ -587,9 +589,9 @@ def measure_decode(torch, cfg, dev, steps, warmup, copies=3, max_parts=0, use_me
     del ref_partials
 
     others = {}
-    if extras:
-        if metadata is not None and cfg.block_size in (16, 64):
-            others["partition_kernel_auto_partitions"] = _timed(torch, lambda i: step(i, md=None), steps, warmup)[0] * 1e3
+    if extras and metadata is not None and cfg.block_size in (16, 64):
+        others["partition_kernel_auto_partitions"] = _timed(torch, lambda i: step(i, md=None), steps, warmup)[0] * 1e3
+    if extras or graph:
         # the schedule rebuilt every step together with the decode, both captured in one
         # HIP graph per KV copy (get_pa_metadata(graph_safe=True) reads nothing back to
         # the host), replayed in rotation
@@ -705,7 +707,7 @@ def main():
         c = CONFIGS[name]
         try:
             o = measure_decode(torch, c, dev, config_steps, config_warmup, copies=args.copies,
-                               use_metadata=not args.no_metadata, extras=False)
+                               use_metadata=not args.no_metadata, extras=False, graph=True)
         except ValueError as e:  # a configuration the launcher refuses leaves the headline line intact
             print(f"[bench] {name} refused: {e}", file=sys.stderr, flush=True)
             configs[name] = {"workload": c.description, "error": str(e)}
@@ -732,6 +734,8 @@ def main():
                 "traffic": o["traffic"],
             },
             "reference_default_partitions": _reference_entry(o),
+            "graph_schedule_plus_decode_us": (round(o["others"]["graph_schedule_plus_decode"], 2)
+                                              if "graph_schedule_plus_decode" in o["others"] else None),
             "steps": config_steps,
             "warmup": config_warmup,
         }
